@@ -1,0 +1,492 @@
+// C ABI of the decode path (see include/qwen3vl_decode.h): argument checks,
+// dtype dispatch, and the full batch-1 decode step.
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+#include <vector>
+
+#include "qd_common.h"
+#include "qd_kernels.h"
+
+// ---------------------------------------------------------------- host helpers
+
+namespace qd_host {
+
+static thread_local char g_err[512] = "";
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+int launch_status(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("%s launch failed: %s", what, hipGetErrorString(e));
+    return (int)e;
+  }
+  return QD_OK;
+}
+
+int cu_count() {
+  static std::mutex mu;
+  static std::vector<int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  std::lock_guard<std::mutex> lk(mu);
+  if ((int)cache.size() <= dev) cache.resize(dev + 1, 0);
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
+}  // namespace qd_host
+
+namespace {
+
+using qd::GemvArgs;
+using u16 = uint16_t;
+
+inline hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
+inline bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Workspace layout of the lm_head argmax: [counter (256 B)] [vals] [idx].
+constexpr size_t kArgmaxHeader = 256;
+size_t argmax_ws_bytes() {
+  return kArgmaxHeader + (size_t)qd::kMaxArgmaxBlocks * (sizeof(float) + sizeof(long));
+}
+void argmax_ws(void* ws, GemvArgs& a) {
+  char* b = reinterpret_cast<char*>(ws);
+  a.counter = reinterpret_cast<unsigned*>(b);
+  a.part_idx = reinterpret_cast<long*>(b + kArgmaxHeader);
+  a.part_val = reinterpret_cast<float*>(b + kArgmaxHeader + (size_t)qd::kMaxArgmaxBlocks * sizeof(long));
+}
+
+// Attention workspace: [counters (256 B)] [o_part Hq*S*128 f32] [lse Hq*S f32].
+size_t attn_ws_bytes(int Hq, int Hkv, int S_) {
+  (void)Hkv;
+  return 256 + (size_t)Hq * S_ * 128 * 4 + (size_t)Hq * S_ * 4;
+}
+void attn_ws(void* ws, qd::AttnArgs& a) {
+  char* b = reinterpret_cast<char*>(ws);
+  a.counters = reinterpret_cast<unsigned*>(b);
+  a.o_part = reinterpret_cast<float*>(b + 256);
+  a.lse = reinterpret_cast<float*>(b + 256 + (size_t)a.Hq * a.n_split * 128 * 4);
+}
+
+int check_gemv_ptrs(const void* x, const void* W, const void* y, int N, int K) {
+  QD_REQUIRE(x && W && y, QD_ERR_ARG, "null pointer");
+  QD_REQUIRE(N > 0 && K > 0 && (K % 8) == 0, QD_ERR_SHAPE, "need N > 0 and K %% 8 == 0 (N=%d K=%d)", N, K);
+  QD_REQUIRE(a16(x) && a16(W), QD_ERR_ARG, "x and W must be 16-byte aligned");
+  return QD_OK;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- C ABI
+
+extern "C" {
+
+int qd_version(void) { return 1; }
+const char* qd_last_error(void) { return qd_host::g_err; }
+int qd_device_cu_count(void) { return qd_host::cu_count(); }
+
+int qd_matvec_f16(const void* x, const void* W, const void* bias, void* y, int N, int K, void* stream) {
+  int st = check_gemv_ptrs(x, W, y, N, K);
+  if (st) return st;
+  GemvArgs a;
+  a.x = x; a.W = (const u16*)W; a.bias = bias; a.y = y; a.N = N; a.K = K; a.ldw = K;
+  return qd::gemv_store<qd::PRO_PLAIN, u16, u16>(a, S(stream));
+}
+
+int qd_splitk_matvec_f16(const void* x, const void* W, const void* bias, float* scratch, void* y, int N, int K,
+                         int split_k, void* stream) {
+  int st = check_gemv_ptrs(x, W, y, N, K);
+  if (st) return st;
+  QD_REQUIRE(scratch, QD_ERR_ARG, "null scratch");
+  QD_REQUIRE(split_k >= 1 && K % split_k == 0, QD_ERR_SHAPE, "split_k %d must divide K %d", split_k, K);
+  GemvArgs a;
+  a.x = x; a.W = (const u16*)W; a.bias = bias; a.y = y; a.N = N; a.K = K; a.ldw = K; a.part_val = scratch;
+  st = qd::gemv_splitk<u16, u16>(a, split_k, S(stream));
+  QD_REQUIRE(st != QD_ERR_SHAPE && st != 1, QD_ERR_SHAPE,
+             "split-K slice K/split_k=%d unsupported (need 512/1024/2048/3072/4096/6144)", K / split_k);
+  return st;
+}
+
+int qd_rmsnorm_matvec_f16(const void* x, const void* gamma, const void* W, const void* bias, void* y, int N, int K,
+                          float eps, void* stream) {
+  int st = check_gemv_ptrs(x, W, y, N, K);
+  if (st) return st;
+  QD_REQUIRE(gamma && a16(gamma), QD_ERR_ARG, "gamma null or misaligned");
+  GemvArgs a;
+  a.x = x; a.gamma = (const u16*)gamma; a.W = (const u16*)W; a.bias = bias; a.y = y;
+  a.N = N; a.K = K; a.ldw = K; a.eps = eps;
+  return qd::gemv_store<qd::PRO_RMSNORM, u16, u16>(a, S(stream));
+}
+
+int qd_post_attn_mlp_f16(const void* residual, const void* attn, const void* gamma, const void* W_gu,
+                         const void* W_d, const void* bias, void* hidden_out, void* out, int H, int I, float eps,
+                         void* stream) {
+  QD_REQUIRE(residual && attn && gamma && W_gu && W_d && hidden_out && out, QD_ERR_ARG, "null pointer");
+  QD_REQUIRE(a16(residual) && a16(attn) && a16(gamma) && a16(W_gu) && a16(W_d) && a16(hidden_out) && a16(out),
+             QD_ERR_ARG, "pointers must be 16-byte aligned");
+  QD_REQUIRE(H > 0 && I > 0 && H % 512 == 0 && I % 512 == 0, QD_ERR_SHAPE, "H, I must be multiples of 512");
+  // r = residual + attn is written to `out` first, then used as the residual of down_proj
+  // and overwritten element-wise in place (each element read before it is written).
+  GemvArgs g;
+  g.x = residual; g.x2 = attn; g.gamma = (const u16*)gamma; g.W = (const u16*)W_gu; g.y = hidden_out;
+  g.r_out = out; g.N = I; g.K = H; g.ldw = H; g.up_offset = I; g.eps = eps;
+  int st = qd::gemv_silu<qd::PRO_ADD_RMSNORM, u16, u16>(g, S(stream));
+  QD_REQUIRE(st != QD_ERR_SHAPE && st != 1, QD_ERR_SHAPE, "unsupported H=%d", H);
+  if (st) return st;
+  GemvArgs d;
+  d.x = hidden_out; d.W = (const u16*)W_d; d.bias = bias; d.residual = out; d.y = out;
+  d.N = H; d.K = I; d.ldw = I;
+  st = qd::gemv_store<qd::PRO_PLAIN, u16, u16>(d, S(stream));
+  return st;
+}
+
+int qd_gateup_silu_down_f16(const void* x, const void* W_gu, const void* W_d, const void* bias, void* hidden_out,
+                            void* out, int H, int I, void* stream) {
+  QD_REQUIRE(x && W_gu && W_d && hidden_out && out, QD_ERR_ARG, "null pointer");
+  QD_REQUIRE(a16(x) && a16(W_gu) && a16(W_d) && a16(hidden_out), QD_ERR_ARG, "pointers must be 16-byte aligned");
+  QD_REQUIRE(H > 0 && I > 0 && H % 512 == 0 && I % 512 == 0, QD_ERR_SHAPE, "H, I must be multiples of 512");
+  GemvArgs g;
+  g.x = x; g.W = (const u16*)W_gu; g.y = hidden_out; g.N = I; g.K = H; g.ldw = H; g.up_offset = I;
+  int st = qd::gemv_silu<qd::PRO_PLAIN, u16, u16>(g, S(stream));
+  QD_REQUIRE(st != QD_ERR_SHAPE && st != 1, QD_ERR_SHAPE, "unsupported H=%d", H);
+  if (st) return st;
+  GemvArgs d;
+  d.x = hidden_out; d.W = (const u16*)W_d; d.bias = bias; d.y = out; d.N = H; d.K = I; d.ldw = I;
+  return qd::gemv_store<qd::PRO_PLAIN, u16, u16>(d, S(stream));
+}
+
+int qd_add_rmsnorm_matvec_f16(const void* residual, const void* x, const void* gamma, const void* W,
+                              const void* bias, void* residual_out, void* y, int N, int K, float eps, void* stream) {
+  int st = check_gemv_ptrs(x, W, y, N, K);
+  if (st) return st;
+  QD_REQUIRE(residual && gamma && a16(residual) && a16(gamma) && (!residual_out || a16(residual_out)), QD_ERR_ARG,
+             "residual/gamma null or misaligned");
+  QD_REQUIRE(K % 512 == 0, QD_ERR_SHAPE, "K must be a multiple of 512 (K=%d)", K);
+  GemvArgs a;
+  a.x = residual; a.x2 = x; a.gamma = (const u16*)gamma; a.W = (const u16*)W; a.bias = bias; a.y = y;
+  a.r_out = residual_out; a.N = N; a.K = K; a.ldw = K; a.eps = eps;
+  st = qd::gemv_store<qd::PRO_ADD_RMSNORM, u16, u16>(a, S(stream));
+  QD_REQUIRE(st != QD_ERR_SHAPE && st != 1, QD_ERR_SHAPE, "unsupported K=%d", K);
+  return st;
+}
+
+int qd_silu_matvec_f16(const void* gate_up, const void* W, const void* bias, void* y, int N, int K, void* stream) {
+  int st = check_gemv_ptrs(gate_up, W, y, N, K);
+  if (st) return st;
+  QD_REQUIRE(K % 512 == 0, QD_ERR_SHAPE, "K must be a multiple of 512 (K=%d)", K);
+  GemvArgs a;
+  a.x = gate_up; a.x2 = (const u16*)gate_up + K; a.W = (const u16*)W; a.bias = bias; a.y = y;
+  a.N = N; a.K = K; a.ldw = K;
+  st = qd::gemv_store<qd::PRO_SILU, u16, u16>(a, S(stream));
+  QD_REQUIRE(st != QD_ERR_SHAPE && st != 1, QD_ERR_SHAPE, "unsupported K=%d", K);
+  return st;
+}
+
+size_t qd_lm_head_workspace_bytes(int V) {
+  (void)V;
+  return argmax_ws_bytes();
+}
+
+int qd_lm_head_argmax(const void* h, int h_dtype, const void* gamma, float eps, const void* W, int V, int H,
+                      void* logits_out, int64_t* token_out, void* workspace, void* stream) {
+  QD_REQUIRE(h && W && token_out && workspace, QD_ERR_ARG, "null pointer");
+  QD_REQUIRE(a16(h) && a16(W) && (!gamma || a16(gamma)), QD_ERR_ARG, "pointers must be 16-byte aligned");
+  QD_REQUIRE(V > 0 && H > 0 && H % 512 == 0, QD_ERR_SHAPE, "H must be a multiple of 512 (H=%d)", H);
+  QD_REQUIRE(h_dtype == QD_F16 || h_dtype == QD_F32, QD_ERR_ARG, "bad h dtype");
+  GemvArgs a;
+  a.x = h; a.gamma = (const u16*)gamma; a.eps = eps; a.W = (const u16*)W; a.N = V; a.K = H; a.ldw = H;
+  a.y = logits_out; a.token = token_out;
+  argmax_ws(workspace, a);
+  int st;
+  if (h_dtype == QD_F32) {
+    QD_REQUIRE(gamma, QD_ERR_ARG, "fp32 hidden requires the final-norm gamma");
+    st = qd::gemv_argmax<qd::PRO_RMSNORM, float, u16>(a, S(stream));
+  } else if (gamma) {
+    st = qd::gemv_argmax<qd::PRO_RMSNORM, u16, u16>(a, S(stream));
+  } else {
+    st = qd::gemv_argmax<qd::PRO_PLAIN, u16, u16>(a, S(stream));
+  }
+  QD_REQUIRE(st != QD_ERR_SHAPE && st != 1, QD_ERR_SHAPE, "unsupported H=%d", H);
+  return st;
+}
+
+int qd_q_rope_kv_update(const void* q, const void* k, const void* v, int qkv_dtype, long q_stride, long k_stride,
+                        long v_stride, const void* q_weight, const void* k_weight, float eps, const void* cos,
+                        const void* sin, const int64_t* rope_pos, const float* inv_freq, int sec_t, int sec_h,
+                        int sec_w, void* q_out, int q_out_dtype, void* k_cache, void* v_cache, long cache_stride_h,
+                        long cache_stride_s, int T, const int64_t* cache_position, int Hq, int Hkv, void* stream) {
+  (void)sec_t;
+  QD_REQUIRE(q && k && v && q_weight && k_weight && q_out && k_cache && v_cache && cache_position, QD_ERR_ARG,
+             "null pointer");
+  QD_REQUIRE((cos && sin) || (rope_pos && inv_freq), QD_ERR_ARG, "need cos/sin or rope_pos + inv_freq");
+  QD_REQUIRE(Hkv > 0 && Hq > 0 && Hq % Hkv == 0 && Hq / Hkv <= 4, QD_ERR_SHAPE, "need Hq = G*Hkv with G <= 4");
+  QD_REQUIRE(T > 0, QD_ERR_SHAPE, "T must be positive");
+  QD_REQUIRE(qkv_dtype == q_out_dtype && (qkv_dtype == QD_F16 || qkv_dtype == QD_F32), QD_ERR_ARG,
+             "q/k/v and q_out dtype must match (f16 or f32)");
+  qd::RopeArgs a;
+  a.q = q; a.k = k; a.v = v; a.q_stride = q_stride; a.k_stride = k_stride; a.v_stride = v_stride;
+  a.q_weight = (const u16*)q_weight; a.k_weight = (const u16*)k_weight; a.eps = eps;
+  a.cos = (const u16*)cos; a.sin = (const u16*)sin; a.rope_pos = rope_pos; a.inv_freq = inv_freq;
+  a.sec_h = sec_h; a.sec_w = sec_w; a.q_out = q_out; a.k_cache = (u16*)k_cache; a.v_cache = (u16*)v_cache;
+  a.cache_stride_h = cache_stride_h; a.cache_stride_s = cache_stride_s; a.T = T; a.cache_position = cache_position;
+  a.Hq = Hq; a.Hkv = Hkv;
+  return qkv_dtype == QD_F16 ? qd::q_rope_kv_launch<u16, u16>(a, S(stream))
+                             : qd::q_rope_kv_launch<float, float>(a, S(stream));
+}
+
+int qd_qk_norm_rope_f16(const void* q, const void* k, const void* q_weight, const void* k_weight, const void* cos,
+                        const void* sin, void* q_out, void* k_out, int M, int Hq, int Hkv, float eps, void* stream) {
+  QD_REQUIRE(q && k && q_weight && k_weight && cos && sin && q_out && k_out, QD_ERR_ARG, "null pointer");
+  QD_REQUIRE(M > 0 && Hkv > 0 && Hq % Hkv == 0 && Hq / Hkv <= 4, QD_ERR_SHAPE, "bad head counts");
+  qd::RopeArgs a;
+  a.q = q; a.k = k; a.q_stride = 128; a.k_stride = 128; a.q_row = (long)Hq * 128; a.k_row = (long)Hkv * 128;
+  a.q_weight = (const u16*)q_weight; a.k_weight = (const u16*)k_weight; a.eps = eps;
+  a.cos = (const u16*)cos; a.sin = (const u16*)sin; a.cs_row = 128; a.q_out = q_out; a.k_out = k_out;
+  a.Hq = Hq; a.Hkv = Hkv; a.M = M;
+  return qd::qk_norm_rope_f16_launch(a, S(stream));
+}
+
+int qd_add_rmsnorm_f16(const void* residual, const void* x, const void* weight, void* out_sum, void* out_norm,
+                       int rows, int cols, float eps, void* stream) {
+  QD_REQUIRE(residual && x && weight && out_sum && out_norm, QD_ERR_ARG, "null pointer");
+  QD_REQUIRE(rows > 0 && cols > 0, QD_ERR_SHAPE, "empty input");
+  return qd::add_rmsnorm_f16_launch((const u16*)residual, (const u16*)x, (const u16*)weight, (u16*)out_sum,
+                                    (u16*)out_norm, rows, cols, eps, S(stream));
+}
+
+int qd_rmsnorm_f16(const void* x, const void* weight, void* out, int rows, int cols, float eps, void* stream) {
+  QD_REQUIRE(x && weight && out, QD_ERR_ARG, "null pointer");
+  QD_REQUIRE(rows > 0 && cols > 0, QD_ERR_SHAPE, "empty input");
+  return qd::add_rmsnorm_f16_launch(nullptr, (const u16*)x, (const u16*)weight, nullptr, (u16*)out, rows, cols, eps,
+                                    S(stream));
+}
+
+int qd_silu_mul_f16(const void* gate, const void* up, void* out, long n, void* stream) {
+  QD_REQUIRE(gate && up && out, QD_ERR_ARG, "null pointer");
+  if (n <= 0) return QD_OK;
+  return qd::silu_mul_f16_launch((const u16*)gate, (const u16*)up, (u16*)out, n, S(stream));
+}
+
+int qd_add_f16(const void* a, const void* b, void* out, long n, void* stream) {
+  QD_REQUIRE(a && b && out, QD_ERR_ARG, "null pointer");
+  if (n <= 0) return QD_OK;
+  return qd::add_f16_launch((const u16*)a, (const u16*)b, (u16*)out, n, S(stream));
+}
+
+size_t qd_attention_workspace_bytes(int Hq, int Hkv, int n_split) { return attn_ws_bytes(Hq, Hkv, n_split); }
+
+int qd_attention_default_splits(int T) {
+  int s = (T + 127) / 128;
+  if (s < 4) s = 4;
+  if (s > 32) s = 32;
+  return s;
+}
+
+static int attn_common(qd::AttnArgs& a, const void* q, int q_dtype, long q_stride, const void* k_cache,
+                       const void* v_cache, long cache_stride_h, long cache_stride_s, int T,
+                       const int64_t* cache_position, float scale, int Hq, int Hkv, int n_split) {
+  QD_REQUIRE(q && k_cache && v_cache && cache_position, QD_ERR_ARG, "null pointer");
+  QD_REQUIRE(q_dtype == QD_F16 || q_dtype == QD_F32, QD_ERR_ARG, "bad q dtype");
+  QD_REQUIRE(Hkv > 0 && Hq % Hkv == 0 && (Hq / Hkv == 1 || Hq / Hkv == 2 || Hq / Hkv == 4), QD_ERR_SHAPE,
+             "need Hq/Hkv in {1,2,4}");
+  QD_REQUIRE(T > 0 && n_split >= 1 && n_split <= 1024, QD_ERR_SHAPE, "bad T or n_split");
+  QD_REQUIRE(a16(q) && a16(k_cache) && a16(v_cache) && cache_stride_s % 8 == 0 && cache_stride_h % 8 == 0 &&
+                 q_stride % 8 == 0,
+             QD_ERR_ARG, "q/cache pointers and strides must be 16-byte aligned");
+  a.q = q; a.q_stride = q_stride; a.k = (const u16*)k_cache; a.v = (const u16*)v_cache;
+  a.stride_h = cache_stride_h; a.stride_s = cache_stride_s; a.T = T; a.cache_position = cache_position;
+  a.scale = scale; a.Hq = Hq; a.Hkv = Hkv; a.n_split = n_split;
+  return QD_OK;
+}
+
+int qd_attention_decode(const void* q, int q_dtype, long q_stride, const void* k_cache, const void* v_cache,
+                        long cache_stride_h, long cache_stride_s, int T, const int64_t* cache_position, float scale,
+                        void* out, int out_dtype, int Hq, int Hkv, int n_split, void* workspace, void* stream) {
+  qd::AttnArgs a;
+  int st = attn_common(a, q, q_dtype, q_stride, k_cache, v_cache, cache_stride_h, cache_stride_s, T, cache_position,
+                       scale, Hq, Hkv, n_split);
+  if (st) return st;
+  QD_REQUIRE(out && workspace, QD_ERR_ARG, "null out/workspace");
+  QD_REQUIRE(out_dtype == QD_F16 || out_dtype == QD_F32, QD_ERR_ARG, "bad out dtype");
+  a.out = out;
+  attn_ws(workspace, a);
+  if (q_dtype == QD_F16)
+    return out_dtype == QD_F16 ? qd::attention_launch<u16, u16>(a, true, S(stream))
+                               : qd::attention_launch<u16, float>(a, true, S(stream));
+  return out_dtype == QD_F16 ? qd::attention_launch<float, u16>(a, true, S(stream))
+                             : qd::attention_launch<float, float>(a, true, S(stream));
+}
+
+int qd_attention_partial(const void* q, int q_dtype, long q_stride, const void* k_cache, const void* v_cache,
+                         long cache_stride_h, long cache_stride_s, int T, const int64_t* cache_position, float scale,
+                         float* o_part, float* lse, int Hq, int Hkv, int n_split, void* stream) {
+  qd::AttnArgs a;
+  int st = attn_common(a, q, q_dtype, q_stride, k_cache, v_cache, cache_stride_h, cache_stride_s, T, cache_position,
+                       scale, Hq, Hkv, n_split);
+  if (st) return st;
+  QD_REQUIRE(o_part && lse, QD_ERR_ARG, "null partial buffers");
+  a.o_part = o_part; a.lse = lse;
+  return q_dtype == QD_F16 ? qd::attention_launch<u16, u16>(a, false, S(stream))
+                           : qd::attention_launch<float, float>(a, false, S(stream));
+}
+
+int qd_attention_merge(const float* o_part, const float* lse, void* out, int out_dtype, int Hq, int n_split,
+                       void* stream) {
+  QD_REQUIRE(o_part && lse && out, QD_ERR_ARG, "null pointer");
+  QD_REQUIRE(Hq > 0 && n_split >= 1, QD_ERR_SHAPE, "bad sizes");
+  qd::AttnArgs a;
+  a.o_part = const_cast<float*>(o_part); a.lse = const_cast<float*>(lse); a.out = out; a.Hq = Hq;
+  a.n_split = n_split;
+  return out_dtype == QD_F16 ? qd::attention_merge_launch<u16>(a, S(stream))
+                             : qd::attention_merge_launch<float>(a, S(stream));
+}
+
+// ---------------------------------------------------------------- decode step
+
+namespace {
+
+struct StepBuffers {
+  float* x;        // residual stream [H]
+  float* qkv;      // [Hq*D + 2*Hkv*D]
+  float* q_rot;    // [Hq*D]
+  float* attn;     // [Hq*D]
+  float* r;        // [H]
+  float* hidden;   // [I]
+  char* attn_ws;
+  char* argmax_ws;
+};
+
+size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+bool step_layout(const qd_model_desc* d, int splits, StepBuffers* b, size_t* total) {
+  const size_t qkv_rows = (size_t)d->num_heads * d->head_dim + 2 * (size_t)d->num_kv_heads * d->head_dim;
+  size_t off = 0;
+  size_t o_x = off; off += align256(4 * (size_t)d->hidden);
+  size_t o_qkv = off; off += align256(4 * qkv_rows);
+  size_t o_q = off; off += align256(4 * (size_t)d->num_heads * d->head_dim);
+  size_t o_a = off; off += align256(4 * (size_t)d->num_heads * d->head_dim);
+  size_t o_r = off; off += align256(4 * (size_t)d->hidden);
+  size_t o_h = off; off += align256(4 * (size_t)d->intermediate);
+  size_t o_aw = off; off += align256(attn_ws_bytes(d->num_heads, d->num_kv_heads, splits));
+  size_t o_gw = off; off += align256(argmax_ws_bytes());
+  *total = off;
+  if (b != nullptr) {
+    char* base = reinterpret_cast<char*>(d->workspace);
+    b->x = reinterpret_cast<float*>(base + o_x);
+    b->qkv = reinterpret_cast<float*>(base + o_qkv);
+    b->q_rot = reinterpret_cast<float*>(base + o_q);
+    b->attn = reinterpret_cast<float*>(base + o_a);
+    b->r = reinterpret_cast<float*>(base + o_r);
+    b->hidden = reinterpret_cast<float*>(base + o_h);
+    b->attn_ws = base + o_aw;
+    b->argmax_ws = base + o_gw;
+  }
+  return true;
+}
+
+int splits_of(const qd_model_desc* d) {
+  return d->attn_splits > 0 ? d->attn_splits : qd_attention_default_splits(d->capacity);
+}
+
+}  // namespace
+
+size_t qd_decode_workspace_bytes(const qd_model_desc* d) {
+  if (d == nullptr) return 0;
+  size_t total = 0;
+  step_layout(d, splits_of(d), nullptr, &total);
+  return total;
+}
+
+int qd_decode_step(const qd_model_desc* d, void* stream) {
+  return qd_decode_step_phases(d, 0, d ? d->num_layers : 0, QD_PHASE_ALL, stream);
+}
+
+int qd_decode_step_phases(const qd_model_desc* d, int first_layer, int n_layers, unsigned phase_mask,
+                          void* stream) {
+  QD_REQUIRE(d && d->layers && d->embed && d->final_norm && d->token && d->cache_position && d->rope_position &&
+                 d->inv_freq && d->workspace,
+             QD_ERR_ARG, "incomplete model descriptor");
+  QD_REQUIRE(d->head_dim == 128 && d->hidden % 512 == 0 && d->intermediate % 512 == 0 &&
+                 d->num_heads % d->num_kv_heads == 0 && d->num_heads * d->head_dim % 512 == 0,
+             QD_ERR_SHAPE, "unsupported model shape");
+  QD_REQUIRE(first_layer >= 0 && n_layers >= 0 && first_layer + n_layers <= d->num_layers, QD_ERR_ARG,
+             "layer range [%d, %d) outside the model", first_layer, first_layer + n_layers);
+  hipStream_t s = S(stream);
+  const int splits = splits_of(d);
+  StepBuffers b;
+  size_t total = 0;
+  step_layout(d, splits, &b, &total);
+  const int H = d->hidden, D = d->head_dim, Hq = d->num_heads, Hkv = d->num_kv_heads, I = d->intermediate;
+  const long qs = (long)Hq * D, kvs = (long)Hkv * D;
+  int st = QD_OK;
+  if (phase_mask & QD_PHASE_EMBED) {
+    if ((st = qd::embed_gather_launch((const u16*)d->embed, d->token, b.x, H, d->vocab, s))) return st;
+  }
+  for (int li = first_layer; li < first_layer + n_layers; ++li) {
+    const qd_layer_weights& w = d->layers[li];
+    // 1. input RMSNorm + fused QKV GEMV
+    GemvArgs g1;
+    g1.x = b.x; g1.gamma = (const u16*)w.input_norm; g1.W = (const u16*)w.qkv; g1.y = b.qkv;
+    g1.N = qs + 2 * kvs; g1.K = H; g1.ldw = H; g1.eps = d->eps;
+    if ((phase_mask & QD_PHASE_QKV) && (st = qd::gemv_store<qd::PRO_RMSNORM, float, float>(g1, s))) return st;
+    // 2. q/k head RMSNorm + M-RoPE, K/V written at cache_position
+    qd::RopeArgs ra;
+    ra.q = b.qkv; ra.k = b.qkv + qs; ra.v = b.qkv + qs + kvs;
+    ra.q_weight = (const u16*)w.q_norm; ra.k_weight = (const u16*)w.k_norm; ra.eps = d->eps;
+    ra.rope_pos = d->rope_position; ra.inv_freq = d->inv_freq; ra.sec_h = d->sec_h; ra.sec_w = d->sec_w;
+    ra.q_out = b.q_rot; ra.k_cache = (u16*)w.k_cache; ra.v_cache = (u16*)w.v_cache;
+    ra.cache_stride_h = (long)d->capacity * D; ra.cache_stride_s = D; ra.T = d->capacity;
+    ra.cache_position = d->cache_position; ra.Hq = Hq; ra.Hkv = Hkv;
+    if ((phase_mask & QD_PHASE_ROPE_KV) && (st = qd::q_rope_kv_launch<float, float>(ra, s))) return st;
+    // 3. split-KV attention with fused merge
+    qd::AttnArgs aa;
+    aa.q = b.q_rot; aa.q_stride = D; aa.k = (const u16*)w.k_cache; aa.v = (const u16*)w.v_cache;
+    aa.stride_h = (long)d->capacity * D; aa.stride_s = D; aa.T = d->capacity; aa.cache_position = d->cache_position;
+    aa.scale = 1.0f / sqrtf((float)D); aa.Hq = Hq; aa.Hkv = Hkv; aa.n_split = splits; aa.out = b.attn;
+    attn_ws(b.attn_ws, aa);
+    if ((phase_mask & QD_PHASE_ATTN) && (st = qd::attention_launch<float, float>(aa, true, s))) return st;
+    // 4. o_proj + residual: r = x + W_o attn
+    GemvArgs g4;
+    g4.x = b.attn; g4.W = (const u16*)w.o_proj; g4.residual = b.x; g4.y = b.r; g4.N = H; g4.K = qs; g4.ldw = qs;
+    if ((phase_mask & QD_PHASE_O_PROJ) && (st = qd::gemv_store<qd::PRO_PLAIN, float, float>(g4, s))) return st;
+    // 5. post-attn RMSNorm + gate_up + SiLU*up
+    GemvArgs g5;
+    g5.x = b.r; g5.gamma = (const u16*)w.post_norm; g5.W = (const u16*)w.gate_up; g5.y = b.hidden;
+    g5.N = I; g5.K = H; g5.ldw = H; g5.up_offset = I; g5.eps = d->eps;
+    if ((phase_mask & QD_PHASE_GATE_UP) && (st = qd::gemv_silu<qd::PRO_RMSNORM, float, float>(g5, s))) return st;
+    // 6. down_proj + residual: x = r + W_d hidden
+    GemvArgs g6;
+    g6.x = b.hidden; g6.W = (const u16*)w.down; g6.residual = b.r; g6.y = b.x; g6.N = H; g6.K = I; g6.ldw = I;
+    if ((phase_mask & QD_PHASE_DOWN) && (st = qd::gemv_store<qd::PRO_PLAIN, float, float>(g6, s))) return st;
+  }
+  // final RMSNorm + tied lm_head + argmax -> token
+  GemvArgs gl;
+  gl.x = b.x; gl.gamma = (const u16*)d->final_norm; gl.eps = d->eps; gl.W = (const u16*)d->embed;
+  gl.N = d->vocab; gl.K = H; gl.ldw = H; gl.y = d->logits_out; gl.token = d->token;
+  argmax_ws(b.argmax_ws, gl);
+  if (phase_mask & QD_PHASE_LM_HEAD) return qd::gemv_argmax<qd::PRO_RMSNORM, float, u16>(gl, s);
+  return QD_OK;
+}
+
+int qd_decode_advance(const int64_t* token, int64_t* out_tokens, int64_t* counter, int64_t* cache_position,
+                      int64_t* rope_position, int max_tokens, void* stream) {
+  QD_REQUIRE(token && counter && cache_position && rope_position, QD_ERR_ARG, "null pointer");
+  return qd::decode_advance_launch(token, out_tokens, counter, cache_position, rope_position, max_tokens,
+                                   S(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,201 @@
+// Device helpers shared by the gfx950 decode kernels.
+//
+// Wave64 throughout: a wavefront is 64 lanes; cross-lane sums use DPP row
+// operations inside each 16-lane row and v_readlane across the four rows, so a
+// full-wave reduction costs 4 DPP adds + 3 scalar-operand adds and leaves the
+// (bit-identical) result in every lane.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include "../../include/qwen3vl_decode.h"
+
+namespace qd {
+
+constexpr int kWave = 64;
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------- conversions
+
+__device__ __forceinline__ float h2f(uint16_t bits) {
+  return (float)__builtin_bit_cast(_Float16, bits);
+}
+__device__ __forceinline__ uint16_t f2h(float v) {
+  return __builtin_bit_cast(uint16_t, (_Float16)v);
+}
+__device__ __forceinline__ float lo_f(unsigned int u) { return h2f((uint16_t)(u & 0xffffu)); }
+__device__ __forceinline__ float hi_f(unsigned int u) { return h2f((uint16_t)(u >> 16)); }
+
+// 8 consecutive fp16 values -> fp32.
+__device__ __forceinline__ void unpack8(const u32x4 v, float* o) {
+  o[0] = lo_f(v.x); o[1] = hi_f(v.x);
+  o[2] = lo_f(v.y); o[3] = hi_f(v.y);
+  o[4] = lo_f(v.z); o[5] = hi_f(v.z);
+  o[6] = lo_f(v.w); o[7] = hi_f(v.w);
+}
+
+__device__ __forceinline__ unsigned int pack2(float a, float b) {
+  return (unsigned int)f2h(a) | ((unsigned int)f2h(b) << 16);
+}
+
+// acc += sum_i w[i] * x[i] for 8 fp16 weights and fp32 x (fp32 products).
+__device__ __forceinline__ float dot8(const u32x4 w, const float* x, float acc) {
+  acc = __builtin_fmaf(lo_f(w.x), x[0], acc);
+  acc = __builtin_fmaf(hi_f(w.x), x[1], acc);
+  acc = __builtin_fmaf(lo_f(w.y), x[2], acc);
+  acc = __builtin_fmaf(hi_f(w.y), x[3], acc);
+  acc = __builtin_fmaf(lo_f(w.z), x[4], acc);
+  acc = __builtin_fmaf(hi_f(w.z), x[5], acc);
+  acc = __builtin_fmaf(lo_f(w.w), x[6], acc);
+  acc = __builtin_fmaf(hi_f(w.w), x[7], acc);
+  return acc;
+}
+
+// ---------------------------------------------------------------- memory
+
+// Streamed (read-once) 16-byte load: weights and KV rows.
+__device__ __forceinline__ u32x4 ld_stream(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+__device__ __forceinline__ u32x4 ld16(const void* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+
+// Load 8 activation values starting at element i of a fp16 or fp32 vector.
+template <typename T>
+__device__ __forceinline__ void load_act8(const T* p, long i, float* o);
+template <>
+__device__ __forceinline__ void load_act8<uint16_t>(const uint16_t* p, long i, float* o) {
+  unpack8(ld16(p + i), o);
+}
+template <>
+__device__ __forceinline__ void load_act8<float>(const float* p, long i, float* o) {
+  const u32x4 a = ld16(p + i);
+  const u32x4 b = ld16(p + i + 4);
+  o[0] = __builtin_bit_cast(float, a.x); o[1] = __builtin_bit_cast(float, a.y);
+  o[2] = __builtin_bit_cast(float, a.z); o[3] = __builtin_bit_cast(float, a.w);
+  o[4] = __builtin_bit_cast(float, b.x); o[5] = __builtin_bit_cast(float, b.y);
+  o[6] = __builtin_bit_cast(float, b.z); o[7] = __builtin_bit_cast(float, b.w);
+}
+
+template <typename T>
+__device__ __forceinline__ float load_act(const T* p, long i);
+template <>
+__device__ __forceinline__ float load_act<uint16_t>(const uint16_t* p, long i) { return h2f(p[i]); }
+template <>
+__device__ __forceinline__ float load_act<float>(const float* p, long i) { return p[i]; }
+
+template <typename T>
+__device__ __forceinline__ void store_act(T* p, long i, float v);
+template <>
+__device__ __forceinline__ void store_act<uint16_t>(uint16_t* p, long i, float v) { p[i] = f2h(v); }
+template <>
+__device__ __forceinline__ void store_act<float>(float* p, long i, float v) { p[i] = v; }
+
+template <typename T>
+__device__ __forceinline__ void store_act8(T* p, long i, const float* v);
+template <>
+__device__ __forceinline__ void store_act8<uint16_t>(uint16_t* p, long i, const float* v) {
+  u32x4 o;
+  o.x = pack2(v[0], v[1]); o.y = pack2(v[2], v[3]);
+  o.z = pack2(v[4], v[5]); o.w = pack2(v[6], v[7]);
+  *reinterpret_cast<u32x4*>(p + i) = o;
+}
+template <>
+__device__ __forceinline__ void store_act8<float>(float* p, long i, const float* v) {
+  u32x4 a, b;
+  a.x = __builtin_bit_cast(unsigned, v[0]); a.y = __builtin_bit_cast(unsigned, v[1]);
+  a.z = __builtin_bit_cast(unsigned, v[2]); a.w = __builtin_bit_cast(unsigned, v[3]);
+  b.x = __builtin_bit_cast(unsigned, v[4]); b.y = __builtin_bit_cast(unsigned, v[5]);
+  b.z = __builtin_bit_cast(unsigned, v[6]); b.w = __builtin_bit_cast(unsigned, v[7]);
+  *reinterpret_cast<u32x4*>(p + i) = a;
+  *reinterpret_cast<u32x4*>(p + i + 4) = b;
+}
+
+// ---------------------------------------------------------------- cross-lane
+
+// DPP controls (GCN/CDNA encoding).
+constexpr int kDppQuadXor1 = 0xB1;   // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;   // quad_perm [2,3,0,1]
+constexpr int kDppRowRor4 = 0x124;   // row_ror:4
+constexpr int kDppRowRor8 = 0x128;   // row_ror:8
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+      0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over each 16-lane row; every lane of the row receives the row sum.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp<kDppQuadXor1>(v);
+  v += dpp<kDppQuadXor2>(v);
+  v += dpp<kDppRowRor4>(v);
+  v += dpp<kDppRowRor8>(v);
+  return v;
+}
+
+__device__ __forceinline__ float readlane(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// Full-wave sum, uniform in all lanes, fixed summation order.
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row16_sum(v);
+  return (readlane(v, 0) + readlane(v, 16)) + (readlane(v, 32) + readlane(v, 48));
+}
+
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp<kDppQuadXor1>(v));
+  v = fmaxf(v, dpp<kDppQuadXor2>(v));
+  v = fmaxf(v, dpp<kDppRowRor4>(v));
+  v = fmaxf(v, dpp<kDppRowRor8>(v));
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  v = row16_max(v);
+  return fmaxf(fmaxf(readlane(v, 0), readlane(v, 16)), fmaxf(readlane(v, 32), readlane(v, 48)));
+}
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
+
+// ---------------------------------------------------------------- cross-workgroup hand-off
+//
+// L2 is private to each XCD, so data handed between workgroups of one launch
+// is published with an agent-scope release (write-back of dirty L2 lines) and
+// read after an agent-scope acquire (invalidate of stale L2 lines).
+
+__device__ __forceinline__ unsigned atomic_add_release(unsigned* p, unsigned v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_relaxed(unsigned* p, unsigned v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void fence_acquire() {
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+}
+__device__ __forceinline__ void fence_release() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+}
+
+}  // namespace qd
+
+// Host-side error reporting shared by the C-ABI translation units.
+namespace qd_host {
+void set_error(const char* fmt, ...);
+int launch_status(const char* what);
+int cu_count();
+}  // namespace qd_host
+
+#define QD_REQUIRE(cond, code, ...)          \
+  do {                                       \
+    if (!(cond)) {                           \
+      qd_host::set_error(__VA_ARGS__);       \
+      return (code);                         \
+    }                                        \
+  } while (0)

@@ -1,0 +1,382 @@
+// Batch-1 decode GEMV family for gfx950.
+//
+// y[N] = W[N, K] . x[K] with fp16 weights, fp32 accumulation and optional
+// prologues (RMSNorm, residual-add + RMSNorm) and epilogues (bias/residual
+// add, SiLU(gate)*up over row pairs, fused argmax, split-K partials).
+//
+// Layout: one wave64 owns R whole rows at a time.  Lane l of the wave holds the
+// K-slice {c*512 + 8l .. c*512 + 8l + 7 : c < K/512} of x in registers (fp32),
+// so every weight load is a 16-byte-per-lane, 1 KiB-per-wave contiguous
+// stream and x never goes through LDS.  The row sum is a DPP + readlane wave
+// reduction.  The RMSNorm prologue needs sum(x^2) over all K, which each wave
+// already holds across its 64 lanes: no LDS, no block barrier.
+//
+// Reference kernels replaced: decode_gemv_kernel_matvec.cuh:208-347
+// (nosplit k2048 / row2), decode_gemv_kernel_fused.cuh:99-185 (rmsnorm+qkv),
+// :856-1076 (post-attn MLP phases), decode_gemv_kernel_matvec.cuh:1-205 (split-K).
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "qd_common.h"
+#include "qd_kernels.h"
+
+namespace qd {
+
+template <int KCH, int R, int PRO, int EPI, typename TX, typename TY>
+__global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
+  constexpr int K = KCH * 512;
+  constexpr int RO = (EPI == EPI_SILU) ? R / 2 : R;  // outputs per wave iteration
+  static_assert(EPI != EPI_SILU || (R % 2) == 0, "SiLU epilogue works on row pairs");
+  const int lane = lane_id();
+  const int wpb = blockDim.x / kWave;
+  const int wib = threadIdx.x / kWave;
+  const long kofs = (long)blockIdx.y * K;  // split-K slice (gridDim.y == 1 otherwise)
+  const long gw = (long)blockIdx.x * wpb + wib;
+  const long nw = (long)gridDim.x * wpb;
+
+  // ---- x slice -> registers (+ prologue)
+  float xr[KCH][8];
+  const TX* x = reinterpret_cast<const TX*>(a.x);
+#pragma unroll
+  for (int c = 0; c < KCH; ++c) load_act8(x, kofs + c * 512 + lane * 8, xr[c]);
+  if constexpr (PRO == PRO_ADD_RMSNORM) {
+    const TX* x2 = reinterpret_cast<const TX*>(a.x2);
+#pragma unroll
+    for (int c = 0; c < KCH; ++c) {
+      float t[8];
+      load_act8(x2, c * 512 + lane * 8, t);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) xr[c][i] += t[i];
+    }
+    if (a.r_out != nullptr && blockIdx.x == 0 && wib == 0) {
+#pragma unroll
+      for (int c = 0; c < KCH; ++c) store_act8(reinterpret_cast<TY*>(a.r_out), c * 512 + lane * 8, xr[c]);
+    }
+  }
+  if constexpr (PRO == PRO_SILU) {
+    const TX* x2 = reinterpret_cast<const TX*>(a.x2);
+#pragma unroll
+    for (int c = 0; c < KCH; ++c) {
+      float t[8];
+      load_act8(x2, kofs + c * 512 + lane * 8, t);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) xr[c][i] = (xr[c][i] / (1.0f + __expf(-xr[c][i]))) * t[i];
+    }
+  }
+  if constexpr (PRO == PRO_RMSNORM || PRO == PRO_ADD_RMSNORM) {
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < KCH; ++c)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(xr[c][i], xr[c][i], ss);
+    ss = wave_sum(ss);
+    const float rstd = rsqrtf(ss / (float)K + a.eps);
+#pragma unroll
+    for (int c = 0; c < KCH; ++c) {
+      float g[8];
+      unpack8(ld16(a.gamma + c * 512 + lane * 8), g);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) xr[c][i] = (xr[c][i] * rstd) * g[i];
+    }
+  }
+
+  float best_v = -INFINITY;
+  long best_i = 0x7fffffffffffL;
+
+  // ---- row loop
+  for (long o0 = gw * RO; o0 < a.N; o0 += nw * RO) {
+    u32x4 wv[R][KCH];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const long oi = o0 + (r % RO);
+      const long row = (EPI == EPI_SILU && r >= RO) ? oi + a.up_offset : oi;
+      if (oi < a.N) {
+        const uint16_t* wr = a.W + row * a.ldw + kofs + lane * 8;
+#pragma unroll
+        for (int c = 0; c < KCH; ++c) wv[r][c] = ld_stream(wr + c * 512);
+      } else {
+#pragma unroll
+        for (int c = 0; c < KCH; ++c) wv[r][c] = u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float s = 0.f;
+#pragma unroll
+      for (int c = 0; c < KCH; ++c) s = dot8(wv[r][c], xr[c], s);
+      acc[r] = wave_sum(s);
+    }
+
+    if constexpr (EPI == EPI_STORE) {
+      if (lane == 0) {
+        TY* y = reinterpret_cast<TY*>(a.y);
+        const TY* bias = reinterpret_cast<const TY*>(a.bias);
+        const TY* res = reinterpret_cast<const TY*>(a.residual);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const long o = o0 + r;
+          if (o < a.N) {
+            float v = acc[r];
+            if (bias != nullptr) v += load_act(bias, o);
+            if (res != nullptr) v += load_act(res, o);
+            store_act(y, o, v);
+          }
+        }
+      }
+    } else if constexpr (EPI == EPI_SILU) {
+      if (lane == 0) {
+        TY* y = reinterpret_cast<TY*>(a.y);
+#pragma unroll
+        for (int r = 0; r < RO; ++r) {
+          const long o = o0 + r;
+          if (o < a.N) {
+            const float g = acc[r];
+            const float u = acc[r + RO];
+            store_act(y, o, (g / (1.0f + __expf(-g))) * u);
+          }
+        }
+      }
+    } else if constexpr (EPI == EPI_PARTIAL) {
+      if (lane == 0) {
+        float* part = a.part_val + (long)blockIdx.y * a.N;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+          if (o0 + r < a.N) part[o0 + r] = acc[r];
+      }
+    } else {  // EPI_ARGMAX
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const long o = o0 + r;
+        if (o < a.N && acc[r] > best_v) {  // rows visited in increasing order: first max wins
+          best_v = acc[r];
+          best_i = o;
+        }
+      }
+      if (a.y != nullptr && lane == 0) {
+        TY* y = reinterpret_cast<TY*>(a.y);
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+          if (o0 + r < a.N) store_act(y, o0 + r, acc[r]);
+      }
+    }
+  }
+
+  if constexpr (EPI == EPI_ARGMAX) {
+    __shared__ float s_v[16];
+    __shared__ long s_i[16];
+    __shared__ int s_last;
+    if (lane == 0) {
+      s_v[wib] = best_v;
+      s_i[wib] = best_i;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float bv = s_v[0];
+      long bi = s_i[0];
+      for (int w = 1; w < wpb; ++w) {
+        if (s_v[w] > bv || (s_v[w] == bv && s_i[w] < bi)) {
+          bv = s_v[w];
+          bi = s_i[w];
+        }
+      }
+      a.part_val[blockIdx.x] = bv;
+      a.part_idx[blockIdx.x] = bi;
+      const unsigned prev = atomic_add_release(a.counter, 1u);
+      s_last = (prev == gridDim.x - 1);
+    }
+    __syncthreads();
+    if (s_last) {
+      fence_acquire();
+      float bv = -INFINITY;
+      long bi = 0x7fffffffffffL;
+      for (int b = threadIdx.x; b < (int)gridDim.x; b += blockDim.x) {
+        const float v = a.part_val[b];
+        const long i = a.part_idx[b];
+        if (v > bv || (v == bv && i < bi)) {
+          bv = v;
+          bi = i;
+        }
+      }
+      __shared__ float r_v[256];
+      __shared__ long r_i[256];
+      r_v[threadIdx.x] = bv;
+      r_i[threadIdx.x] = bi;
+      __syncthreads();
+      for (int s = blockDim.x / 2; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) {
+          const float v = r_v[threadIdx.x + s];
+          const long i = r_i[threadIdx.x + s];
+          if (v > r_v[threadIdx.x] || (v == r_v[threadIdx.x] && i < r_i[threadIdx.x])) {
+            r_v[threadIdx.x] = v;
+            r_i[threadIdx.x] = i;
+          }
+        }
+        __syncthreads();
+      }
+      if (threadIdx.x == 0) {
+        a.token[0] = (int64_t)r_i[0];
+        store_relaxed(a.counter, 0u);  // self-reset for the next launch / graph replay
+      }
+    }
+  }
+}
+
+// Generic fallback: any K % 8 == 0; one wave per output row, x streamed from
+// global memory.  Used by the drop-in entry points for non-model shapes.
+template <int PRO, typename TX, typename TY>
+__global__ __launch_bounds__(256) void gemv_generic_kernel(const GemvArgs a) {
+  const int lane = lane_id();
+  const long gw = (long)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  const long nw = (long)gridDim.x * (blockDim.x / kWave);
+  const TX* x = reinterpret_cast<const TX*>(a.x);
+  float rstd = 1.f;
+  if constexpr (PRO == PRO_RMSNORM) {
+    float ss = 0.f;
+    for (long k = lane; k < a.K; k += kWave) {
+      const float v = load_act(x, k);
+      ss = __builtin_fmaf(v, v, ss);
+    }
+    ss = wave_sum(ss);
+    rstd = rsqrtf(ss / (float)a.K + a.eps);
+  }
+  for (long o = gw; o < a.N; o += nw) {
+    const uint16_t* wr = a.W + o * a.ldw;
+    float s = 0.f;
+    for (long k = lane * 8; k < a.K; k += kWave * 8) {
+      float xv[8];
+      load_act8(x, k, xv);
+      if constexpr (PRO == PRO_RMSNORM) {
+        float g[8];
+        unpack8(ld16(a.gamma + k), g);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xv[i] = (xv[i] * rstd) * g[i];
+      }
+      s = dot8(ld_stream(wr + k), xv, s);
+    }
+    s = wave_sum(s);
+    if (lane == 0) {
+      const TY* bias = reinterpret_cast<const TY*>(a.bias);
+      const TY* res = reinterpret_cast<const TY*>(a.residual);
+      if (bias != nullptr) s += load_act(bias, o);
+      if (res != nullptr) s += load_act(res, o);
+      store_act(reinterpret_cast<TY*>(a.y), o, s);
+    }
+  }
+}
+
+// Split-K reduce: y[o] = sum_s part[s*N + o] (+ bias[o]) in slice order.
+template <typename TY>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* part, const TY* bias, TY* y, long N,
+                                                            int splits) {
+  for (long o = (long)blockIdx.x * blockDim.x + threadIdx.x; o < N; o += (long)gridDim.x * blockDim.x) {
+    float s = 0.f;
+    for (int p = 0; p < splits; ++p) s += part[(long)p * N + o];
+    if (bias != nullptr) s += load_act(bias, o);
+    store_act(y, o, s);
+  }
+}
+
+// ---------------------------------------------------------------- host launchers
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWavesPerBlock = kThreads / kWave;
+
+long ceil_div(long a, long b) { return (a + b - 1) / b; }
+
+template <int KCH, int R, int PRO, int EPI, typename TX, typename TY>
+int launch_fixed(const GemvArgs& a, int splits, long max_blocks, hipStream_t s) {
+  constexpr int RO = (EPI == EPI_SILU) ? R / 2 : R;
+  long blocks = ceil_div(ceil_div(a.N, RO), kWavesPerBlock);
+  if (max_blocks > 0 && blocks > max_blocks) blocks = max_blocks;
+  if (blocks < 1) blocks = 1;
+  hipLaunchKernelGGL((gemv_kernel<KCH, R, PRO, EPI, TX, TY>), dim3((unsigned)blocks, (unsigned)splits),
+                     dim3(kThreads), 0, s, a);
+  return qd_host::launch_status("gemv_kernel");
+}
+
+// Dispatch on K (per split slice) to a register-resident kernel; R rows per wave.
+template <int R, int PRO, int EPI, typename TX, typename TY>
+int launch_k(const GemvArgs& a, int k_slice, int splits, long max_blocks, hipStream_t s) {
+  switch (k_slice) {
+    case 512: return launch_fixed<1, R, PRO, EPI, TX, TY>(a, splits, max_blocks, s);
+    case 1024: return launch_fixed<2, R, PRO, EPI, TX, TY>(a, splits, max_blocks, s);
+    case 2048: return launch_fixed<4, R, PRO, EPI, TX, TY>(a, splits, max_blocks, s);
+    case 3072: return launch_fixed<6, (R > 2 ? 2 : R), PRO, EPI, TX, TY>(a, splits, max_blocks, s);
+    case 4096: return launch_fixed<8, (R > 2 ? 2 : R), PRO, EPI, TX, TY>(a, splits, max_blocks, s);
+    case 6144: return launch_fixed<12, (R > 2 ? 2 : R), PRO, EPI, TX, TY>(a, splits, max_blocks, s);
+    default: return 1;  // caller falls back
+  }
+}
+
+bool has_fixed_k(int k) {
+  return k == 512 || k == 1024 || k == 2048 || k == 3072 || k == 4096 || k == 6144;
+}
+
+}  // namespace
+
+// Rows per wave chosen so that small N still spreads over every SIMD.
+static int rows_for(long n_out) { return n_out <= 2048 ? 2 : 4; }
+
+template <int PRO, typename TX, typename TY>
+int gemv_store(const GemvArgs& a, hipStream_t s) {
+  if (has_fixed_k(a.K)) {
+    const int r = rows_for(a.N);
+    return r == 2 ? launch_k<2, PRO, EPI_STORE, TX, TY>(a, a.K, 1, 0, s)
+                  : launch_k<4, PRO, EPI_STORE, TX, TY>(a, a.K, 1, 0, s);
+  }
+  if constexpr (PRO == PRO_ADD_RMSNORM || PRO == PRO_SILU) return QD_ERR_SHAPE;
+  long blocks = ceil_div(a.N, kWavesPerBlock);
+  const long cap = (long)qd_host::cu_count() * 8;
+  if (blocks > cap) blocks = cap;
+  hipLaunchKernelGGL((gemv_generic_kernel<PRO, TX, TY>), dim3((unsigned)blocks), dim3(kThreads), 0, s, a);
+  return qd_host::launch_status("gemv_generic_kernel");
+}
+
+template <int PRO, typename TX, typename TY>
+int gemv_silu(const GemvArgs& a, hipStream_t s) {
+  if (!has_fixed_k(a.K)) return QD_ERR_SHAPE;
+  return launch_k<4, PRO, EPI_SILU, TX, TY>(a, a.K, 1, 0, s);
+}
+
+template <int PRO, typename TX, typename TY>
+int gemv_argmax(const GemvArgs& a, hipStream_t s) {
+  if (!has_fixed_k(a.K)) return QD_ERR_SHAPE;
+  const long max_blocks = (long)qd_host::cu_count() * 4;
+  return launch_k<4, PRO, EPI_ARGMAX, TX, TY>(a, a.K, 1, max_blocks > kMaxArgmaxBlocks ? kMaxArgmaxBlocks : max_blocks, s);
+}
+
+template <typename TX, typename TY>
+int gemv_splitk(const GemvArgs& a, int splits, hipStream_t s) {
+  const int k_slice = a.K / splits;
+  if (a.K % splits != 0 || !has_fixed_k(k_slice)) return QD_ERR_SHAPE;
+  int st = launch_k<4, PRO_PLAIN, EPI_PARTIAL, TX, TY>(a, k_slice, splits, 0, s);
+  if (st != QD_OK) return st;
+  long blocks = ceil_div(a.N, kThreads);
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL((splitk_reduce_kernel<TY>), dim3((unsigned)blocks), dim3(kThreads), 0, s, a.part_val,
+                     reinterpret_cast<const TY*>(a.bias), reinterpret_cast<TY*>(a.y), (long)a.N, splits);
+  return qd_host::launch_status("splitk_reduce_kernel");
+}
+
+// Explicit instantiations used by the C ABI and the decode step.
+template int gemv_store<PRO_PLAIN, uint16_t, uint16_t>(const GemvArgs&, hipStream_t);
+template int gemv_store<PRO_RMSNORM, uint16_t, uint16_t>(const GemvArgs&, hipStream_t);
+template int gemv_store<PRO_ADD_RMSNORM, uint16_t, uint16_t>(const GemvArgs&, hipStream_t);
+template int gemv_store<PRO_SILU, uint16_t, uint16_t>(const GemvArgs&, hipStream_t);
+template int gemv_store<PRO_PLAIN, float, float>(const GemvArgs&, hipStream_t);
+template int gemv_store<PRO_RMSNORM, float, float>(const GemvArgs&, hipStream_t);
+template int gemv_silu<PRO_ADD_RMSNORM, uint16_t, uint16_t>(const GemvArgs&, hipStream_t);
+template int gemv_silu<PRO_RMSNORM, uint16_t, uint16_t>(const GemvArgs&, hipStream_t);
+template int gemv_silu<PRO_PLAIN, uint16_t, uint16_t>(const GemvArgs&, hipStream_t);
+template int gemv_silu<PRO_RMSNORM, float, float>(const GemvArgs&, hipStream_t);
+template int gemv_argmax<PRO_RMSNORM, float, uint16_t>(const GemvArgs&, hipStream_t);
+template int gemv_argmax<PRO_RMSNORM, uint16_t, uint16_t>(const GemvArgs&, hipStream_t);
+template int gemv_argmax<PRO_PLAIN, uint16_t, uint16_t>(const GemvArgs&, hipStream_t);
+template int gemv_splitk<uint16_t, uint16_t>(const GemvArgs&, int, hipStream_t);
+
+}  // namespace qd

@@ -1,0 +1,107 @@
+// Internal (C++) launch interface shared by the kernel translation units and
+// the C-ABI layer.  Not part of the public ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qd {
+
+// PRO_SILU: x[k] = silu(x[k]) * x2[k] (x2 = the 'up' half of a gate_up vector).
+enum GemvPrologue { PRO_PLAIN = 0, PRO_RMSNORM = 1, PRO_ADD_RMSNORM = 2, PRO_SILU = 3 };
+enum GemvEpilogue { EPI_STORE = 0, EPI_SILU = 1, EPI_ARGMAX = 2, EPI_PARTIAL = 3 };
+
+constexpr int kMaxArgmaxBlocks = 4096;
+
+struct GemvArgs {
+  const void* x = nullptr;         // activation [K] (TX)
+  const void* x2 = nullptr;        // PRO_ADD_RMSNORM second addend [K] (TX)
+  const uint16_t* gamma = nullptr; // RMSNorm weight [K] fp16
+  const uint16_t* W = nullptr;     // fp16 [rows, ldw]
+  const void* bias = nullptr;      // [N] (TY) or null
+  const void* residual = nullptr;  // [N] (TY) added after the dot, or null
+  void* y = nullptr;               // output [N] (TY); EPI_ARGMAX: optional logits
+  void* r_out = nullptr;           // PRO_ADD_RMSNORM: pre-norm sum [K] (TY) or null
+  long N = 0;                      // outputs (EPI_SILU: gate rows == up rows == N)
+  long K = 0;
+  long ldw = 0;
+  long up_offset = 0;              // EPI_SILU: row offset of the up half
+  float eps = 1e-6f;
+  float* part_val = nullptr;       // EPI_ARGMAX per-block max / EPI_PARTIAL [splits, N]
+  long* part_idx = nullptr;        // EPI_ARGMAX per-block argmax
+  unsigned* counter = nullptr;     // EPI_ARGMAX arrival counter (self-resetting)
+  int64_t* token = nullptr;        // EPI_ARGMAX result
+};
+
+template <int PRO, typename TX, typename TY>
+int gemv_store(const GemvArgs& a, hipStream_t s);
+template <int PRO, typename TX, typename TY>
+int gemv_silu(const GemvArgs& a, hipStream_t s);
+template <int PRO, typename TX, typename TY>
+int gemv_argmax(const GemvArgs& a, hipStream_t s);
+template <typename TX, typename TY>
+int gemv_splitk(const GemvArgs& a, int splits, hipStream_t s);
+
+// ---------------------------------------------------------------- attention
+
+struct AttnArgs {
+  const void* q = nullptr;         // [Hq, 128] rows of stride q_stride (TQ)
+  long q_stride = 128;
+  const uint16_t* k = nullptr;     // fp16 cache [Hkv, T, 128]
+  const uint16_t* v = nullptr;
+  long stride_h = 0, stride_s = 128;
+  int T = 0;
+  const int64_t* cache_position = nullptr;
+  float scale = 0.f;
+  int Hq = 16, Hkv = 8, n_split = 1;
+  float* o_part = nullptr;         // [Hq, n_split, 128]
+  float* lse = nullptr;            // [Hq, n_split]
+  unsigned* counters = nullptr;    // [Hkv] (fused merge only)
+  void* out = nullptr;             // [Hq, 128] (TO)
+};
+
+template <typename TQ, typename TO>
+int attention_launch(const AttnArgs& a, bool fused_merge, hipStream_t s);
+template <typename TO>
+int attention_merge_launch(const AttnArgs& a, hipStream_t s);
+
+// ---------------------------------------------------------------- small ops
+
+struct RopeArgs {
+  const void* q = nullptr;
+  const void* k = nullptr;
+  const void* v = nullptr;
+  long q_stride = 128, k_stride = 128, v_stride = 128;   // per head (elements)
+  long q_row = 0, k_row = 0;                              // per token row (qk-norm op)
+  const uint16_t* q_weight = nullptr;
+  const uint16_t* k_weight = nullptr;
+  float eps = 1e-6f;
+  const uint16_t* cos = nullptr;   // fp16 [M, 128] or null
+  const uint16_t* sin = nullptr;
+  long cs_row = 128;
+  const int64_t* rope_pos = nullptr;  // int64 [3]
+  const float* inv_freq = nullptr;    // fp32 [64]
+  int sec_h = 20, sec_w = 20;
+  void* q_out = nullptr;           // [M, Hq, 128]
+  void* k_out = nullptr;           // [M, Hkv, 128] (qk-norm op) or null
+  uint16_t* k_cache = nullptr;     // cache-write op
+  uint16_t* v_cache = nullptr;
+  long cache_stride_h = 0, cache_stride_s = 128;
+  int T = 0;
+  const int64_t* cache_position = nullptr;
+  int Hq = 16, Hkv = 8, M = 1;
+};
+
+template <typename TI, typename TO>
+int q_rope_kv_launch(const RopeArgs& a, hipStream_t s);
+int qk_norm_rope_f16_launch(const RopeArgs& a, hipStream_t s);
+
+int add_rmsnorm_f16_launch(const uint16_t* res, const uint16_t* x, const uint16_t* w, uint16_t* out_sum,
+                           uint16_t* out_norm, int rows, int cols, float eps, hipStream_t s);
+int silu_mul_f16_launch(const uint16_t* g, const uint16_t* u, uint16_t* out, long n, hipStream_t s);
+int add_f16_launch(const uint16_t* a, const uint16_t* b, uint16_t* out, long n, hipStream_t s);
+int embed_gather_launch(const uint16_t* table, const int64_t* token, float* out, int H, long V, hipStream_t s);
+int decode_advance_launch(const int64_t* token, int64_t* out_tokens, int64_t* counter, int64_t* cache_position,
+                          int64_t* rope_position, int max_tokens, hipStream_t s);
+
+}  // namespace qd

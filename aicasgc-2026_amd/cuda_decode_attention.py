@@ -1,0 +1,186 @@
+#!/usr/bin/env python3
+"""Decode-attention entry points backed by the gfx950 split-KV kernels.
+
+Same names, arguments and return conventions as the reference's
+cuda_decode_attention.py: inputs are q [1, Hq, 1, D] (any row stride),
+static K/V caches [1, Hkv, T, D] and a device ``cache_position`` [1]; the
+valid length is min(cache_position + 1, T); the result is returned as a
+[1, 1, Hq, D] view, or ``None`` when the inputs are outside what the kernels
+support (the caller then falls back, optimized_layer.py:2404-2458).
+
+All variants compute the same softmax(q K^T * scale) V.  On MI355X one kernel
+serves them: each workgroup owns a (kv head, KV split) and serves all q heads
+of the group, so K/V is read once; splits are merged from (normalised output,
+LSE) partials either by the last-arriving workgroup (``*_fused`` and
+``*_cta_*`` names) or by a separate merge launch (``decode_attn_v4_splitkv``).
+``split_k`` is honoured as a minimum split count; the kernel may use more
+splits to fill 256 CUs (results do not depend on the split count).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from qwen3vl_hip import _lib
+
+_WS_KEY = "_qd_attention_ws"
+
+
+def _load_ext():
+    return _lib.lib()
+
+
+def _workspace_layout(*, num_kv_heads: int, num_key_value_groups: int, head_dim: int, split_k: int) -> dict:
+    """Reference workspace shapes (cuda_decode_attention.py:74-79), kept for callers that build them."""
+    return {
+        "partial_acc_shape": (num_kv_heads, split_k, num_key_value_groups, head_dim),
+        "partial_stats_shape": (num_kv_heads, split_k, num_key_value_groups, 2),
+        "out_shape": (1, num_kv_heads * num_key_value_groups, head_dim),
+    }
+
+
+def _qhead_workspace_layout(*, num_heads: int, head_dim: int, split_k: int) -> dict:
+    return {
+        "partial_acc_shape": (num_heads, split_k, head_dim),
+        "partial_stats_shape": (num_heads, split_k, 2),
+        "out_shape": (1, num_heads, head_dim),
+    }
+
+
+def _v4_launch_config(seq_len: int) -> int:
+    """Reference split heuristic (cuda_decode_attention.py:216-223)."""
+    if seq_len < 1024:
+        return 16
+    return 32
+
+
+def _supported(q, k, v, num_key_value_groups, cache_position) -> bool:
+    return not (
+        q.device.type != "cuda" or k.device.type != "cuda" or v.device.type != "cuda"
+        or cache_position.device.type != "cuda"
+        or q.dtype != torch.float16 or k.dtype != torch.float16 or v.dtype != torch.float16
+        or q.ndim != 4 or k.ndim != 4 or v.ndim != 4
+        or q.shape[0] != 1 or q.shape[2] != 1 or q.shape[-1] != 128
+        or k.shape[0] != 1 or k.shape != v.shape or k.shape[-1] != 128
+        or k.shape[1] * num_key_value_groups != q.shape[1]
+        or num_key_value_groups not in (1, 2, 4)
+        or q.stride(-1) != 1 or k.stride(-1) != 1 or v.stride(-1) != 1
+        or k.stride(1) != v.stride(1) or k.stride(2) != v.stride(2)
+        or q.stride(1) % 8 != 0 or k.stride(1) % 8 != 0 or k.stride(2) % 8 != 0
+        or q.data_ptr() % 16 != 0 or k.data_ptr() % 16 != 0 or v.data_ptr() % 16 != 0
+        or cache_position.dtype != torch.long or cache_position.numel() != 1
+    )
+
+
+def _splits(seq_len: int, split_k: int | None) -> int:
+    s = int(_load_ext().qd_attention_default_splits(int(seq_len)))
+    return max(s, int(split_k)) if split_k else s
+
+
+def _out_buffer(workspace, q) -> torch.Tensor:
+    hq, d = q.shape[1], q.shape[-1]
+    if (workspace is not None and "out" in workspace and tuple(workspace["out"].shape) == (1, hq, d)
+            and workspace["out"].dtype == q.dtype and workspace["out"].device == q.device):
+        return workspace["out"]
+    return torch.empty((1, hq, d), dtype=q.dtype, device=q.device)
+
+
+def _ws_buffer(workspace, q, n_bytes: int) -> torch.Tensor:
+    """Graph-stable kernel workspace; zero-initialised once (its counters self-reset)."""
+    if workspace is not None:
+        t = workspace.get(_WS_KEY)
+        if t is not None and t.numel() >= n_bytes and t.device == q.device:
+            return t
+    t = torch.zeros(n_bytes, dtype=torch.uint8, device=q.device)
+    if workspace is not None:
+        workspace[_WS_KEY] = t
+    return t
+
+
+def _run_fused(q, k, v, scaling, num_key_value_groups, cache_position, split_k, workspace):
+    if not _supported(q, k, v, num_key_value_groups, cache_position):
+        return None
+    lib = _load_ext()
+    hq, hkv, T = q.shape[1], k.shape[1], k.shape[2]
+    n_split = _splits(T, split_k)
+    out = _out_buffer(workspace, q)
+    ws = _ws_buffer(workspace, q, int(lib.qd_attention_workspace_bytes(hq, hkv, n_split)))
+    _lib.check(lib.qd_attention_decode(
+        _lib.ptr(q), _lib.QD_F16, q.stride(1), _lib.ptr(k), _lib.ptr(v), k.stride(1), k.stride(2), T,
+        _lib.ptr(cache_position), float(scaling), _lib.ptr(out), _lib.QD_F16, hq, hkv, n_split, _lib.ptr(ws),
+        _lib.stream(q.device)), "qd_attention_decode")
+    return out.unsqueeze(2).transpose(1, 2)
+
+
+def decode_attn_v4_cta_qhead_splitkv_fused(q, k, v, scaling, num_key_value_groups, cache_position, split_k: int = 4,
+                                           workspace: dict | None = None):
+    """Reference cuda_decode_attention.py:489-558 (default decode attention)."""
+    if split_k <= 1:
+        return None
+    return _run_fused(q, k, v, scaling, num_key_value_groups, cache_position, split_k, workspace)
+
+
+def decode_attn_v4_fused(q, k, v, scaling, num_key_value_groups, cache_position, split_k: int | None = None,
+                         workspace: dict | None = None, prefetch_weight=None, prefetch_blocks: int = 0):
+    """Reference cuda_decode_attention.py:305-392.  The o_proj L2-prefetch
+    sidecar is an A800 experiment and is ignored."""
+    del prefetch_weight, prefetch_blocks
+    return _run_fused(q, k, v, scaling, num_key_value_groups, cache_position, split_k, workspace)
+
+
+def decode_attn_v4_cta_local(q, k, v, scaling, num_key_value_groups, cache_position, out=None):
+    """Reference cuda_decode_attention.py:395-432."""
+    ws = {"out": out} if out is not None else None
+    return _run_fused(q, k, v, scaling, num_key_value_groups, cache_position, None, ws)
+
+
+def decode_attn_v4_cta_qhead(q, k, v, scaling, num_key_value_groups, cache_position, warps_per_cta: int = 4,
+                             lane_layout: int = 0, prefetch_mode: int = 0, merge_mode: int = 0, out=None):
+    """Reference cuda_decode_attention.py:435-486 (A800 lane-layout knobs ignored)."""
+    del warps_per_cta, lane_layout, prefetch_mode, merge_mode
+    ws = {"out": out} if out is not None else None
+    return _run_fused(q, k, v, scaling, num_key_value_groups, cache_position, None, ws)
+
+
+def decode_attn_v4_splitkv(q, k, v, scaling, num_key_value_groups, cache_position, split_k: int | None = None,
+                           workspace: dict | None = None, prefetch_weight=None, prefetch_blocks: int = 0):
+    """Reference cuda_decode_attention.py:226-302: partials then a merge launch.
+
+    ``workspace`` may hold fp32 ``partial_acc`` [Hq, S, 128] and ``lse`` [Hq, S]."""
+    del prefetch_weight, prefetch_blocks
+    if not _supported(q, k, v, num_key_value_groups, cache_position):
+        return None
+    lib = _load_ext()
+    hq, hkv, T = q.shape[1], k.shape[1], k.shape[2]
+    n_split = _splits(T, split_k)
+    if (workspace is not None and "partial_acc" in workspace and "lse" in workspace
+            and tuple(workspace["partial_acc"].shape) == (hq, n_split, 128)
+            and tuple(workspace["lse"].shape) == (hq, n_split)):
+        o_part, lse = workspace["partial_acc"], workspace["lse"]
+    else:
+        o_part = torch.empty((hq, n_split, 128), dtype=torch.float32, device=q.device)
+        lse = torch.empty((hq, n_split), dtype=torch.float32, device=q.device)
+    out = _out_buffer(workspace, q)
+    st = _lib.stream(q.device)
+    _lib.check(lib.qd_attention_partial(
+        _lib.ptr(q), _lib.QD_F16, q.stride(1), _lib.ptr(k), _lib.ptr(v), k.stride(1), k.stride(2), T,
+        _lib.ptr(cache_position), float(scaling), _lib.ptr(o_part), _lib.ptr(lse), hq, hkv, n_split, st),
+        "qd_attention_partial")
+    _lib.check(lib.qd_attention_merge(_lib.ptr(o_part), _lib.ptr(lse), _lib.ptr(out), _lib.QD_F16, hq, n_split, st),
+               "qd_attention_merge")
+    return out.unsqueeze(2).transpose(1, 2)
+
+
+def grouped_prefix_cachepos_splitkv(q, k, v, scaling, num_key_value_groups, cache_position, split_k: int,
+                                    workspace: dict | None = None):
+    """Reference cuda_decode_attention.py:90-150 (older kernel family)."""
+    if split_k <= 1:
+        return None
+    return _run_fused(q, k, v, scaling, num_key_value_groups, cache_position, split_k, workspace)
+
+
+def grouped_prefix_cachepos_splitkv_qhead(q, k, v, scaling, num_key_value_groups, cache_position, split_k: int,
+                                          workspace: dict | None = None):
+    if split_k <= 1:
+        return None
+    return _run_fused(q, k, v, scaling, num_key_value_groups, cache_position, split_k, workspace)

@@ -1,0 +1,243 @@
+"""Fused decode GEMV entry points (batch 1, fp16) backed by gfx950 kernels.
+
+Same names, arguments and return conventions as the reference's
+cuda_decode_gemv_ops/fused.py.  The reference ships several launch strategies
+for the same math (persistent, softsync, gridsync, mega); each name maps to
+the MI355X kernel that computes that math, so callers selecting any of them
+get identical results.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .matvec import nosplit_matvec_half
+from .runtime import _check, _contig_weight, _load_ext, _p, _require_decode_half, _reuse, _stream
+
+__all__ = [
+    "fused_add_rmsnorm_gateup_half", "fused_rmsnorm_qkv_half", "fused_silu_downproj_half",
+    "fused_gateup_silu_downproj_half", "fused_post_attn_mlp_persistent_half", "fused_post_attn_mlp_softsync_half",
+    "fused_o_proj_post_attn_mlp_persistent_half", "fused_o_proj_post_attn_mlp_softsync_half",
+    "fused_decode_full_layer_softsync_half", "fused_gateup_silu_downproj_mega_half",
+    "fused_gateup_silu_downproj_mega_partial_half", "fused_gateup_silu_downproj_softsync_half",
+    "fused_gateup_silu_downproj_gridsync_half", "fused_gateup_silu_downproj_persistent_half",
+    "decode_attn_persistent_half",
+]
+
+
+def _vec(t: torch.Tensor) -> torch.Tensor:
+    return t.reshape(-1).contiguous()
+
+
+def fused_rmsnorm_qkv_half(x: torch.Tensor, norm_weight: torch.Tensor, weight: torch.Tensor,
+                           bias: torch.Tensor | None, eps: float) -> torch.Tensor:
+    """out = W (rmsnorm(x) * gamma) (+ b)  (reference fused.py:71-105)."""
+    name = "fused_rmsnorm_qkv_half"
+    _require_decode_half(name, x, norm_weight, weight, x=x)
+    w = _contig_weight(weight, name)
+    n, k = w.shape
+    x_vec, g = _vec(x), _vec(norm_weight)
+    if x_vec.numel() != k or g.numel() != k:
+        raise RuntimeError(f"{name}: x/norm_weight must have K={k} elements")
+    out = torch.empty((n,), dtype=x.dtype, device=x.device)
+    b = _vec(bias) if bias is not None else None
+    _check(_load_ext().qd_rmsnorm_matvec_f16(_p(x_vec), _p(g), _p(w), _p(b), _p(out), n, k, float(eps),
+                                             _stream(x)), name)
+    return out.view(*x.shape[:-1], n)
+
+
+def fused_add_rmsnorm_gateup_half(residual: torch.Tensor, x: torch.Tensor, norm_weight: torch.Tensor,
+                                  weight: torch.Tensor, bias: torch.Tensor | None, eps: float,
+                                  workspace: dict | None = None):
+    """(residual + x, W rmsnorm(residual + x)) (reference fused.py:12-68)."""
+    name = "fused_add_rmsnorm_gateup_half"
+    _require_decode_half(name, residual, x, norm_weight, weight, x=residual)
+    if residual.shape != x.shape:
+        raise RuntimeError(f"{name}: residual/x shapes differ")
+    w = _contig_weight(weight, name)
+    n, k = w.shape
+    res_out = _reuse(workspace, "fused_add_rmsnorm_gateup", "residual_out", (k,), residual.dtype, residual.device)
+    out = _reuse(workspace, "fused_add_rmsnorm_gateup", "out", (n,), residual.dtype, residual.device)
+    b = _vec(bias) if bias is not None else None
+    _check(_load_ext().qd_add_rmsnorm_matvec_f16(_p(_vec(residual)), _p(_vec(x)), _p(_vec(norm_weight)), _p(w),
+                                                 _p(b), _p(res_out), _p(out), n, k, float(eps), _stream(x)), name)
+    return res_out.view_as(residual), out.view(*residual.shape[:-1], n)
+
+
+def fused_silu_downproj_half(gate_up: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None,
+                             workspace: dict | None = None) -> torch.Tensor:
+    """W (silu(gate) * up) (+ b) for gate_up = [gate; up] (reference fused.py:108-145)."""
+    name = "fused_silu_downproj_half"
+    _require_decode_half(name, gate_up, weight, x=gate_up)
+    w = _contig_weight(weight, name)
+    n, k = w.shape
+    gu = _vec(gate_up)
+    if gu.numel() != 2 * k:
+        raise RuntimeError(f"{name}: gate_up must have 2*K = {2 * k} elements")
+    out = _reuse(workspace, "fused_silu_downproj", "out", (n,), gate_up.dtype, gate_up.device)
+    b = _vec(bias) if bias is not None else None
+    _check(_load_ext().qd_silu_matvec_f16(_p(gu), _p(w), _p(b), _p(out), n, k, _stream(gate_up)), name)
+    return out.view(*gate_up.shape[:-1], n)
+
+
+def _gateup_silu_down(name: str, x, gate_up_weight, down_proj_weight, bias, workspace, kind):
+    _require_decode_half(name, x, gate_up_weight, down_proj_weight, x=x)
+    wgu = _contig_weight(gate_up_weight, name)
+    wd = _contig_weight(down_proj_weight, name)
+    two_i, h = wgu.shape
+    n, i = wd.shape
+    if two_i != 2 * i or _vec(x).numel() != h:
+        raise RuntimeError(f"{name}: inconsistent shapes gate_up {tuple(wgu.shape)} down {tuple(wd.shape)}")
+    hidden = _reuse(workspace, kind, "hidden_out", (i,), x.dtype, x.device)
+    out = _reuse(workspace, kind, "out", (n,), x.dtype, x.device)
+    b = _vec(bias) if bias is not None else None
+    _check(_load_ext().qd_gateup_silu_down_f16(_p(_vec(x)), _p(wgu), _p(wd), _p(b), _p(hidden), _p(out), h, i,
+                                               _stream(x)), name)
+    return hidden.view(*x.shape[:-1], i), out.view(*x.shape[:-1], n)
+
+
+def fused_gateup_silu_downproj_half(x, gate_up_weight, down_proj_weight, bias, workspace=None):
+    """(silu(W_g x) * W_u x, W_d of it (+ b)) (reference fused.py:148-197)."""
+    return _gateup_silu_down("fused_gateup_silu_downproj_half", x, gate_up_weight, down_proj_weight, bias,
+                             workspace, "fused_gateup_silu_downproj")
+
+
+def fused_gateup_silu_downproj_persistent_half(x, gate_up_weight, down_proj_weight, workspace=None):
+    return _gateup_silu_down("fused_gateup_silu_downproj_persistent_half", x, gate_up_weight, down_proj_weight,
+                             None, workspace, "fused_gateup_silu_downproj_persistent")
+
+
+def fused_gateup_silu_downproj_softsync_half(x, gate_up_weight, down_proj_weight, workspace=None):
+    return _gateup_silu_down("fused_gateup_silu_downproj_softsync_half", x, gate_up_weight, down_proj_weight,
+                             None, workspace, "fused_gateup_silu_downproj_softsync")
+
+
+def fused_gateup_silu_downproj_gridsync_half(x, gate_up_weight, down_proj_weight, workspace=None):
+    return _gateup_silu_down("fused_gateup_silu_downproj_gridsync_half", x, gate_up_weight, down_proj_weight,
+                             None, workspace, "fused_gateup_silu_downproj_gridsync")
+
+
+def fused_gateup_silu_downproj_mega_half(x, gate_up_weight, down_proj_weight, workspace=None):
+    return _gateup_silu_down("fused_gateup_silu_downproj_mega_half", x, gate_up_weight, down_proj_weight,
+                             None, workspace, "fused_gateup_silu_downproj_mega")
+
+
+def fused_gateup_silu_downproj_mega_partial_half(x, gate_up_weight, down_proj_weight, workspace=None):
+    return _gateup_silu_down("fused_gateup_silu_downproj_mega_partial_half", x, gate_up_weight,
+                             down_proj_weight, None, workspace, "fused_gateup_silu_downproj_mega_partial")
+
+
+def _post_attn_mlp(name, residual, attn_output, norm_weight, gate_up_weight, down_proj_weight, bias, eps, workspace,
+                   kind):
+    _require_decode_half(name, residual, attn_output, norm_weight, gate_up_weight, down_proj_weight, x=residual)
+    if residual.shape != attn_output.shape:
+        raise RuntimeError(f"{name} expects fp16 CUDA single-token decode tensors")
+    if bias is not None:
+        _require_decode_half(name, bias)
+    wgu = _contig_weight(gate_up_weight, name)
+    wd = _contig_weight(down_proj_weight, name)
+    two_i, h = wgu.shape
+    n, i = wd.shape
+    if two_i != 2 * i or n != h or residual.shape[-1] != h:
+        raise RuntimeError(f"{name}: inconsistent shapes")
+    hidden = _reuse(workspace, kind, "hidden_out", (i,), residual.dtype, residual.device)
+    out = _reuse(workspace, kind, "out", (n,), residual.dtype, residual.device)
+    b = _vec(bias) if bias is not None else None
+    _check(_load_ext().qd_post_attn_mlp_f16(_p(_vec(residual)), _p(_vec(attn_output)), _p(_vec(norm_weight)),
+                                            _p(wgu), _p(wd), _p(b), _p(hidden), _p(out), h, i, float(eps),
+                                            _stream(residual)), name)
+    return hidden.view(*residual.shape[:-1], i), out.view(*residual.shape[:-1], n)
+
+
+def fused_post_attn_mlp_softsync_half(residual, attn_output, norm_weight, gate_up_weight, down_proj_weight, bias,
+                                      eps, workspace=None, threads_per_block: int = 1024, launch_blocks=None):
+    """Post-attention MLP of a layer (reference fused.py:261-337):
+    r = residual + attn; hidden = silu(W_g x) * W_u x with x = rmsnorm(r) * gamma;
+    out = W_d hidden + r (+ b).  Returns (hidden [.., I], out [.., H]).
+    ``threads_per_block`` / ``launch_blocks`` tuned the A800 launch and are
+    accepted for compatibility."""
+    del threads_per_block, launch_blocks
+    return _post_attn_mlp("fused_post_attn_mlp_softsync_half", residual, attn_output, norm_weight, gate_up_weight,
+                          down_proj_weight, bias, eps, workspace, "fused_post_attn_mlp_softsync")
+
+
+def fused_post_attn_mlp_persistent_half(residual, attn_output, norm_weight, gate_up_weight, down_proj_weight, bias,
+                                        eps, workspace=None):
+    return _post_attn_mlp("fused_post_attn_mlp_persistent_half", residual, attn_output, norm_weight,
+                          gate_up_weight, down_proj_weight, bias, eps, workspace, "fused_post_attn_mlp_persistent")
+
+
+def _o_proj_post_attn_mlp(name, residual, attn_input, o_proj_weight, o_proj_bias, norm_weight, gate_up_weight,
+                          down_proj_weight, down_proj_bias, eps, workspace):
+    o = nosplit_matvec_half(attn_input, o_proj_weight, o_proj_bias)
+    return _post_attn_mlp(name, residual, o.view_as(residual), norm_weight, gate_up_weight, down_proj_weight,
+                          down_proj_bias, eps, workspace, name)
+
+
+def fused_o_proj_post_attn_mlp_persistent_half(residual, attn_input, o_proj_weight, o_proj_bias, norm_weight,
+                                               gate_up_weight, down_proj_weight, down_proj_bias, eps, workspace=None):
+    """o_proj followed by the post-attention MLP (reference fused.py:340-409)."""
+    return _o_proj_post_attn_mlp("fused_o_proj_post_attn_mlp_persistent_half", residual, attn_input, o_proj_weight,
+                                 o_proj_bias, norm_weight, gate_up_weight, down_proj_weight, down_proj_bias, eps,
+                                 workspace)
+
+
+def fused_o_proj_post_attn_mlp_softsync_half(residual, attn_input, o_proj_weight, o_proj_bias, norm_weight,
+                                             gate_up_weight, down_proj_weight, down_proj_bias, eps, workspace=None,
+                                             gate_up_active_sms: int = 0):
+    del gate_up_active_sms
+    return _o_proj_post_attn_mlp("fused_o_proj_post_attn_mlp_softsync_half", residual, attn_input, o_proj_weight,
+                                 o_proj_bias, norm_weight, gate_up_weight, down_proj_weight, down_proj_bias, eps,
+                                 workspace)
+
+
+def fused_decode_full_layer_softsync_half(hidden_states, qkv_weight, input_layernorm_weight, q_norm_weight,
+                                          k_norm_weight, cos, sin, k_cache, v_cache, cache_position, o_proj_weight,
+                                          o_proj_bias, post_attn_norm_weight, gate_up_weight, down_proj_weight,
+                                          down_proj_bias, eps, attn_scale, workspace=None, launch_blocks=None):
+    """One full decoder layer for one token (reference fused.py:498-665): the
+    layer chain of QKV, q/k norm + RoPE + KV write, attention, o_proj and MLP."""
+    import cuda_decode_attention
+    import cuda_decode_small_ops
+
+    del launch_blocks
+    name = "fused_decode_full_layer_softsync_half"
+    _require_decode_half(name, hidden_states, qkv_weight, x=hidden_states)
+    hkv, d = k_cache.shape[1], k_cache.shape[3]
+    hq = (qkv_weight.shape[0] - 2 * hkv * d) // d
+    qkv = fused_rmsnorm_qkv_half(hidden_states, input_layernorm_weight, qkv_weight, None, eps).reshape(-1)
+    q = qkv[: hq * d].view(1, 1, hq, d)
+    k = qkv[hq * d: (hq + hkv) * d].view(1, 1, hkv, d)
+    v = qkv[(hq + hkv) * d:].view(1, 1, hkv, d)
+    q_rot = cuda_decode_small_ops.fused_q_rope_kv_cache_update(q, k, v, q_norm_weight, k_norm_weight, eps, cos, sin,
+                                                               k_cache, v_cache, cache_position)
+    attn = cuda_decode_attention.decode_attn_v4_cta_qhead_splitkv_fused(
+        q_rot.transpose(1, 2), k_cache, v_cache, attn_scale, hq // hkv, cache_position)
+    if attn is None:
+        raise RuntimeError(f"{name}: unsupported attention shape")
+    attn = attn.reshape(*hidden_states.shape[:-1], hq * d)
+    _hidden, out = fused_o_proj_post_attn_mlp_persistent_half(hidden_states, attn, o_proj_weight, o_proj_bias,
+                                                              post_attn_norm_weight, gate_up_weight,
+                                                              down_proj_weight, down_proj_bias, eps, workspace)
+    return out
+
+
+def decode_attn_persistent_half(q, k_cache, v_cache, cache_position, scale, workspace=None):
+    """Decode attention returning [1, Hq, 1, D] (reference fused.py:895-965)."""
+    import cuda_decode_attention
+
+    if (q.device.type != "cuda" or k_cache.device.type != "cuda" or v_cache.device.type != "cuda"
+            or q.dtype != torch.float16 or k_cache.dtype != torch.float16 or v_cache.dtype != torch.float16):
+        raise RuntimeError("decode_attn_persistent_half expects fp16 CUDA tensors")
+    if q.ndim == 4:
+        hq, d = q.shape[1], q.shape[3]
+    elif q.ndim == 3:
+        hq, d = q.shape[1], q.shape[2]
+    else:
+        raise RuntimeError("q must be 3D or 4D")
+    q4 = q.reshape(1, hq, 1, d)
+    out = cuda_decode_attention.decode_attn_v4_fused(q4, k_cache, v_cache, scale, hq // k_cache.shape[1],
+                                                     cache_position)
+    if out is None:
+        raise RuntimeError("decode_attn_persistent_half: unsupported shape")
+    return out.reshape(1, hq, 1, d)

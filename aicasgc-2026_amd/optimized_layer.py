@@ -1,0 +1,265 @@
+"""Qwen3-VL decoder layer whose batch-1 decode step runs on gfx950 HIP kernels.
+
+Drop-in for the reference's optimized_layer.py: ``OptimizedDecoderLayer``
+wraps an HF ``Qwen3VLTextDecoderLayer`` (same constructor, same forward
+signature, fused qkv / gate_up weights as at optimized_layer.py:60-84), and
+``replace_decoder_layers`` swaps it into a model.
+
+Decode step (one token, batch 1, fp16, GPU, static KV cache; the chain of
+optimized_layer.py:108-469):
+
+    fused_rmsnorm_qkv_half            RMSNorm + QKV GEMV        (HIP)
+    fused_q_rope_kv_cache_update      q/k norm + RoPE + KV write (HIP)
+    decode_attn_v4_cta_qhead_splitkv_fused  split-KV attention  (HIP)
+    nosplit_matvec_half               o_proj GEMV               (HIP)
+    fused_post_attn_mlp_softsync_half add+RMSNorm, gate_up+SiLU, down+residual (HIP)
+
+If the HIP library is missing these raise RuntimeError.  Other inputs
+(prefill with several tokens) take the HF layer math with PyTorch-ROCm ops,
+like the reference's own non-decode path.  CPU tensors are rejected: the
+CPU restatement of this math lives in the test oracle, not in the product.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+import cuda_decode_attention
+import cuda_decode_gemv
+import cuda_decode_small_ops
+
+
+@dataclass(slots=True)
+class PrefillFastpathContext:
+    """Kept for import compatibility with the reference (optimized_layer.py:22-27)."""
+
+    position_embeddings: tuple
+    past_key_values: object
+    cache_position: torch.Tensor
+    cache_kwargs: dict | None
+
+
+class OptimizedDecoderLayer(nn.Module):
+    """Drop-in replacement for Qwen3VLTextDecoderLayer (reference optimized_layer.py:30-469)."""
+
+    def __init__(self, orig_layer):
+        super().__init__()
+        attn = orig_layer.self_attn
+        mlp = orig_layer.mlp
+        self.hidden_size = orig_layer.hidden_size
+        self.head_dim = attn.head_dim
+        self.num_heads = attn.config.num_attention_heads
+        self.num_kv_heads = attn.config.num_key_value_heads
+        self.num_key_value_groups = attn.num_key_value_groups
+        self.scaling = attn.scaling
+        self.is_causal = attn.is_causal
+        self.layer_idx = attn.layer_idx
+        self.attention_dropout = attn.attention_dropout
+        self.rms_norm_eps = attn.config.rms_norm_eps
+
+        self.input_layernorm_weight = orig_layer.input_layernorm.weight
+        self.post_attn_layernorm_weight = orig_layer.post_attention_layernorm.weight
+        self.q_norm_weight = attn.q_norm.weight
+        self.k_norm_weight = attn.k_norm.weight
+
+        self.q_size = self.num_heads * self.head_dim
+        self.kv_size = self.num_kv_heads * self.head_dim
+        self.qkv_weight = nn.Parameter(
+            torch.cat([attn.q_proj.weight.data, attn.k_proj.weight.data, attn.v_proj.weight.data], 0).contiguous(),
+            requires_grad=False)
+        self.qkv_bias = None
+        if getattr(attn.q_proj, "bias", None) is not None:
+            self.qkv_bias = torch.cat([attn.q_proj.bias.data, attn.k_proj.bias.data, attn.v_proj.bias.data], 0)
+        self.o_proj = attn.o_proj
+        self.o_proj_weight = attn.o_proj.weight
+        self.o_proj_bias = attn.o_proj.bias
+
+        self.intermediate_size = mlp.intermediate_size
+        self.gate_up_weight = nn.Parameter(
+            torch.cat([mlp.gate_proj.weight.data, mlp.up_proj.weight.data], 0).contiguous(), requires_grad=False)
+        self.down_proj = mlp.down_proj
+        self.down_proj_weight = mlp.down_proj.weight
+        self.down_proj_bias = mlp.down_proj.bias
+
+        self.config = attn.config
+        self._attn_implementation = getattr(attn.config, "_attn_implementation", "sdpa")
+        self._prefer_small_decode_triton = False
+        # graph-stable workspaces of the decode kernels
+        self._attention_workspace: dict = {}
+        self._post_attn_mlp_workspace: dict = {"type": "fused_post_attn_mlp_softsync"}
+        self._o_proj_workspace: dict = {"type": "nosplit"}
+
+    # ------------------------------------------------------------ dispatch
+    def _static_kv(self, past_key_values, k_like: torch.Tensor):
+        if past_key_values is None:
+            return None
+        layers = getattr(past_key_values, "layers", None)
+        if layers is None or self.layer_idx >= len(layers):
+            return None
+        layer = layers[self.layer_idx]
+        if not getattr(layer, "is_initialized", True) and hasattr(layer, "lazy_initialization"):
+            layer.lazy_initialization(k_like, k_like)
+        kc, vc = getattr(layer, "keys", None), getattr(layer, "values", None)
+        if kc is None or vc is None or kc.ndim != 4 or kc.shape[0] != 1 or kc.device != k_like.device:
+            return None
+        if getattr(layer, "max_cache_len", kc.shape[2]) != kc.shape[2]:
+            return None
+        return kc, vc
+
+    def _decode_ok(self, hidden_states, position_embeddings, cache_position) -> bool:
+        cos, sin = position_embeddings
+        return (hidden_states.device.type == "cuda" and hidden_states.dtype == torch.float16
+                and hidden_states.ndim == 3 and hidden_states.shape[0] == 1 and hidden_states.shape[1] == 1
+                and cache_position is not None and cache_position.device.type == "cuda"
+                and cache_position.numel() == 1 and self.head_dim == 128
+                and self.num_heads == 2 * self.num_kv_heads and cos.dtype == torch.float16
+                and cos.numel() == 128 and sin.numel() == 128 and self.qkv_bias is None)
+
+    def forward(self, hidden_states: torch.Tensor, position_embeddings: tuple, attention_mask=None,
+                position_ids=None, past_key_values=None, use_cache=False, cache_position=None,
+                **kwargs) -> torch.Tensor:
+        if hidden_states.device.type != "cuda":
+            raise RuntimeError("OptimizedDecoderLayer runs on a ROCm GPU (got a CPU tensor)")
+        kwargs.pop("prefill_static_cache_no_mask", None)
+        if self._decode_ok(hidden_states, position_embeddings, cache_position):
+            kv = self._static_kv(past_key_values, hidden_states.new_empty(1, self.num_kv_heads, 1, self.head_dim))
+            if kv is not None:
+                return self._decode_step(hidden_states, position_embeddings, kv, cache_position.reshape(1))
+        return self._general_forward(hidden_states, position_embeddings, attention_mask, position_ids,
+                                     past_key_values, use_cache, cache_position, **kwargs)
+
+    # ------------------------------------------------------------ HIP decode chain
+    def _decode_step(self, hidden_states, position_embeddings, kv, cache_position):
+        cos, sin = position_embeddings
+        k_cache, v_cache = kv
+        eps = self.rms_norm_eps
+        qkv = cuda_decode_gemv.fused_rmsnorm_qkv_half(hidden_states, self.input_layernorm_weight, self.qkv_weight,
+                                                      None, eps)
+        q, k, v = qkv.split([self.q_size, self.kv_size, self.kv_size], dim=-1)
+        q_rot = cuda_decode_small_ops.fused_q_rope_kv_cache_update(
+            q.view(1, 1, self.num_heads, self.head_dim), k.view(1, 1, self.num_kv_heads, self.head_dim),
+            v.view(1, 1, self.num_kv_heads, self.head_dim), self.q_norm_weight, self.k_norm_weight, eps,
+            cos.reshape(1, 1, 128), sin.reshape(1, 1, 128), k_cache, v_cache, cache_position)
+        attn = cuda_decode_attention.decode_attn_v4_cta_qhead_splitkv_fused(
+            q_rot.transpose(1, 2), k_cache, v_cache, self.scaling, self.num_key_value_groups, cache_position,
+            split_k=4, workspace=self._attention_workspace)
+        if attn is None:
+            raise RuntimeError("decode attention inputs unsupported by the HIP kernel")
+        attn = attn.reshape(1, 1, self.q_size)
+        o = cuda_decode_gemv.nosplit_matvec_half(attn, self.o_proj_weight, self.o_proj_bias,
+                                                 workspace=self._o_proj_workspace)
+        _hidden, out = cuda_decode_gemv.fused_post_attn_mlp_softsync_half(
+            hidden_states, o, self.post_attn_layernorm_weight, self.gate_up_weight, self.down_proj_weight,
+            self.down_proj_bias, eps, workspace=self._post_attn_mlp_workspace)
+        return out
+
+    # ------------------------------------------------------------ general (prefill) path
+    def _general_forward(self, hidden_states, position_embeddings, attention_mask, position_ids, past_key_values,
+                         use_cache, cache_position, **kwargs):
+        """HF Qwen3VLTextDecoderLayer math (transformers modeling_qwen3_vl.py:526-568) on PyTorch-ROCm."""
+        from transformers.models.qwen3_vl.modeling_qwen3_vl import apply_rotary_pos_emb, eager_attention_forward
+        from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
+
+        residual = hidden_states
+        input_shape = hidden_states.shape[:-1]
+        x = _rms_norm(hidden_states, self.input_layernorm_weight, self.rms_norm_eps)
+        qkv = F.linear(x, self.qkv_weight, self.qkv_bias)
+        q, k, v = qkv.split([self.q_size, self.kv_size, self.kv_size], dim=-1)
+        q = _rms_norm(q.view(*input_shape, -1, self.head_dim), self.q_norm_weight, self.rms_norm_eps).transpose(1, 2)
+        k = _rms_norm(k.view(*input_shape, -1, self.head_dim), self.k_norm_weight, self.rms_norm_eps).transpose(1, 2)
+        v = v.view(*input_shape, -1, self.head_dim).transpose(1, 2)
+        cos, sin = position_embeddings
+        q, k = apply_rotary_pos_emb(q, k, cos, sin)
+        if past_key_values is not None:
+            k, v = past_key_values.update(k, v, self.layer_idx, {"sin": sin, "cos": cos,
+                                                                  "cache_position": cache_position})
+        interface = ALL_ATTENTION_FUNCTIONS.get_interface(self._attn_implementation, eager_attention_forward)
+        attn, _ = interface(self, q, k, v, attention_mask, dropout=0.0, scaling=self.scaling, **kwargs)
+        attn = attn.reshape(*input_shape, -1).contiguous()
+        h = residual + F.linear(attn, self.o_proj_weight, self.o_proj_bias)
+        x2 = _rms_norm(h, self.post_attn_layernorm_weight, self.rms_norm_eps)
+        gu = F.linear(x2, self.gate_up_weight)
+        gate, up = gu.split([self.intermediate_size, self.intermediate_size], dim=-1)
+        return h + F.linear(F.silu(gate) * up, self.down_proj_weight, self.down_proj_bias)
+
+
+def _rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    """HF Qwen3VLTextRMSNorm (modeling_qwen3_vl.py:400-405)."""
+    dt = x.dtype
+    xf = x.to(torch.float32)
+    xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    return w * xf.to(dt)
+
+
+def _decoder_layers(model):
+    for path in ("model.language_model.layers", "language_model.layers", "model.layers", "layers"):
+        obj = model
+        try:
+            for part in path.split("."):
+                obj = getattr(obj, part)
+        except AttributeError:
+            continue
+        return obj
+    raise RuntimeError("could not find the decoder layer list on this model")
+
+
+def replace_decoder_layers(model) -> int:
+    """Swap every text decoder layer for OptimizedDecoderLayer (reference optimized_layer.py:3848-3858)."""
+    layers = _decoder_layers(model)
+    n = 0
+    for i, layer in enumerate(layers):
+        if not isinstance(layer, OptimizedDecoderLayer):
+            layers[i] = OptimizedDecoderLayer(layer)
+            n += 1
+    return n
+
+
+def set_small_decode_triton_enabled(model, enabled: bool) -> bool:
+    """Reference optimized_layer.py:3861-3873 toggled the graph-only fast paths.
+
+    The HIP decode chain is used whenever inputs qualify, so the flag is only
+    recorded on each layer.  Returns the previous value of the first layer."""
+    layers = _decoder_layers(model)
+    prev = bool(getattr(layers[0], "_prefer_small_decode_triton", False)) if len(layers) else False
+    for layer in layers:
+        if isinstance(layer, OptimizedDecoderLayer):
+            layer._prefer_small_decode_triton = bool(enabled)
+    return prev
+
+
+_FUSION_FLAG_NAMES = ("add_rmsnorm_gateup", "full_layer_softsync", "post_attn_mlp_persistent",
+                      "o_proj_post_attn_mlp_persistent", "o_proj_post_attn_mlp_softsync", "silu_downproj",
+                      "gateup_silu_downproj", "gateup_silu_downproj_mega")
+_FUSION_FLAGS = {n: n == "post_attn_mlp_persistent" for n in _FUSION_FLAG_NAMES}
+
+
+def set_cuda_mlp_fusion_flags(*, add_rmsnorm_gateup: bool | None = None, full_layer_softsync: bool | None = None,
+                              post_attn_mlp_persistent: bool | None = None,
+                              o_proj_post_attn_mlp_persistent: bool | None = None,
+                              o_proj_post_attn_mlp_softsync: bool | None = None, silu_downproj: bool | None = None,
+                              gateup_silu_downproj: bool | None = None,
+                              gateup_silu_downproj_mega: bool | None = None) -> tuple:
+    """Reference optimized_layer.py:3876-3921: sets the MLP fusion choices and
+    returns the previous 8-tuple.  Every choice computes the same math on
+    gfx950 (the decode chain above); the flags are recorded for callers that
+    read them back."""
+    prev = tuple(_FUSION_FLAGS[n] for n in _FUSION_FLAG_NAMES)
+    new = dict(add_rmsnorm_gateup=add_rmsnorm_gateup, full_layer_softsync=full_layer_softsync,
+               post_attn_mlp_persistent=post_attn_mlp_persistent,
+               o_proj_post_attn_mlp_persistent=o_proj_post_attn_mlp_persistent,
+               o_proj_post_attn_mlp_softsync=o_proj_post_attn_mlp_softsync, silu_downproj=silu_downproj,
+               gateup_silu_downproj=gateup_silu_downproj, gateup_silu_downproj_mega=gateup_silu_downproj_mega)
+    for n, v in new.items():
+        if v is not None:
+            _FUSION_FLAGS[n] = bool(v)
+    return prev
+
+
+def fused_vision_rope(*args, **kwargs):
+    """The reference's vision-tower RoPE kernel (optimized_layer.py:3268) belongs to the
+    prefill path, which this build does not provide."""
+    raise NotImplementedError("fused_vision_rope is part of the vision prefill path (out of scope)")

@@ -1,0 +1,269 @@
+"""Batch-1 greedy decode engine for the Qwen3-VL-2B text decoder on one MI355X.
+
+The hot path is one call of the native ``qd_decode_step`` (embedding row,
+28 layers of HIP kernels, final norm, lm_head + argmax) followed by
+``qd_decode_advance`` (append the token, advance cache/rope positions on the
+device).  Both are captured once into a HIP graph (``torch.cuda.CUDAGraph``);
+generation is a loop of graph replays with no host writes in between.
+
+Mirrors the reference's decode engine: GreedyDecodeEngine.generate
+(evaluation_wrapper.py:149-315) and DecodeCudaGraphRunner
+(evaluation_wrapper.py:747-1005: static input buffers, graph prebuild and
+replay).  The prefill that fills the static KV cache
+(evaluation_wrapper.py:218-228, a full HF forward in the reference) runs here
+as plain PyTorch-ROCm ops in fp32; it is not part of the decode step.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from .config import QWEN3VL_2B, Qwen3VLTextShape
+from .synthetic import ModelWeights, MultimodalPrompt
+
+
+def rope_inv_freq(shape: Qwen3VLTextShape = QWEN3VL_2B) -> torch.Tensor:
+    """inv_freq[j] = 1 / theta^(2j/d) in fp32, the same expression HF evaluates
+    (transformers modeling_qwen3_vl.py:340-342)."""
+    d = shape.head_dim
+    return 1.0 / (shape.rope_theta ** (torch.arange(0, d, 2, dtype=torch.float32) / d))
+
+
+class DecodeEngine:
+    """Owns device weights, the static KV cache and the captured decode step."""
+
+    def __init__(self, weights: ModelWeights, capacity: int, device="cuda", attn_splits: int = 0,
+                 keep_logits: bool = False):
+        if not torch.cuda.is_available():
+            raise RuntimeError("DecodeEngine needs a ROCm GPU")
+        self.device = torch.device(device)
+        if self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
+        self.shape = weights.shape
+        s = self.shape
+        self.capacity = int(capacity)
+        self.w = weights if weights.embed_tokens.device == self.device else weights.to(self.device)
+        self.k_caches = [torch.zeros(1, s.num_kv_heads, self.capacity, s.head_dim, dtype=torch.float16,
+                                     device=self.device) for _ in self.w.layers]
+        self.v_caches = [torch.zeros_like(k) for k in self.k_caches]
+        dev = self.device
+        self.token = torch.zeros(1, dtype=torch.int64, device=dev)
+        self.cache_position = torch.zeros(1, dtype=torch.int64, device=dev)
+        self.rope_position = torch.zeros(3, dtype=torch.int64, device=dev)
+        self.step_counter = torch.zeros(1, dtype=torch.int64, device=dev)
+        self.out_tokens = torch.zeros(1, dtype=torch.int64, device=dev)
+        self.inv_freq = rope_inv_freq(s).to(dev)
+        self.logits = torch.empty(s.vocab, dtype=torch.float16, device=dev) if keep_logits else None
+
+        layers = (_lib.LayerDesc * len(self.w.layers))()
+        for i, lw in enumerate(self.w.layers):
+            L = layers[i]
+            L.qkv = lw.qkv_weight.data_ptr()
+            L.o_proj = lw.o_proj_weight.data_ptr()
+            L.gate_up = lw.gate_up_weight.data_ptr()
+            L.down = lw.down_proj_weight.data_ptr()
+            L.input_norm = lw.input_layernorm_weight.data_ptr()
+            L.post_norm = lw.post_attn_layernorm_weight.data_ptr()
+            L.q_norm = lw.q_norm_weight.data_ptr()
+            L.k_norm = lw.k_norm_weight.data_ptr()
+            L.k_cache = self.k_caches[i].data_ptr()
+            L.v_cache = self.v_caches[i].data_ptr()
+        self._layers = layers
+        d = _lib.ModelDesc()
+        d.num_layers = len(self.w.layers)
+        d.hidden, d.num_heads, d.num_kv_heads = s.hidden, s.num_heads, s.num_kv_heads
+        d.head_dim, d.intermediate, d.vocab = s.head_dim, s.intermediate, s.vocab
+        d.capacity = self.capacity
+        d.eps = s.rms_eps
+        d.sec_t, d.sec_h, d.sec_w = s.mrope_section
+        d.inv_freq = self.inv_freq.data_ptr()
+        d.layers = ctypes.cast(layers, ctypes.POINTER(_lib.LayerDesc))
+        d.embed = self.w.embed_tokens.data_ptr()
+        d.final_norm = self.w.final_norm_weight.data_ptr()
+        d.token = self.token.data_ptr()
+        d.cache_position = self.cache_position.data_ptr()
+        d.rope_position = self.rope_position.data_ptr()
+        d.logits_out = self.logits.data_ptr() if self.logits is not None else None
+        d.attn_splits = int(attn_splits)
+        nbytes = _lib.lib().qd_decode_workspace_bytes(ctypes.byref(d))
+        self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+        d.workspace = self.workspace.data_ptr()
+        self.desc = d
+        self.graph = None
+        self._graph_max_tokens = 0
+
+    # ------------------------------------------------------------ state
+    def set_state(self, token: int, cache_position: int, rope_position: int) -> None:
+        self.token.fill_(int(token))
+        self.cache_position.fill_(int(cache_position))
+        self.rope_position.fill_(int(rope_position))
+
+    def reserve_tokens(self, n: int) -> None:
+        if self.out_tokens.numel() < n:
+            self.out_tokens = torch.zeros(n, dtype=torch.int64, device=self.device)
+            self.graph = None  # the captured advance kernel points at the old buffer
+
+    # ------------------------------------------------------------ step
+    def step_eager(self) -> None:
+        """Enqueue one decode step + advance on the current stream."""
+        st = torch.cuda.current_stream(self.device).cuda_stream
+        _lib.check(_lib.lib().qd_decode_step(ctypes.byref(self.desc), ctypes.c_void_p(st)), "qd_decode_step")
+        _lib.check(_lib.lib().qd_decode_advance(
+            ctypes.c_void_p(self.token.data_ptr()), ctypes.c_void_p(self.out_tokens.data_ptr()),
+            ctypes.c_void_p(self.step_counter.data_ptr()), ctypes.c_void_p(self.cache_position.data_ptr()),
+            ctypes.c_void_p(self.rope_position.data_ptr()), int(self.out_tokens.numel()),
+            ctypes.c_void_p(st)), "qd_decode_advance")
+
+    def run_phases(self, phases, first_layer: int = 0, n_layers: int | None = None) -> None:
+        """Enqueue only the named phases of the step (timing / profiling one kernel)."""
+        mask = 0
+        for p in phases:
+            mask |= _lib.PHASE[p]
+        n = len(self.w.layers) if n_layers is None else n_layers
+        st = torch.cuda.current_stream(self.device).cuda_stream
+        _lib.check(_lib.lib().qd_decode_step_phases(ctypes.byref(self.desc), int(first_layer), int(n), mask,
+                                                    ctypes.c_void_p(st)), "qd_decode_step_phases")
+
+    def capture(self) -> None:
+        """Capture one step into a HIP graph (decode + advance)."""
+        # Warm up once on a side stream so lazy initialisation is not captured,
+        # restoring the device state afterwards.
+        saved = [t.clone() for t in (self.token, self.cache_position, self.rope_position, self.step_counter)]
+        snap = self._snapshot_row()
+        side = torch.cuda.Stream(self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(side):
+            self.step_eager()
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        torch.cuda.synchronize(self.device)
+        for t, v in zip((self.token, self.cache_position, self.rope_position, self.step_counter), saved):
+            t.copy_(v)
+        self._restore_row(snap)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.step_eager()
+        torch.cuda.synchronize(self.device)
+        self.graph = g
+
+    def _snapshot_row(self):
+        pos = int(self.cache_position.item())
+        if not (0 <= pos < self.capacity):
+            return None
+        return pos, [(k[:, :, pos].clone(), v[:, :, pos].clone()) for k, v in zip(self.k_caches, self.v_caches)]
+
+    def _restore_row(self, snap) -> None:
+        if snap is None:
+            return
+        pos, rows = snap
+        for (k, v), (kr, vr) in zip(zip(self.k_caches, self.v_caches), rows):
+            k[:, :, pos].copy_(kr)
+            v[:, :, pos].copy_(vr)
+
+    def replay(self) -> None:
+        if self.graph is None:
+            self.capture()
+        self.graph.replay()
+
+    # ------------------------------------------------------------ generation
+    def decode(self, first_token: int, start_position: int, rope_delta: int, n_steps: int,
+               use_graph: bool = True) -> list:
+        """Greedy decode n_steps tokens after ``first_token`` at cache row start_position."""
+        if start_position + n_steps > self.capacity:
+            raise ValueError("static cache too small for the requested generation")
+        self.reserve_tokens(n_steps)
+        self.set_state(first_token, start_position, start_position + rope_delta)
+        self.step_counter.zero_()
+        if use_graph and self.graph is None:
+            self.capture()
+        for _ in range(n_steps):
+            if use_graph:
+                self.graph.replay()
+            else:
+                self.step_eager()
+        torch.cuda.synchronize(self.device)
+        return self.out_tokens[:n_steps].tolist()
+
+    # ------------------------------------------------------------ prefill
+    @torch.no_grad()
+    def prefill(self, prompt: MultimodalPrompt) -> int:
+        """Causal prefill of the prompt into the static cache (fp32 PyTorch-ROCm ops).
+
+        Follows the text-model loop of transformers Qwen3VLTextModel
+        (modeling_qwen3_vl.py:769-852) with M-RoPE positions [3, S]; returns
+        the argmax token of the last position.
+        """
+        s = self.shape
+        dev = self.device
+        S = prompt.length
+        if S > self.capacity:
+            raise ValueError("prompt longer than the static cache")
+        emb = torch.cat([prompt.vision_embeds.to(dev).float(),
+                         self.w.embed_tokens[prompt.text_ids.to(dev)].float()], 0)
+        pos = prompt.position_ids.to(dev)
+        inv = self.inv_freq
+        slot_stream = torch.zeros(s.head_dim // 2, dtype=torch.long)
+        for dim, off in ((1, 1), (2, 2)):
+            slot_stream[off: s.mrope_section[dim] * 3: 3] = dim
+        p = pos[slot_stream.to(dev), :].T.float()              # [S, d/2]
+        freqs = p * inv[None, :]
+        emb_f = torch.cat([freqs, freqs], -1)
+        cos, sin = emb_f.cos()[:, None, :], emb_f.sin()[:, None, :]
+        g = s.num_heads // s.num_kv_heads
+        causal = torch.full((S, S), float("-inf"), device=dev).triu(1)
+        h = emb
+        for li, lw in enumerate(self.w.layers):
+            xn = _rms(h, lw.input_layernorm_weight, s.rms_eps)
+            qkv = xn @ lw.qkv_weight.float().T
+            q = qkv[:, : s.q_size].view(S, s.num_heads, s.head_dim)
+            k = qkv[:, s.q_size: s.q_size + s.kv_size].view(S, s.num_kv_heads, s.head_dim)
+            v = qkv[:, s.q_size + s.kv_size:].view(S, s.num_kv_heads, s.head_dim)
+            q = _rope(_rms(q, lw.q_norm_weight, s.rms_eps), cos, sin)
+            k = _rope(_rms(k, lw.k_norm_weight, s.rms_eps), cos, sin)
+            self.k_caches[li][0, :, :S] = k.transpose(0, 1).half()
+            self.v_caches[li][0, :, :S] = v.transpose(0, 1).half()
+            qh = q.transpose(0, 1).contiguous()                                      # [Hq, S, D]
+            kh = k.transpose(0, 1).repeat_interleave(g, 0).contiguous()
+            vh = v.transpose(0, 1).repeat_interleave(g, 0).contiguous()
+            sc = torch.matmul(qh, kh.transpose(1, 2).contiguous()) * (s.head_dim ** -0.5) + causal
+            attn = torch.matmul(torch.softmax(sc, -1), vh)
+            o = attn.transpose(0, 1).reshape(S, s.q_size) @ lw.o_proj_weight.float().T
+            r = h + o
+            xn2 = _rms(r, lw.post_attn_layernorm_weight, s.rms_eps)
+            gu = xn2 @ lw.gate_up_weight.float().T
+            gate, up = gu[:, : s.intermediate], gu[:, s.intermediate:]
+            h = r + (torch.nn.functional.silu(gate) * up) @ lw.down_proj_weight.float().T
+        hn = _rms(h[-1], self.w.final_norm_weight, s.rms_eps)
+        logits = hn @ self.w.embed_tokens.float().T
+        return int(torch.argmax(logits))
+
+    def generate(self, prompt: MultimodalPrompt, n_tokens: int, use_graph: bool = True) -> list:
+        """Prefill + greedy decode; returns n_tokens ids (the first from the prefill)."""
+        first = self.prefill(prompt)
+        rest = self.decode(first, prompt.length, prompt.rope_delta, n_tokens - 1, use_graph) if n_tokens > 1 else []
+        return [first] + rest
+
+
+def _rms(x, w, eps):
+    xf = x.float()
+    return xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * w.float()
+
+
+def _rope(x, cos, sin):
+    h = x.shape[-1] // 2
+    rot = torch.cat([-x[..., h:], x[..., :h]], -1)
+    return x * cos + rot * sin
+
+
+def roofline_bytes_step(context_len: int, shape: Qwen3VLTextShape = QWEN3VL_2B) -> int:
+    """Algorithmic HBM bytes of one batch-1 decode step at KV length L: every
+    weight once, K/V[0:L] of every layer once, the embedding row and final norm."""
+    h, i, d = shape.hidden, shape.intermediate, shape.head_dim
+    layer_w = 2 * (shape.qkv_rows * h + h * shape.q_size + 3 * i * h) + 2 * (2 * h + 2 * d)
+    kv = 2 * 2 * shape.num_kv_heads * d * context_len
+    return shape.num_layers * (layer_w + kv) + 2 * shape.vocab * h + 2 * h + 2 * h
+
+
+__all__ = ["DecodeEngine", "rope_inv_freq", "roofline_bytes_step"]

@@ -1,0 +1,279 @@
+/*
+ * qwen3vl_decode.h — C ABI of the MI355X (gfx950) batch-1 decode path for the
+ * Qwen3-VL-2B text decoder.
+ *
+ * Every entry point:
+ *   - takes raw device pointers, sizes, scalars and a hipStream_t (passed as
+ *     void*; NULL = the null stream), never framework types;
+ *   - only borrows the pointers for the duration of the (asynchronous) launch
+ *     and allocates nothing on the hot path;
+ *   - returns an int status: QD_OK, a negative QD_ERR_* for a rejected
+ *     argument (nothing was launched), or a positive hipError_t from the
+ *     launch; qd_last_error() returns a message for the last failure on the
+ *     calling thread;
+ *   - launches on the given stream, never synchronises, and is safe inside HIP
+ *     stream capture (counters used for cross-workgroup hand-off are reset by
+ *     the kernels themselves, and no memset nodes are issued).
+ *
+ * Activation dtype codes (QD_F16 / QD_F32) select the storage type of
+ * activation vectors; weights and the KV cache are always fp16.  All
+ * arithmetic is fp32 (fp16 products accumulated in fp32).
+ *
+ * Each function cites the reference interface it replaces
+ * (/root/reference = wangxiyu191/AICASGC-2026).
+ */
+#ifndef QWEN3VL_DECODE_H
+#define QWEN3VL_DECODE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QD_OK 0
+#define QD_ERR_ARG (-1)          /* null pointer / bad scalar */
+#define QD_ERR_SHAPE (-2)        /* unsupported or inconsistent size */
+#define QD_ERR_WORKSPACE (-3)    /* workspace too small */
+
+#define QD_F16 0
+#define QD_F32 1
+
+/* Library version and last error message on this thread ("" if none). */
+int qd_version(void);
+const char* qd_last_error(void);
+
+/* Number of compute units of the current device (cached per device). */
+int qd_device_cu_count(void);
+
+/* ------------------------------------------------------------------ GEMV family */
+
+/* y[N] = W[N,K] x[K] (+ bias[N]).  fp16 x/bias/y.  Replaces
+ * nosplit_matvec_half (cuda_decode_gemv_ops/matvec.py:274-321 ->
+ * decode_gemv_kernel_launchers.cuh:367-445). bias may be NULL.  K % 8 == 0. */
+int qd_matvec_f16(const void* x, const void* W, const void* bias, void* y,
+                  int N, int K, void* stream);
+
+/* Split-K form of the same product: the K dimension is cut into split_k
+ * slices, each writes fp32 partials to scratch[split_k * N], and a reduce pass
+ * adds them in slice order (deterministic) + bias.  Replaces splitk_matvec
+ * (cuda_decode_gemv_ops/matvec.py:10-51).  scratch needs split_k*N floats. */
+int qd_splitk_matvec_f16(const void* x, const void* W, const void* bias,
+                         float* scratch, void* y, int N, int K, int split_k,
+                         void* stream);
+
+/* y = W (rmsnorm(x) * gamma) (+ bias), rmsnorm over K with eps.  fp16 I/O.
+ * Replaces fused_rmsnorm_qkv_half (cuda_decode_gemv_ops/fused.py:71-105 ->
+ * decode_gemv_kernel_fused.cuh:99-185). */
+int qd_rmsnorm_matvec_f16(const void* x, const void* gamma, const void* W,
+                          const void* bias, void* y, int N, int K, float eps,
+                          void* stream);
+
+/* Post-attention MLP of one layer, fp16 I/O:
+ *   r = residual + attn; xn = rmsnorm(r) * gamma;
+ *   hidden[j] = silu(W_gu[j] xn) * W_gu[I + j] xn   (j < I);
+ *   out = W_d hidden + r (+ bias).
+ * W_gu is [2I, H], W_d is [H, I].  Replaces fused_post_attn_mlp_softsync_half
+ * (cuda_decode_gemv_ops/fused.py:261-337 -> decode_gemv_kernel_fused.cuh:856-1076)
+ * and fused_post_attn_mlp_persistent_half (fused.py:198-259).  bias may be NULL. */
+int qd_post_attn_mlp_f16(const void* residual, const void* attn, const void* gamma,
+                         const void* W_gu, const void* W_d, const void* bias,
+                         void* hidden_out, void* out, int H, int I, float eps,
+                         void* stream);
+
+/* hidden = silu(W_gu[:I] x) * (W_gu[I:] x); out = W_d hidden (+ bias).  fp16
+ * I/O, bias may be NULL.  Replaces fused_gateup_silu_downproj_half and its
+ * persistent / softsync / gridsync / mega variants
+ * (cuda_decode_gemv_ops/fused.py:148-197, :668-892). */
+int qd_gateup_silu_down_f16(const void* x, const void* W_gu, const void* W_d,
+                            const void* bias, void* hidden_out, void* out, int H, int I,
+                            void* stream);
+
+/* residual_out = residual + x; y = W (rmsnorm(residual_out) * gamma) (+ bias).
+ * fp16 I/O, K % 512 == 0.  Replaces fused_add_rmsnorm_gateup_half
+ * (cuda_decode_gemv_ops/fused.py:12-68). */
+int qd_add_rmsnorm_matvec_f16(const void* residual, const void* x, const void* gamma,
+                              const void* W, const void* bias, void* residual_out, void* y,
+                              int N, int K, float eps, void* stream);
+
+/* y = W (silu(gate_up[:K]) * gate_up[K:]) (+ bias).  fp16 I/O, K % 512 == 0.
+ * Replaces fused_silu_downproj_half (cuda_decode_gemv_ops/fused.py:108-145). */
+int qd_silu_matvec_f16(const void* gate_up, const void* W, const void* bias, void* y,
+                       int N, int K, void* stream);
+
+/* Tied lm_head with fused argmax:
+ *   logits = W[V,H] (rmsnorm(h) * gamma)   (gamma == NULL: no norm)
+ *   token  = first index of max(logits)      (fp32 logits, torch.argmax order)
+ * h dtype h_dtype; logits_out (fp16, may be NULL); token_out int64[1].
+ * partial: workspace of qd_lm_head_workspace_bytes(V) bytes; its counter is
+ * self-resetting (zero it once at allocation).  Replaces FastLmHead.forward +
+ * torch.argmax (evaluation_wrapper.py:1227-1238, :952). */
+size_t qd_lm_head_workspace_bytes(int V);
+int qd_lm_head_argmax(const void* h, int h_dtype, const void* gamma, float eps,
+                      const void* W, int V, int H, void* logits_out,
+                      int64_t* token_out, void* workspace, void* stream);
+
+/* ------------------------------------------------------------------ small ops */
+
+/* Per-head RMSNorm (head_dim 128) + rotate-half RoPE on q and k, K_rot and V
+ * written into the static cache at row cache_position[0] (rows outside [0,T)
+ * are not written).  qkv_dtype is the dtype of q/k/v; q_out has q_out_dtype.
+ * q: [Hq,128] (row stride q_stride), k/v: [Hkv,128] (strides k_stride,
+ * v_stride).  Caches fp16 [Hkv, T, 128] with head stride cache_stride_h and
+ * row stride cache_stride_s (elements).
+ * RoPE source: cos/sin fp16 [128] when non-NULL (the reference's form);
+ * otherwise computed in fp32 from rope_pos[0..2] (int64 T/H/W positions, all
+ * three read) + the fp32 inv_freq[64] table and the mrope section triple.
+ * Replaces fused_q_rope_kv_cache_update (cuda_decode_small_ops.py:136-225 ->
+ * decode_small_ops_kernel.cu:115-182). */
+int qd_q_rope_kv_update(const void* q, const void* k, const void* v, int qkv_dtype,
+                        long q_stride, long k_stride, long v_stride,
+                        const void* q_weight, const void* k_weight, float eps,
+                        const void* cos, const void* sin,
+                        const int64_t* rope_pos, const float* inv_freq,
+                        int sec_t, int sec_h, int sec_w,
+                        void* q_out, int q_out_dtype,
+                        void* k_cache, void* v_cache, long cache_stride_h,
+                        long cache_stride_s, int T, const int64_t* cache_position,
+                        int Hq, int Hkv, void* stream);
+
+/* q/k per-head RMSNorm + RoPE without cache write, fp16 [M, H, 128] rows
+ * (cos/sin fp16 [M, 128]).  Replaces fused_qk_rms_norm_rope
+ * (cuda_decode_small_ops.py:70-133). */
+int qd_qk_norm_rope_f16(const void* q, const void* k, const void* q_weight,
+                        const void* k_weight, const void* cos, const void* sin,
+                        void* q_out, void* k_out, int M, int Hq, int Hkv,
+                        float eps, void* stream);
+
+/* out_sum = residual + x; out_norm = rmsnorm(out_sum) * weight; rows x cols fp16.
+ * Replaces fused_add_rms_norm (cuda_decode_small_ops.py:250-287). */
+int qd_add_rmsnorm_f16(const void* residual, const void* x, const void* weight,
+                       void* out_sum, void* out_norm, int rows, int cols,
+                       float eps, void* stream);
+
+/* out = rmsnorm(x) * weight; rows x cols fp16.  Replaces rms_norm
+ * (cuda_decode_small_ops.py:290-317). */
+int qd_rmsnorm_f16(const void* x, const void* weight, void* out, int rows, int cols,
+                   float eps, void* stream);
+
+/* out = silu(gate) * up, n fp16 elements.  Replaces fused_silu_mul
+ * (cuda_decode_small_ops.py:228-247). */
+int qd_silu_mul_f16(const void* gate, const void* up, void* out, long n, void* stream);
+
+/* out = a + b, n fp16 elements.  Replaces add (cuda_decode_small_ops.py:320-339). */
+int qd_add_f16(const void* a, const void* b, void* out, long n, void* stream);
+
+/* ------------------------------------------------------------------ attention */
+
+/* Split-KV GQA decode attention at batch 1, fused merge:
+ *   L = min(cache_position[0] + 1, T); out[h] = softmax(q_h K[:L]^T * scale) V[:L]
+ * for q head h on kv head h / (Hq/Hkv).  head_dim 128.  Each workgroup owns
+ * one (kv head, split) and serves every q head of the group, so K/V is read
+ * once.  Partials (normalised output + LSE) go to the workspace; the last
+ * workgroup of a kv head merges them and resets its counter.
+ * q: [Hq,128] with row stride q_stride (q_dtype); caches fp16 with head
+ * stride cache_stride_h and row stride cache_stride_s; out [Hq,128] out_dtype.
+ * Workspace: qd_attention_workspace_bytes(Hq, Hkv, n_split) bytes, zeroed
+ * once at allocation.  Replaces decode_attn_v4_cta_qhead_splitkv_fused
+ * (cuda_decode_attention.py:489-558 -> decode_attention_v4_kernel.cu:646-910)
+ * and decode_attn_v4_fused (cuda_decode_attention.py:305-392). */
+size_t qd_attention_workspace_bytes(int Hq, int Hkv, int n_split);
+int qd_attention_decode(const void* q, int q_dtype, long q_stride,
+                        const void* k_cache, const void* v_cache,
+                        long cache_stride_h, long cache_stride_s, int T,
+                        const int64_t* cache_position, float scale,
+                        void* out, int out_dtype, int Hq, int Hkv, int n_split,
+                        void* workspace, void* stream);
+
+/* The same computation as two launches: partials only (o_part fp32
+ * [Hq, n_split, 128], lse fp32 [Hq, n_split]), then the merge.  Replaces
+ * decode_attn_v4_splitkv (cuda_decode_attention.py:226-302). */
+int qd_attention_partial(const void* q, int q_dtype, long q_stride,
+                         const void* k_cache, const void* v_cache,
+                         long cache_stride_h, long cache_stride_s, int T,
+                         const int64_t* cache_position, float scale,
+                         float* o_part, float* lse, int Hq, int Hkv, int n_split,
+                         void* stream);
+int qd_attention_merge(const float* o_part, const float* lse, void* out, int out_dtype,
+                       int Hq, int n_split, void* stream);
+
+/* Default split count for a cache of capacity T (fixed per captured graph). */
+int qd_attention_default_splits(int T);
+
+/* ------------------------------------------------------------------ decode step */
+
+/* One decoder layer's weights (fused layout of optimized_layer.py:60-84). */
+typedef struct qd_layer_weights {
+  const void* qkv;             /* fp16 [Hq*D + 2*Hkv*D, H] */
+  const void* o_proj;          /* fp16 [H, Hq*D] */
+  const void* gate_up;         /* fp16 [2I, H] */
+  const void* down;            /* fp16 [H, I] */
+  const void* input_norm;      /* fp16 [H] */
+  const void* post_norm;       /* fp16 [H] */
+  const void* q_norm;          /* fp16 [D] */
+  const void* k_norm;          /* fp16 [D] */
+  void* k_cache;               /* fp16 [Hkv, T, D] */
+  void* v_cache;               /* fp16 [Hkv, T, D] */
+} qd_layer_weights;
+
+typedef struct qd_model_desc {
+  int num_layers, hidden, num_heads, num_kv_heads, head_dim, intermediate, vocab;
+  int capacity;                /* T: static-cache rows per layer */
+  float eps;
+  int sec_t, sec_h, sec_w;     /* M-RoPE sections */
+  const float* inv_freq;       /* device fp32 [D/2] */
+  const qd_layer_weights* layers;  /* host array [num_layers] */
+  const void* embed;           /* fp16 [V, H] (also the tied lm_head) */
+  const void* final_norm;      /* fp16 [H] */
+  /* step state (device) */
+  int64_t* token;              /* int64 [1]: input token, overwritten with the next token */
+  const int64_t* cache_position;   /* int64 [1] */
+  const int64_t* rope_position;    /* int64 [3]: T/H/W rope positions of this step */
+  void* logits_out;            /* fp16 [V] or NULL */
+  void* workspace;             /* qd_decode_workspace_bytes() bytes, zeroed once */
+  int attn_splits;             /* 0 = qd_attention_default_splits(capacity) */
+} qd_model_desc;
+
+size_t qd_decode_workspace_bytes(const qd_model_desc* d);
+
+/* Enqueue one full batch-1 decode step: embedding row of *token, 28 layers,
+ * final norm, lm_head, argmax -> *token.  The K/V of the new token are written
+ * at *cache_position.  Capturable into a hipGraph.  Replaces the captured step
+ * DecodeCudaGraphRunner._run_step (evaluation_wrapper.py:941-952) driving
+ * OptimizedDecoderLayer.forward (optimized_layer.py:108-469) x 28 and
+ * FastLmHead (evaluation_wrapper.py:1227-1238). */
+int qd_decode_step(const qd_model_desc* d, void* stream);
+
+/* The same step restricted to layers [first_layer, first_layer + n_layers)
+ * and to the phases in phase_mask (QD_PHASE_* bits); qd_decode_step is
+ * (0, num_layers, QD_PHASE_ALL).  Used to time or profile one phase of the
+ * chain in isolation, the role of the reference's *_profile entry points
+ * (cuda_decode_gemv_ops/profile.py). */
+#define QD_PHASE_EMBED 0x01u
+#define QD_PHASE_QKV 0x02u
+#define QD_PHASE_ROPE_KV 0x04u
+#define QD_PHASE_ATTN 0x08u
+#define QD_PHASE_O_PROJ 0x10u
+#define QD_PHASE_GATE_UP 0x20u
+#define QD_PHASE_DOWN 0x40u
+#define QD_PHASE_LM_HEAD 0x80u
+#define QD_PHASE_ALL 0xFFu
+int qd_decode_step_phases(const qd_model_desc* d, int first_layer, int n_layers,
+                          unsigned phase_mask, void* stream);
+
+/* Device-side end of a generation step (single thread):
+ *   out_tokens[*counter] = *token (when *counter < max_tokens); ++*counter;
+ *   ++*cache_position; ++rope_position[0..2].
+ * Captured after qd_decode_step it lets a hipGraph replay loop generate with
+ * no host writes; it replaces the host-side input staging of
+ * DecodeCudaGraphRunner._write_inputs (evaluation_wrapper.py:954-960). */
+int qd_decode_advance(const int64_t* token, int64_t* out_tokens, int64_t* counter,
+                      int64_t* cache_position, int64_t* rope_position, int max_tokens,
+                      void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QWEN3VL_DECODE_H */

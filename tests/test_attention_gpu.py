@@ -1,0 +1,120 @@
+"""Split-KV GQA decode attention parity on the GPU (config 2) against the
+CPU oracle's fp32 softmax attention.
+
+Bar: max |gpu - oracle| <= 2e-3 * max |oracle|.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from conftest import assert_close_rel
+from oracle import qwen3vl_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+SCALE = 128 ** -0.5
+
+
+def _run(fn, q, kc, vc, pos, cuda, **kw):
+    qd = q.to(cuda)
+    cp = torch.tensor([pos], dtype=torch.int64, device=cuda)
+    out = fn(qd, kc.to(cuda), vc.to(cuda), SCALE, 2, cp, **kw)
+    assert out is not None
+    assert out.shape == (1, 1, 16, 128)
+    return out.reshape(16, 128)
+
+
+@pytest.mark.parametrize("L", [256, 1024, 4096, 8192])
+@pytest.mark.parametrize("stale", [False, True])
+def test_attention_config2(cuda, L, stale):
+    import cuda_decode_attention as A
+    from qwen3vl_hip import synthetic as syn
+
+    cap = L + 320 if stale else L
+    q, kc, vc, pos = syn.attention_inputs(L, capacity=cap)
+    print(f"case attention L={L} T={cap}", flush=True)
+    out = _run(A.decode_attn_v4_cta_qhead_splitkv_fused, q, kc, vc, pos, cuda)
+    ref = O.decode_attention(q.reshape(16, 128), kc, vc, pos, SCALE)
+    assert_close_rel(out, ref, what=f"attention L={L} T={cap}")
+
+
+@pytest.mark.parametrize("split_k", [2, 4, 16, 64, 200])
+def test_attention_split_count_invariance(cuda, split_k):
+    import cuda_decode_attention as A
+    from qwen3vl_hip import synthetic as syn
+
+    q, kc, vc, pos = syn.attention_inputs(1024, capacity=1100)
+    ref = O.decode_attention(q.reshape(16, 128), kc, vc, pos, SCALE)
+    out = _run(A.decode_attn_v4_fused, q, kc, vc, pos, cuda, split_k=split_k)
+    assert_close_rel(out, ref, what=f"split_k={split_k}")
+
+
+def test_attention_partial_merge_matches_fused(cuda):
+    import cuda_decode_attention as A
+    from qwen3vl_hip import synthetic as syn
+
+    q, kc, vc, pos = syn.attention_inputs(4096)
+    fused = _run(A.decode_attn_v4_fused, q, kc, vc, pos, cuda)
+    two = _run(A.decode_attn_v4_splitkv, q, kc, vc, pos, cuda)
+    # same partials, same merge order: bit-identical
+    assert torch.equal(fused.cpu(), two.cpu())
+
+
+def test_attention_length_one_returns_v0(cuda):
+    import cuda_decode_attention as A
+    from qwen3vl_hip import synthetic as syn
+
+    q, kc, vc, _ = syn.attention_inputs(256, capacity=512)
+    out = _run(A.decode_attn_v4_cta_qhead_splitkv_fused, q, kc, vc, 0, cuda).cpu()
+    expect = vc[0, :, 0, :].repeat_interleave(2, 0)
+    assert torch.equal(out, expect)
+
+
+def test_attention_equal_keys_give_mean_of_values(cuda):
+    import cuda_decode_attention as A
+    from qwen3vl_hip import synthetic as syn
+
+    q, kc, vc, pos = syn.attention_inputs(1024)
+    kc[:] = kc[:, :, :1, :]  # every key identical -> uniform softmax
+    out = _run(A.decode_attn_v4_cta_qhead_splitkv_fused, q, kc, vc, pos, cuda)
+    expect = vc[0].float().mean(1).repeat_interleave(2, 0)
+    assert_close_rel(out, expect, what="equal keys")
+
+
+def test_attention_graph_replay_self_resets(cuda):
+    """Capture once, replay at several cache positions: the arrival counters
+    reset themselves, so every replay matches the eager result and the oracle."""
+    import cuda_decode_attention as A
+    from qwen3vl_hip import synthetic as syn
+
+    q, kc, vc, _ = syn.attention_inputs(2048)
+    qd, kd, vd = q.to(cuda), kc.to(cuda), vc.to(cuda)
+    cp = torch.tensor([100], dtype=torch.int64, device=cuda)
+    ws: dict = {}
+    A.decode_attn_v4_cta_qhead_splitkv_fused(qd, kd, vd, SCALE, 2, cp, workspace=ws)  # warm-up
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = A.decode_attn_v4_cta_qhead_splitkv_fused(qd, kd, vd, SCALE, 2, cp, workspace=ws)
+    for pos in (100, 2047, 5, 999, 1500):
+        cp.fill_(pos)
+        g.replay()
+        torch.cuda.synchronize()
+        got = out.reshape(16, 128).clone()
+        eager = A.decode_attn_v4_cta_qhead_splitkv_fused(qd, kd, vd, SCALE, 2, cp, workspace={})
+        torch.cuda.synchronize()
+        assert torch.equal(got, eager.reshape(16, 128))
+        assert_close_rel(got, O.decode_attention(q.reshape(16, 128), kc, vc, pos, SCALE), what=f"replay pos={pos}")
+
+
+def test_attention_unsupported_returns_none(cuda):
+    import cuda_decode_attention as A
+    from qwen3vl_hip import synthetic as syn
+
+    q, kc, vc, pos = syn.attention_inputs(256)
+    cp = torch.tensor([pos], dtype=torch.int64, device=cuda)
+    # head_dim 64 is not supported -> None (caller falls back)
+    assert A.decode_attn_v4_fused(q[..., :64].contiguous().to(cuda), kc[..., :64].contiguous().to(cuda),
+                                  vc[..., :64].contiguous().to(cuda), SCALE, 2, cp) is None

@@ -1,0 +1,89 @@
+"""One decoder layer, one decode step (config 0) on the GPU against the oracle.
+
+Two product paths are checked: the drop-in ``OptimizedDecoderLayer`` built
+from a transformers ``Qwen3VLTextDecoderLayer`` (fp16 activations between
+kernels, HF fp16 cos/sin), and the native decode step of the engine (fp32
+activations between kernels, device-side M-RoPE) on a 1-layer model.
+"""
+
+from __future__ import annotations
+
+import types
+
+import pytest
+import torch
+
+from conftest import assert_close_rel
+from oracle import qwen3vl_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _hf_layer(lw):
+    from transformers.models.qwen3_vl.configuration_qwen3_vl import Qwen3VLTextConfig
+    from transformers.models.qwen3_vl.modeling_qwen3_vl import Qwen3VLTextDecoderLayer
+
+    cfg = Qwen3VLTextConfig(hidden_size=2048, intermediate_size=6144, num_attention_heads=16,
+                            num_key_value_heads=8, head_dim=128, rms_norm_eps=1e-6, num_hidden_layers=1,
+                            vocab_size=1024)
+    cfg._attn_implementation = "sdpa"
+    layer = Qwen3VLTextDecoderLayer(cfg, 0)
+    a, m = layer.self_attn, layer.mlp
+    with torch.no_grad():
+        a.q_proj.weight.copy_(lw.qkv_weight[:2048].float())
+        a.k_proj.weight.copy_(lw.qkv_weight[2048:3072].float())
+        a.v_proj.weight.copy_(lw.qkv_weight[3072:].float())
+        a.o_proj.weight.copy_(lw.o_proj_weight.float())
+        a.q_norm.weight.copy_(lw.q_norm_weight.float())
+        a.k_norm.weight.copy_(lw.k_norm_weight.float())
+        m.gate_proj.weight.copy_(lw.gate_up_weight[:6144].float())
+        m.up_proj.weight.copy_(lw.gate_up_weight[6144:].float())
+        m.down_proj.weight.copy_(lw.down_proj_weight.float())
+        layer.input_layernorm.weight.copy_(lw.input_layernorm_weight.float())
+        layer.post_attention_layernorm.weight.copy_(lw.post_attn_layernorm_weight.float())
+    return layer
+
+
+def test_optimized_decoder_layer_config0(cuda):
+    import optimized_layer
+    from qwen3vl_hip import synthetic as syn
+
+    inp = syn.layer_step_inputs(seed=0, cache_position=512, capacity=640)
+    lw = inp.weights
+    layer = optimized_layer.OptimizedDecoderLayer(_hf_layer(lw)).to(cuda).half()
+    kc, vc = inp.k_cache.to(cuda), inp.v_cache.to(cuda)
+    cache = types.SimpleNamespace(layers=[types.SimpleNamespace(keys=kc, values=vc, is_initialized=True,
+                                                                max_cache_len=kc.shape[2])])
+    cos, sin = O.mrope_cos_sin(torch.full((3, 1), inp.rope_position, dtype=torch.int64))
+    cos16, sin16 = cos.half().view(1, 1, 128), sin.half().view(1, 1, 128)
+    cp = torch.tensor([inp.cache_position], dtype=torch.int64, device=cuda)
+    out = layer(inp.hidden.to(cuda), (cos16.to(cuda), sin16.to(cuda)), past_key_values=cache, cache_position=cp)
+    assert out.shape == (1, 1, 2048) and out.dtype == torch.float16
+    kc_ref, vc_ref = inp.k_cache.clone(), inp.v_cache.clone()
+    ref = O.decode_layer(lw.tensors(), inp.hidden.reshape(-1), kc_ref, vc_ref, inp.cache_position,
+                         cos16.float().reshape(128), sin16.float().reshape(128))
+    assert_close_rel(out.reshape(-1), ref, what="OptimizedDecoderLayer decode step")
+    assert_close_rel(kc[0, :, 512].cpu(), kc_ref[0, :, 512].float(), what="layer K write")
+    assert torch.equal(kc[0, :, :512].cpu(), inp.k_cache[0, :, :512])
+
+
+def test_engine_one_layer_step_config0(cuda):
+    """Native step on a 1-layer model: logits and argmax against the oracle."""
+    from qwen3vl_hip import synthetic as syn
+    from qwen3vl_hip.engine import DecodeEngine
+
+    w = syn.model_weights(0, num_layers=1)
+    eng = DecodeEngine(w, capacity=640, keep_logits=True)
+    inp = syn.layer_step_inputs(seed=0, cache_position=512, capacity=640)
+    eng.k_caches[0].copy_(inp.k_cache)
+    eng.v_caches[0].copy_(inp.v_cache)
+    token = 4242
+    toks = eng.decode(token, 512, 0, 1, use_graph=False)
+    kc_ref, vc_ref = inp.k_cache.clone(), inp.v_cache.clone()
+    cos, sin = O.mrope_cos_sin(torch.full((3, 1), 512, dtype=torch.int64))
+    h = O.decode_layer(w.layers[0].tensors(), w.embed_tokens[token], kc_ref, vc_ref, 512, cos[0], sin[0])
+    logits, tok = O.lm_head_argmax(h, w.final_norm_weight, w.embed_tokens, 1e-6)
+    assert_close_rel(eng.logits.cpu(), logits, what="engine 1-layer logits")
+    assert_close_rel(eng.k_caches[0][0, :, 512].cpu(), kc_ref[0, :, 512].float(), what="engine K write")
+    print(f"engine token {toks[0]} oracle {tok} margin {O.top2_margin(logits):.4g}", flush=True)
+    assert toks[0] == tok
