@@ -411,6 +411,17 @@ size_t qd_decode_workspace_bytes(const qd_model_desc* d) {
   return total;
 }
 
+int qd_decode_workspace_layout(const qd_model_desc* d, size_t* offsets, int n) {
+  QD_REQUIRE(d && d->workspace, QD_ERR_ARG, "descriptor without workspace");
+  StepBuffers b;
+  size_t total = 0;
+  step_layout(d, splits_of(d), &b, &total);
+  const char* base = reinterpret_cast<const char*>(d->workspace);
+  const void* bufs[6] = {b.x, b.qkv, b.q_rot, b.attn, b.r, b.hidden};
+  for (int i = 0; i < n && i < 6; ++i) offsets[i] = (size_t)(reinterpret_cast<const char*>(bufs[i]) - base);
+  return 6;
+}
+
 int qd_decode_step(const qd_model_desc* d, void* stream) {
   return qd_decode_step_phases(d, 0, d ? d->num_layers : 0, QD_PHASE_ALL, stream);
 }

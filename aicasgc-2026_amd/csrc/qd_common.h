@@ -18,6 +18,7 @@ constexpr int kWave = 64;
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------- conversions
 
@@ -72,14 +73,15 @@ template <>
 __device__ __forceinline__ void load_act8<uint16_t>(const uint16_t* p, long i, float* o) {
   unpack8(ld16(p + i), o);
 }
+// fp32 activations are moved as float4 vectors.  (Do not bit-cast individual
+// elements of an integer ext-vector to float here: clang folds every
+// __builtin_bit_cast(float, v.y / v.z / v.w) to element x for this pattern.)
 template <>
 __device__ __forceinline__ void load_act8<float>(const float* p, long i, float* o) {
-  const u32x4 a = ld16(p + i);
-  const u32x4 b = ld16(p + i + 4);
-  o[0] = __builtin_bit_cast(float, a.x); o[1] = __builtin_bit_cast(float, a.y);
-  o[2] = __builtin_bit_cast(float, a.z); o[3] = __builtin_bit_cast(float, a.w);
-  o[4] = __builtin_bit_cast(float, b.x); o[5] = __builtin_bit_cast(float, b.y);
-  o[6] = __builtin_bit_cast(float, b.z); o[7] = __builtin_bit_cast(float, b.w);
+  const f32x4 a = *reinterpret_cast<const f32x4*>(p + i);
+  const f32x4 b = *reinterpret_cast<const f32x4*>(p + i + 4);
+  o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+  o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
 }
 
 template <typename T>
@@ -107,13 +109,8 @@ __device__ __forceinline__ void store_act8<uint16_t>(uint16_t* p, long i, const 
 }
 template <>
 __device__ __forceinline__ void store_act8<float>(float* p, long i, const float* v) {
-  u32x4 a, b;
-  a.x = __builtin_bit_cast(unsigned, v[0]); a.y = __builtin_bit_cast(unsigned, v[1]);
-  a.z = __builtin_bit_cast(unsigned, v[2]); a.w = __builtin_bit_cast(unsigned, v[3]);
-  b.x = __builtin_bit_cast(unsigned, v[4]); b.y = __builtin_bit_cast(unsigned, v[5]);
-  b.z = __builtin_bit_cast(unsigned, v[6]); b.w = __builtin_bit_cast(unsigned, v[7]);
-  *reinterpret_cast<u32x4*>(p + i) = a;
-  *reinterpret_cast<u32x4*>(p + i + 4) = b;
+  *reinterpret_cast<f32x4*>(p + i) = f32x4{v[0], v[1], v[2], v[3]};
+  *reinterpret_cast<f32x4*>(p + i + 4) = f32x4{v[4], v[5], v[6], v[7]};
 }
 
 // ---------------------------------------------------------------- cross-lane

@@ -59,8 +59,9 @@ def fused_add_rmsnorm_gateup_half(residual: torch.Tensor, x: torch.Tensor, norm_
     res_out = _reuse(workspace, "fused_add_rmsnorm_gateup", "residual_out", (k,), residual.dtype, residual.device)
     out = _reuse(workspace, "fused_add_rmsnorm_gateup", "out", (n,), residual.dtype, residual.device)
     b = _vec(bias) if bias is not None else None
-    _check(_load_ext().qd_add_rmsnorm_matvec_f16(_p(_vec(residual)), _p(_vec(x)), _p(_vec(norm_weight)), _p(w),
-                                                 _p(b), _p(res_out), _p(out), n, k, float(eps), _stream(x)), name)
+    rv, xv, gv = _vec(residual), _vec(x), _vec(norm_weight)   # held until the launch is enqueued
+    _check(_load_ext().qd_add_rmsnorm_matvec_f16(_p(rv), _p(xv), _p(gv), _p(w), _p(b), _p(res_out), _p(out), n, k,
+                                                 float(eps), _stream(x)), name)
     return res_out.view_as(residual), out.view(*residual.shape[:-1], n)
 
 
@@ -91,7 +92,8 @@ def _gateup_silu_down(name: str, x, gate_up_weight, down_proj_weight, bias, work
     hidden = _reuse(workspace, kind, "hidden_out", (i,), x.dtype, x.device)
     out = _reuse(workspace, kind, "out", (n,), x.dtype, x.device)
     b = _vec(bias) if bias is not None else None
-    _check(_load_ext().qd_gateup_silu_down_f16(_p(_vec(x)), _p(wgu), _p(wd), _p(b), _p(hidden), _p(out), h, i,
+    xv = _vec(x)
+    _check(_load_ext().qd_gateup_silu_down_f16(_p(xv), _p(wgu), _p(wd), _p(b), _p(hidden), _p(out), h, i,
                                                _stream(x)), name)
     return hidden.view(*x.shape[:-1], i), out.view(*x.shape[:-1], n)
 
@@ -143,9 +145,9 @@ def _post_attn_mlp(name, residual, attn_output, norm_weight, gate_up_weight, dow
     hidden = _reuse(workspace, kind, "hidden_out", (i,), residual.dtype, residual.device)
     out = _reuse(workspace, kind, "out", (n,), residual.dtype, residual.device)
     b = _vec(bias) if bias is not None else None
-    _check(_load_ext().qd_post_attn_mlp_f16(_p(_vec(residual)), _p(_vec(attn_output)), _p(_vec(norm_weight)),
-                                            _p(wgu), _p(wd), _p(b), _p(hidden), _p(out), h, i, float(eps),
-                                            _stream(residual)), name)
+    rv, av, gv = _vec(residual), _vec(attn_output), _vec(norm_weight)   # held until the launch is enqueued
+    _check(_load_ext().qd_post_attn_mlp_f16(_p(rv), _p(av), _p(gv), _p(wgu), _p(wd), _p(b), _p(hidden), _p(out), h,
+                                            i, float(eps), _stream(residual)), name)
     return hidden.view(*residual.shape[:-1], i), out.view(*residual.shape[:-1], n)
 
 

@@ -41,8 +41,9 @@ def fused_qk_rms_norm_rope(q, k, q_weight, k_weight, eps: float, cos, sin):
         raise RuntimeError("fused_qk_rms_norm_rope expects cos/sin shaped [B, S, 128]")
     m = q_in.shape[0] * q_in.shape[1]
     q_out, k_out = torch.empty_like(q_in), torch.empty_like(k_in)
+    qw, kw = q_weight.contiguous(), k_weight.contiguous()   # held until the launch is enqueued
     _lib.check(_load_ext().qd_qk_norm_rope_f16(
-        _lib.ptr(q_in), _lib.ptr(k_in), _lib.ptr(q_weight.contiguous()), _lib.ptr(k_weight.contiguous()),
+        _lib.ptr(q_in), _lib.ptr(k_in), _lib.ptr(qw), _lib.ptr(kw),
         _lib.ptr(cos_in), _lib.ptr(sin_in), _lib.ptr(q_out), _lib.ptr(k_out), m, q_in.shape[2], k_in.shape[2],
         float(eps), _lib.stream(q.device)), "fused_qk_rms_norm_rope")
     return q_out, k_out
@@ -82,15 +83,17 @@ def fused_q_rope_kv_cache_update(q, k, v, q_weight, k_weight, eps: float, cos, s
     if (k_cache.stride(-1) != 1 or v_cache.stride(-1) != 1 or k_cache.stride(1) != v_cache.stride(1)
             or k_cache.stride(2) != v_cache.stride(2) or k_cache.shape != v_cache.shape):
         raise RuntimeError("k_cache/v_cache must share one [1, KVH, T, D] layout with unit last stride")
+    # contiguous copies are bound to locals so they outlive the asynchronous launch's enqueue
     q_in, k_in, v_in = q.contiguous(), k.contiguous(), v.contiguous()
+    qw, kw = q_weight.contiguous(), k_weight.contiguous()
+    cos_in, sin_in, cp = cos.contiguous(), sin.contiguous(), cache_position.contiguous()
     q_out = torch.empty((1, 1, q.shape[2], 128), dtype=q.dtype, device=q.device)
     _lib.check(_load_ext().qd_q_rope_kv_update(
         _lib.ptr(q_in), _lib.ptr(k_in), _lib.ptr(v_in), _lib.QD_F16, 128, 128, 128,
-        _lib.ptr(q_weight.contiguous()), _lib.ptr(k_weight.contiguous()), float(eps),
-        _lib.ptr(cos.contiguous()), _lib.ptr(sin.contiguous()), None, None, 24, 20, 20,
+        _lib.ptr(qw), _lib.ptr(kw), float(eps), _lib.ptr(cos_in), _lib.ptr(sin_in), None, None, 24, 20, 20,
         _lib.ptr(q_out), _lib.QD_F16, _lib.ptr(k_cache), _lib.ptr(v_cache), k_cache.stride(1), k_cache.stride(2),
-        k_cache.shape[2], _lib.ptr(cache_position.contiguous()), q.shape[2], k.shape[2],
-        _lib.stream(q.device)), "fused_q_rope_kv_cache_update")
+        k_cache.shape[2], _lib.ptr(cp), q.shape[2], k.shape[2], _lib.stream(q.device)),
+        "fused_q_rope_kv_cache_update")
     return q_out
 
 
@@ -119,7 +122,8 @@ def fused_add_rms_norm(residual, x, weight, eps: float):
     cols = r.shape[-1]
     rows = r.numel() // cols
     out_sum, out_norm = torch.empty_like(r), torch.empty_like(r)
-    _lib.check(_load_ext().qd_add_rmsnorm_f16(_lib.ptr(r), _lib.ptr(xi), _lib.ptr(weight.contiguous()),
+    wc = weight.contiguous()
+    _lib.check(_load_ext().qd_add_rmsnorm_f16(_lib.ptr(r), _lib.ptr(xi), _lib.ptr(wc),
                                               _lib.ptr(out_sum), _lib.ptr(out_norm), rows, cols, float(eps),
                                               _lib.stream(r.device)), "fused_add_rms_norm")
     return out_sum, out_norm
@@ -134,7 +138,8 @@ def rms_norm(x, weight, eps: float):
     xi = x.contiguous()
     cols = xi.shape[-1]
     out = torch.empty_like(xi)
-    _lib.check(_load_ext().qd_rmsnorm_f16(_lib.ptr(xi), _lib.ptr(weight.contiguous()), _lib.ptr(out),
+    wc = weight.contiguous()
+    _lib.check(_load_ext().qd_rmsnorm_f16(_lib.ptr(xi), _lib.ptr(wc), _lib.ptr(out),
                                           xi.numel() // cols, cols, float(eps), _lib.stream(xi.device)), "rms_norm")
     return out
 

@@ -58,6 +58,7 @@ _SIGS = {
     "qd_attention_merge": (c_int, [P, P, P, c_int, c_int, c_int, P]),
     "qd_attention_default_splits": (c_int, [c_int]),
     "qd_decode_workspace_bytes": (c_size_t, [P]),
+    "qd_decode_workspace_layout": (c_int, [P, POINTER(c_size_t), c_int]),
     "qd_decode_step": (c_int, [P, P]),
     "qd_decode_step_phases": (c_int, [P, c_int, c_int, ctypes.c_uint, P]),
     "qd_decode_advance": (c_int, [P, P, P, P, P, c_int, P]),

@@ -127,6 +127,16 @@ class DecodeEngine:
         _lib.check(_lib.lib().qd_decode_step_phases(ctypes.byref(self.desc), int(first_layer), int(n), mask,
                                                     ctypes.c_void_p(st)), "qd_decode_step_phases")
 
+    def buffers(self) -> dict:
+        """fp32 views of the activation vectors the step hands between kernels."""
+        offs = (ctypes.c_size_t * 6)()
+        _lib.lib().qd_decode_workspace_layout(ctypes.byref(self.desc), offs, 6)
+        s = self.shape
+        sizes = {"x": s.hidden, "qkv": s.qkv_rows, "q_rot": s.q_size, "attn": s.q_size, "r": s.hidden,
+                 "hidden": s.intermediate}
+        return {name: self.workspace[o: o + 4 * n].view(torch.float32)
+                for (name, n), o in zip(sizes.items(), offs)}
+
     def capture(self) -> None:
         """Capture one step into a HIP graph (decode + advance)."""
         # Warm up once on a side stream so lazy initialisation is not captured,

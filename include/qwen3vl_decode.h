@@ -237,6 +237,13 @@ typedef struct qd_model_desc {
 
 size_t qd_decode_workspace_bytes(const qd_model_desc* d);
 
+/* Byte offsets inside the step workspace of the fp32 activation vectors the
+ * step hands between kernels, in this order: residual stream x [H], qkv,
+ * rotated q [Hq*D], attention output [Hq*D], post-attention residual r [H],
+ * SiLU(gate)*up [I].  Writes min(n, 6) offsets; returns how many exist (6).
+ * For inspection and parity tests of individual phases. */
+int qd_decode_workspace_layout(const qd_model_desc* d, size_t* offsets, int n);
+
 /* Enqueue one full batch-1 decode step: embedding row of *token, 28 layers,
  * final norm, lm_head, argmax -> *token.  The K/V of the new token are written
  * at *cache_position.  Capturable into a hipGraph.  Replaces the captured step

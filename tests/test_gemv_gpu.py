@@ -186,11 +186,11 @@ def test_lm_head_argmax_tie_takes_first_index(cuda):
     x = w[31337].float() / w[31337].float().norm()
     for j in (40000, 45001, 49999, 31338):
         w[j] = w[31337]
-    xs = x.half().to(cuda)
+    xs, wd = x.half().to(cuda), w.to(cuda)   # device copies stay referenced across the launch
     tok = torch.empty(1, dtype=torch.int64, device=cuda)
     lib = _lib.lib()
     wsp = torch.zeros(int(lib.qd_lm_head_workspace_bytes(V)), dtype=torch.uint8, device=cuda)
-    _lib.check(lib.qd_lm_head_argmax(_lib.ptr(xs), _lib.QD_F16, None, 1e-6, _lib.ptr(w.to(cuda)), V, H, None,
+    _lib.check(lib.qd_lm_head_argmax(_lib.ptr(xs), _lib.QD_F16, None, 1e-6, _lib.ptr(wd), V, H, None,
                                      _lib.ptr(tok), _lib.ptr(wsp), _lib.stream()), "lm_head")
     assert int(tok.item()) == 31337
     assert int(torch.argmax(x.half().float() @ w.float().T)) == 31337

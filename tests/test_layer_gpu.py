@@ -67,6 +67,52 @@ def test_optimized_decoder_layer_config0(cuda):
     assert torch.equal(kc[0, :, :512].cpu(), inp.k_cache[0, :, :512])
 
 
+def test_engine_phases_match_oracle_intermediates(cuda):
+    """Each phase of the native step, run alone, against the oracle's value of
+    the vector that phase produces (fp32 buffers, so the bar is tighter)."""
+    from qwen3vl_hip import synthetic as syn
+    from qwen3vl_hip.engine import DecodeEngine
+
+    w = syn.model_weights(0, num_layers=1)
+    eng = DecodeEngine(w, capacity=640)
+    inp = syn.layer_step_inputs(seed=0, cache_position=512, capacity=640)
+    eng.k_caches[0].copy_(inp.k_cache)
+    eng.v_caches[0].copy_(inp.v_cache)
+    token = 4242
+    eng.set_state(token, 512, 512)
+    lw = w.layers[0].tensors()
+    x0 = w.embed_tokens[token].float()
+    qkv = O.gemv(O.rms_norm(x0, lw["input_layernorm_weight"], 1e-6), lw["qkv_weight"])
+    kc, vc = inp.k_cache.clone(), inp.v_cache.clone()
+    cos, sin = O.mrope_cos_sin(torch.full((3, 1), 512, dtype=torch.int64))
+    q_rot = O.q_rope_kv_update(qkv[:2048].view(16, 128), qkv[2048:3072].view(8, 128), qkv[3072:].view(8, 128),
+                               lw["q_norm_weight"], lw["k_norm_weight"], 1e-6, cos[0], sin[0], kc, vc, 512)
+    attn = O.decode_attention(q_rot, kc, vc, 512, 128 ** -0.5)
+    hid, out, r = O.post_attn_mlp(x0, O.gemv(attn.reshape(-1), lw["o_proj_weight"]),
+                                  lw["post_attn_layernorm_weight"], lw["gate_up_weight"], lw["down_proj_weight"],
+                                  None, 1e-6)
+    b = eng.buffers()
+    expect = [("embed", "x", x0), ("qkv", "qkv", qkv), ("rope_kv", "q_rot", q_rot.reshape(-1)),
+              ("attn", "attn", attn.reshape(-1)), ("o_proj", "r", r), ("gate_up", "hidden", hid),
+              ("down", "x", out)]
+    for phase, buf, ref in expect:
+        print(f"case engine phase {phase}", flush=True)
+        eng.run_phases([phase])
+        torch.cuda.synchronize()
+        assert_close_rel(b[buf].cpu(), ref, rel=1e-4 if phase in ("embed", "qkv") else REL_ENGINE,
+                         what=f"engine phase {phase}")
+        if phase == "rope_kv":
+            # fp32 K/V rounded to the fp16 cache: equal up to one fp16 rounding step
+            assert_close_rel(eng.k_caches[0][0, :, 512].cpu(), kc[0, :, 512].float(), what="engine K row")
+            assert_close_rel(eng.v_caches[0][0, :, 512].cpu(), vc[0, :, 512].float(), what="engine V row")
+            mask = torch.ones(640, dtype=torch.bool)
+            mask[512] = False
+            assert torch.equal(eng.k_caches[0][0, :, mask].cpu(), inp.k_cache[0, :, mask])
+
+
+REL_ENGINE = 2e-3
+
+
 def test_engine_one_layer_step_config0(cuda):
     """Native step on a 1-layer model: logits and argmax against the oracle."""
     from qwen3vl_hip import synthetic as syn

@@ -83,9 +83,10 @@ def test_q_rope_position_mode_fp32(cuda):
     q_out = torch.empty(16, 128, dtype=torch.float32, device=cuda)
     inv = rope_inv_freq().to(cuda)
     rp, cp = pos3.to(cuda), torch.tensor([cpos], device=cuda)
+    qw_d, kw_d = qw.to(cuda), kw.to(cuda)   # device copies stay referenced across the launch
     _lib.check(_lib.lib().qd_q_rope_kv_update(
-        _lib.ptr(qkv), _lib.ptr(qkv[2048:]), _lib.ptr(qkv[3072:]), _lib.QD_F32, 128, 128, 128, _lib.ptr(qw.to(cuda)),
-        _lib.ptr(kw.to(cuda)), 1e-6, None, None, _lib.ptr(rp), _lib.ptr(inv), 24, 20, 20, _lib.ptr(q_out),
+        _lib.ptr(qkv), _lib.ptr(qkv[2048:]), _lib.ptr(qkv[3072:]), _lib.QD_F32, 128, 128, 128, _lib.ptr(qw_d),
+        _lib.ptr(kw_d), 1e-6, None, None, _lib.ptr(rp), _lib.ptr(inv), 24, 20, 20, _lib.ptr(q_out),
         _lib.QD_F32, _lib.ptr(kc), _lib.ptr(vc), T * 128, 128, T, _lib.ptr(cp), 16, 8, _lib.stream()), "rope")
     kc_ref = torch.zeros(1, 8, T, 128, dtype=torch.float16)
     vc_ref = torch.zeros_like(kc_ref)
