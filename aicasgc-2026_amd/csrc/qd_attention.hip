@@ -9,10 +9,18 @@
 // element is read from HBM exactly once (the reference's q-head split-KV kernel
 // reads each kv head once per q head, decode_attention_v4_kernel.cu:646-910).
 //
-// Online softmax per slot in fp32 (one exp per position and head), slot
-// partials merged through LDS into a per-split (normalised output, LSE) pair;
-// splits are merged either by the last workgroup of the kv head to arrive
-// (self-resetting arrival counter) or by a separate merge kernel.
+// Online softmax per slot in fp32 (one exp per position and head); the 16 slot
+// states are merged through LDS into one (normalised output, LSE) pair per
+// split.  A second, tiny kernel merges the splits.  No workgroup waits on
+// another inside a launch, so no device-scope fence is needed: the partials
+// become visible to the merge kernel at the launch boundary.
+//
+// The fused variant (native decode step) also performs the decode step's q/k
+// head RMSNorm + M-RoPE and the static-cache write in its prologue: every
+// workgroup of a kv head recomputes the rotated q, k and v of the new token
+// from the raw qkv vector (4 heads x 128 values), the workgroup whose split
+// holds cache_position writes K/V to the cache, and the new position is read
+// from LDS instead of the cache, so no workgroup depends on another's store.
 
 #include <math.h>
 
@@ -23,33 +31,80 @@ namespace qd {
 
 namespace {
 constexpr int kD = 128;
+constexpr int kHalf = 64;
 constexpr int kSlots = 16;
-constexpr int kUnroll = 4;
+constexpr int kUnroll = 8;
 }  // namespace
 
-template <int G, typename TO>
-__device__ __forceinline__ void merge_splits(const AttnArgs& a, int kvh) {
-  TO* out = reinterpret_cast<TO*>(a.out);
-  for (int t = threadIdx.x; t < G * kD; t += blockDim.x) {
-    const int h = kvh * G + t / kD;
-    const int d = t % kD;
-    const float* lse = a.lse + (long)h * a.n_split;
-    float M = -INFINITY;
-    for (int s = 0; s < a.n_split; ++s) M = fmaxf(M, lse[s]);
-    float num = 0.f, den = 0.f;
-    if (M != -INFINITY) {
-      for (int s = 0; s < a.n_split; ++s) {
-        const float w = __expf(lse[s] - M);
-        den += w;
-        num = __builtin_fmaf(w, a.o_part[((long)h * a.n_split + s) * kD + d], num);
-      }
+// RMSNorm(head) * w then rotate-half RoPE on the pair (j, j + 64) held by lane j.
+__device__ __forceinline__ void head_norm_rope(float x0, float x1, const uint16_t* w, float eps, float c, float s,
+                                               int j, float& o0, float& o1) {
+  const float ss = wave_sum(x0 * x0 + x1 * x1);
+  const float rstd = rsqrtf(ss / (float)kD + eps);
+  const float n0 = (x0 * rstd) * h2f(w[j]);
+  const float n1 = (x1 * rstd) * h2f(w[j + kHalf]);
+  o0 = n0 * c - n1 * s;
+  o1 = n1 * c + n0 * s;
+}
+
+// cos/sin of frequency slot j from the (T, H, W) rope positions (interleaved
+// M-RoPE: j % 3 == 1 (j < 3*sec_h) -> H, j % 3 == 2 (j < 3*sec_w) -> W, else T).
+__device__ __forceinline__ void mrope_cs(const int64_t* pos3, const float* inv_freq, int sec_h, int sec_w, int j,
+                                         float& c, float& s) {
+  int stream = 0;
+  if (j % 3 == 1 && j < 3 * sec_h) stream = 1;
+  else if (j % 3 == 2 && j < 3 * sec_w) stream = 2;
+  const float f = (float)pos3[stream] * inv_freq[j];
+  sincosf(f, &s, &c);
+}
+
+// Online-softmax update of one slot with kUnroll positions t, t+16, ...; a
+// position >= t1 contributes nothing.  Control flow is uniform across the wave
+// (invalid positions are masked with selects, their K/V registers are zero),
+// so the DPP row sums never run under divergent execution masks.
+template <int G>
+__device__ __forceinline__ void online_softmax_batch(const u32x4 (&kk)[kUnroll], const u32x4 (&vv)[kUnroll], int t,
+                                                     int t1, const float (&q)[G][8], float scale, float (&m)[G],
+                                                     float (&l)[G], float (&acc)[G][8]) {
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const bool valid = t + u * kSlots < t1;
+    float vf[8];
+    unpack8(vv[u], vf);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float s = row16_sum(dot8(kk[u], q[g], 0.f)) * scale;
+      const float dlt = s - m[g];
+      const float e = __expf(-fabsf(dlt));
+      const bool up = valid && dlt > 0.f;
+      const float c = up ? e : 1.f;                      // rescale of the running sums
+      const float p = valid ? (up ? 1.f : e) : 0.f;      // weight of this position
+      m[g] = up ? s : m[g];
+      l[g] = __builtin_fmaf(l[g], c, p);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[g][i] = __builtin_fmaf(acc[g][i], c, p * vf[i]);
     }
-    store_act(out, (long)h * kD + d, den > 0.f ? num / den : 0.f);
   }
 }
 
-template <int G, typename TQ, typename TO>
-__global__ __launch_bounds__(256) void attn_split_kernel(const AttnArgs a, const int fused_merge) {
+// K/V rows of positions t, t+16, ... into registers; rows >= t1 (and the new
+// position in the fused variant, patched from LDS by the caller) read as zero.
+__device__ __forceinline__ void load_kv_batch(const uint16_t* kb, const uint16_t* vb, long stride_s, int t, int t1,
+                                              long skip, u32x4 (&kk)[kUnroll], u32x4 (&vv)[kUnroll]) {
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int tt = t + u * kSlots;
+    kk[u] = u32x4{0u, 0u, 0u, 0u};
+    vv[u] = u32x4{0u, 0u, 0u, 0u};
+    if (tt < t1 && tt != skip) {
+      kk[u] = ld_stream(kb + (long)tt * stride_s);
+      vv[u] = ld_stream(vb + (long)tt * stride_s);
+    }
+  }
+}
+
+template <int G, typename TQ, bool FUSED_ROPE>
+__global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
   const int kvh = blockIdx.x / a.n_split;
   const int split = blockIdx.x % a.n_split;
   const int slot = threadIdx.x >> 4;
@@ -63,10 +118,69 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const AttnArgs a, const
   const int t0 = split * chunk;
   const int t1 = min(t0 + chunk, L);
 
+  // The cache rows do not depend on the prologue: the first batch of K/V loads
+  // is issued before it (the new position, if in this batch, is patched in from
+  // LDS afterwards).
+  const uint16_t* kb = a.k + (long)kvh * a.stride_h + dl;
+  const uint16_t* vb = a.v + (long)kvh * a.stride_h + dl;
+  // The wave's four slots advance together (trip count uniform per wave).
+  const int wave_t0 = t0 + (threadIdx.x / kWave) * 4;
+  const int row_off = slot - (threadIdx.x / kWave) * 4;
+  const long skip = FUSED_ROPE ? pos : -1;
+  u32x4 kk[kUnroll], vv[kUnroll];
+  load_kv_batch(kb, vb, a.stride_s, wave_t0 + row_off, t1, skip, kk, vv);
+
+  __shared__ float s_q[G][kD];
+  __shared__ __align__(16) uint16_t s_kv[2][kD];   // new token's K_rot and V, fp16 as cached
+  if constexpr (FUSED_ROPE) {
+    const int w = threadIdx.x / kWave;
+    const int j = lane_id();
+    const TQ* qkv = reinterpret_cast<const TQ*>(a.qkv);
+    float c, s;
+    mrope_cs(a.rope_pos, a.inv_freq, a.sec_h, a.sec_w, j, c, s);
+    for (int item = w; item < G + 2; item += 4) {
+      if (item < G) {
+        const TQ* src = qkv + (long)(kvh * G + item) * kD;
+        float o0, o1;
+        head_norm_rope(load_act(src, j), load_act(src, j + kHalf), a.q_weight, a.eps, c, s, j, o0, o1);
+        s_q[item][j] = o0;
+        s_q[item][j + kHalf] = o1;
+      } else if (item == G) {
+        const TQ* src = qkv + (long)a.Hq * kD + (long)kvh * kD;
+        float o0, o1;
+        head_norm_rope(load_act(src, j), load_act(src, j + kHalf), a.k_weight, a.eps, c, s, j, o0, o1);
+        s_kv[0][j] = f2h(o0);
+        s_kv[0][j + kHalf] = f2h(o1);
+      } else {
+        const TQ* src = qkv + (long)(a.Hq + a.Hkv) * kD + (long)kvh * kD;
+        s_kv[1][j] = f2h(load_act(src, j));
+        s_kv[1][j + kHalf] = f2h(load_act(src, j + kHalf));
+      }
+    }
+    __syncthreads();
+    // the split holding the new position stores it into the static cache
+    if (pos >= t0 && pos < t1) {
+      const int t = threadIdx.x;
+      uint16_t* dst = (t < kD ? a.k_w : a.v_w) + (long)kvh * a.stride_h + pos * a.stride_s;
+      dst[t & (kD - 1)] = s_kv[t >> 7][t & (kD - 1)];
+    }
+    // rotated q for inspection by the host (first split of each kv head)
+    if (split == 0 && a.q_rot_out != nullptr) {
+      for (int i = threadIdx.x; i < G * kD; i += blockDim.x)
+        a.q_rot_out[(long)kvh * G * kD + i] = s_q[i / kD][i % kD];
+    }
+  }
+
   float q[G][8];
-  const TQ* qp = reinterpret_cast<const TQ*>(a.q);
 #pragma unroll
-  for (int g = 0; g < G; ++g) load_act8(qp, (long)(kvh * G + g) * a.q_stride + dl, q[g]);
+  for (int g = 0; g < G; ++g) {
+    if constexpr (FUSED_ROPE) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) q[g][i] = s_q[g][dl + i];
+    } else {
+      load_act8(reinterpret_cast<const TQ*>(a.q), (long)(kvh * G + g) * a.q_stride + dl, q[g]);
+    }
+  }
 
   float m[G], l[G], acc[G][8];
 #pragma unroll
@@ -77,42 +191,24 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const AttnArgs a, const
     for (int i = 0; i < 8; ++i) acc[g][i] = 0.f;
   }
 
-  const uint16_t* kb = a.k + (long)kvh * a.stride_h + dl;
-  const uint16_t* vb = a.v + (long)kvh * a.stride_h + dl;
-  for (int t = t0 + slot; t < t1; t += kSlots * kUnroll) {
-    u32x4 kk[kUnroll], vv[kUnroll];
+#pragma unroll 1
+  for (int tw = wave_t0; tw < t1; tw += kSlots * kUnroll) {
+    const int t = tw + row_off;
+    if (tw != wave_t0) load_kv_batch(kb, vb, a.stride_s, t, t1, skip, kk, vv);
+    if constexpr (FUSED_ROPE) {
+      // the new position comes from LDS (fp16, as written to the cache)
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int tt = t + u * kSlots;
-      if (tt < t1) {
-        kk[u] = ld_stream(kb + (long)tt * a.stride_s);
-        vv[u] = ld_stream(vb + (long)tt * a.stride_s);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int tt = t + u * kSlots;
-      if (tt < t1) {
-        float vf[8];
-        unpack8(vv[u], vf);
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          const float s = row16_sum(dot8(kk[u], q[g], 0.f)) * a.scale;
-          const float dlt = s - m[g];
-          const float e = __expf(-fabsf(dlt));
-          const bool up = dlt > 0.f;
-          const float c = up ? e : 1.f;   // rescale of the running sums
-          const float p = up ? 1.f : e;   // weight of this position
-          m[g] = up ? s : m[g];
-          l[g] = __builtin_fmaf(l[g], c, p);
-#pragma unroll
-          for (int i = 0; i < 8; ++i) acc[g][i] = __builtin_fmaf(acc[g][i], c, p * vf[i]);
+      for (int u = 0; u < kUnroll; ++u) {
+        if (t + u * kSlots == pos && pos < t1) {
+          kk[u] = *reinterpret_cast<const u32x4*>(&s_kv[0][dl]);
+          vv[u] = *reinterpret_cast<const u32x4*>(&s_kv[1][dl]);
         }
       }
     }
+    online_softmax_batch<G>(kk, vv, t, t1, q, a.scale, m, l, acc);
   }
 
-  // ---- merge the 16 slots of this workgroup
+  // ---- merge the 16 slots of this workgroup into one (output, LSE) per q head
   __shared__ float s_acc[kSlots][G][kD];
   __shared__ float s_m[kSlots][G];
   __shared__ float s_l[kSlots][G];
@@ -145,52 +241,89 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const AttnArgs a, const
     a.o_part[((long)h * a.n_split + split) * kD + d] = den > 0.f ? num / den : 0.f;
     if (d == 0) a.lse[(long)h * a.n_split + split] = den > 0.f ? M + __logf(den) : -INFINITY;
   }
-
-  if (!fused_merge) return;
-  __shared__ int s_last;
-  fence_release();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned prev = atomic_add_release(a.counters + kvh, 1u);
-    s_last = (prev == (unsigned)a.n_split - 1u);
-  }
-  __syncthreads();
-  if (!s_last) return;
-  fence_acquire();
-  merge_splits<G, TO>(a, kvh);
-  if (threadIdx.x == 0) store_relaxed(a.counters + kvh, 0u);
 }
+
+// out[h, d] = sum_s w_s o_s[d] / sum_s w_s with w_s = exp(lse_s - max lse).
+// One 256-thread block per q head: the split LSEs are staged in LDS in one
+// parallel load, then each half of the block sums every other split for all
+// 128 dims with the partial loads issued kMergeUnroll at a time.
+constexpr int kMergeMaxSplits = 1024;
+constexpr int kMergeUnroll = 8;
 
 template <typename TO>
-__global__ __launch_bounds__(128) void attn_merge_kernel(const AttnArgs a) {
-  // one block per q head; merge_splits with G = 1 treats blockIdx.x as the head.
-  merge_splits<1, TO>(a, blockIdx.x);
+__global__ __launch_bounds__(256) void attn_merge_kernel(const AttnArgs a) {
+  __shared__ float s_w[kMergeMaxSplits];
+  __shared__ float s_num[kD];
+  __shared__ float s_red[4];
+  const int h = blockIdx.x;
+  const int S = a.n_split;
+  const float* lse = a.lse + (long)h * S;
+  float mx = -INFINITY;
+  for (int s = threadIdx.x; s < S; s += blockDim.x) {
+    const float v = lse[s];
+    s_w[s] = v;
+    mx = fmaxf(mx, v);
+  }
+  mx = wave_max(mx);
+  if (lane_id() == 0) s_red[threadIdx.x / kWave] = mx;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+  __syncthreads();
+  for (int s = threadIdx.x; s < S; s += blockDim.x) s_w[s] = (M == -INFINITY) ? 0.f : __expf(s_w[s] - M);
+  __syncthreads();
+  const int d = threadIdx.x & (kD - 1);
+  const int half = threadIdx.x >> 7;
+  const float* op = a.o_part + (long)h * S * kD + d;
+  float num = 0.f;
+  for (int s0 = half; s0 < S; s0 += 2 * kMergeUnroll) {
+    float v[kMergeUnroll];
+#pragma unroll
+    for (int u = 0; u < kMergeUnroll; ++u) {
+      const int s = s0 + 2 * u;
+      v[u] = s < S ? op[(long)s * kD] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < kMergeUnroll; ++u) {
+      const int s = s0 + 2 * u;
+      if (s < S) num = __builtin_fmaf(s_w[s], v[u], num);
+    }
+  }
+  if (half == 1) s_num[d] = num;
+  __syncthreads();
+  if (half == 0) {
+    float den = 0.f;
+    for (int s = 0; s < S; ++s) den += s_w[s];
+    num += s_num[d];
+    store_act(reinterpret_cast<TO*>(a.out), (long)h * kD + d, den > 0.f ? num / den : 0.f);
+  }
 }
 
-template <typename TQ, typename TO>
-int attention_launch(const AttnArgs& a, bool fused_merge, hipStream_t s) {
-  const int G = a.Hq / a.Hkv;
+template <typename TQ, bool FUSED>
+static int launch_partial_g(const AttnArgs& a, hipStream_t s) {
   const dim3 grid((unsigned)(a.Hkv * a.n_split));
-  const int fm = fused_merge ? 1 : 0;
-  switch (G) {
-    case 1: hipLaunchKernelGGL((attn_split_kernel<1, TQ, TO>), grid, dim3(256), 0, s, a, fm); break;
-    case 2: hipLaunchKernelGGL((attn_split_kernel<2, TQ, TO>), grid, dim3(256), 0, s, a, fm); break;
-    case 4: hipLaunchKernelGGL((attn_split_kernel<4, TQ, TO>), grid, dim3(256), 0, s, a, fm); break;
+  switch (a.Hq / a.Hkv) {
+    case 1: hipLaunchKernelGGL((attn_partial_kernel<1, TQ, FUSED>), grid, dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((attn_partial_kernel<2, TQ, FUSED>), grid, dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((attn_partial_kernel<4, TQ, FUSED>), grid, dim3(256), 0, s, a); break;
     default: return QD_ERR_SHAPE;
   }
-  return qd_host::launch_status("attn_split_kernel");
+  return qd_host::launch_status("attn_partial_kernel");
+}
+
+template <typename TQ>
+int attention_partial_launch(const AttnArgs& a, hipStream_t s) {
+  return a.qkv != nullptr ? launch_partial_g<TQ, true>(a, s) : launch_partial_g<TQ, false>(a, s);
 }
 
 template <typename TO>
 int attention_merge_launch(const AttnArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL((attn_merge_kernel<TO>), dim3((unsigned)a.Hq), dim3(128), 0, s, a);
+  if (a.n_split > kMergeMaxSplits) return QD_ERR_SHAPE;
+  hipLaunchKernelGGL((attn_merge_kernel<TO>), dim3((unsigned)a.Hq), dim3(256), 0, s, a);
   return qd_host::launch_status("attn_merge_kernel");
 }
 
-template int attention_launch<uint16_t, uint16_t>(const AttnArgs&, bool, hipStream_t);
-template int attention_launch<float, float>(const AttnArgs&, bool, hipStream_t);
-template int attention_launch<uint16_t, float>(const AttnArgs&, bool, hipStream_t);
-template int attention_launch<float, uint16_t>(const AttnArgs&, bool, hipStream_t);
+template int attention_partial_launch<uint16_t>(const AttnArgs&, hipStream_t);
+template int attention_partial_launch<float>(const AttnArgs&, hipStream_t);
 template int attention_merge_launch<uint16_t>(const AttnArgs&, hipStream_t);
 template int attention_merge_launch<float>(const AttnArgs&, hipStream_t);
 

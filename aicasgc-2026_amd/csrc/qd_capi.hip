@@ -70,14 +70,13 @@ void argmax_ws(void* ws, GemvArgs& a) {
   a.part_val = reinterpret_cast<float*>(b + kArgmaxHeader + (size_t)qd::kMaxArgmaxBlocks * sizeof(long));
 }
 
-// Attention workspace: [counters (256 B)] [o_part Hq*S*128 f32] [lse Hq*S f32].
+// Attention workspace: [reserved (256 B)] [o_part Hq*S*128 f32] [lse Hq*S f32].
 size_t attn_ws_bytes(int Hq, int Hkv, int S_) {
   (void)Hkv;
   return 256 + (size_t)Hq * S_ * 128 * 4 + (size_t)Hq * S_ * 4;
 }
 void attn_ws(void* ws, qd::AttnArgs& a) {
   char* b = reinterpret_cast<char*>(ws);
-  a.counters = reinterpret_cast<unsigned*>(b);
   a.o_part = reinterpret_cast<float*>(b + 256);
   a.lse = reinterpret_cast<float*>(b + 256 + (size_t)a.Hq * a.n_split * 128 * 4);
 }
@@ -290,9 +289,10 @@ int qd_add_f16(const void* a, const void* b, void* out, long n, void* stream) {
 size_t qd_attention_workspace_bytes(int Hq, int Hkv, int n_split) { return attn_ws_bytes(Hq, Hkv, n_split); }
 
 int qd_attention_default_splits(int T) {
-  int s = (T + 127) / 128;
+  // ~64 positions per workgroup, at least 4 and at most 64 splits per kv head
+  int s = (T + 63) / 64;
   if (s < 4) s = 4;
-  if (s > 32) s = 32;
+  if (s > 64) s = 64;
   return s;
 }
 
@@ -324,11 +324,11 @@ int qd_attention_decode(const void* q, int q_dtype, long q_stride, const void* k
   QD_REQUIRE(out_dtype == QD_F16 || out_dtype == QD_F32, QD_ERR_ARG, "bad out dtype");
   a.out = out;
   attn_ws(workspace, a);
-  if (q_dtype == QD_F16)
-    return out_dtype == QD_F16 ? qd::attention_launch<u16, u16>(a, true, S(stream))
-                               : qd::attention_launch<u16, float>(a, true, S(stream));
-  return out_dtype == QD_F16 ? qd::attention_launch<float, u16>(a, true, S(stream))
-                             : qd::attention_launch<float, float>(a, true, S(stream));
+  st = q_dtype == QD_F16 ? qd::attention_partial_launch<u16>(a, S(stream))
+                         : qd::attention_partial_launch<float>(a, S(stream));
+  if (st) return st;
+  return out_dtype == QD_F16 ? qd::attention_merge_launch<u16>(a, S(stream))
+                             : qd::attention_merge_launch<float>(a, S(stream));
 }
 
 int qd_attention_partial(const void* q, int q_dtype, long q_stride, const void* k_cache, const void* v_cache,
@@ -340,8 +340,8 @@ int qd_attention_partial(const void* q, int q_dtype, long q_stride, const void* 
   if (st) return st;
   QD_REQUIRE(o_part && lse, QD_ERR_ARG, "null partial buffers");
   a.o_part = o_part; a.lse = lse;
-  return q_dtype == QD_F16 ? qd::attention_launch<u16, u16>(a, false, S(stream))
-                           : qd::attention_launch<float, float>(a, false, S(stream));
+  return q_dtype == QD_F16 ? qd::attention_partial_launch<u16>(a, S(stream))
+                           : qd::attention_partial_launch<float>(a, S(stream));
 }
 
 int qd_attention_merge(const float* o_part, const float* lse, void* out, int out_dtype, int Hq, int n_split,
@@ -454,22 +454,19 @@ int qd_decode_step_phases(const qd_model_desc* d, int first_layer, int n_layers,
     g1.x = b.x; g1.gamma = (const u16*)w.input_norm; g1.W = (const u16*)w.qkv; g1.y = b.qkv;
     g1.N = qs + 2 * kvs; g1.K = H; g1.ldw = H; g1.eps = d->eps;
     if ((phase_mask & QD_PHASE_QKV) && (st = qd::gemv_store<qd::PRO_RMSNORM, float, float>(g1, s))) return st;
-    // 2. q/k head RMSNorm + M-RoPE, K/V written at cache_position
-    qd::RopeArgs ra;
-    ra.q = b.qkv; ra.k = b.qkv + qs; ra.v = b.qkv + qs + kvs;
-    ra.q_weight = (const u16*)w.q_norm; ra.k_weight = (const u16*)w.k_norm; ra.eps = d->eps;
-    ra.rope_pos = d->rope_position; ra.inv_freq = d->inv_freq; ra.sec_h = d->sec_h; ra.sec_w = d->sec_w;
-    ra.q_out = b.q_rot; ra.k_cache = (u16*)w.k_cache; ra.v_cache = (u16*)w.v_cache;
-    ra.cache_stride_h = (long)d->capacity * D; ra.cache_stride_s = D; ra.T = d->capacity;
-    ra.cache_position = d->cache_position; ra.Hq = Hq; ra.Hkv = Hkv;
-    if ((phase_mask & QD_PHASE_ROPE_KV) && (st = qd::q_rope_kv_launch<float, float>(ra, s))) return st;
-    // 3. split-KV attention with fused merge
+    // 2. split-KV attention partials with the q/k head RMSNorm + M-RoPE and the
+    //    K/V write of the new token fused into the prologue
     qd::AttnArgs aa;
-    aa.q = b.q_rot; aa.q_stride = D; aa.k = (const u16*)w.k_cache; aa.v = (const u16*)w.v_cache;
+    aa.k = (const u16*)w.k_cache; aa.v = (const u16*)w.v_cache; aa.k_w = (u16*)w.k_cache; aa.v_w = (u16*)w.v_cache;
     aa.stride_h = (long)d->capacity * D; aa.stride_s = D; aa.T = d->capacity; aa.cache_position = d->cache_position;
     aa.scale = 1.0f / sqrtf((float)D); aa.Hq = Hq; aa.Hkv = Hkv; aa.n_split = splits; aa.out = b.attn;
+    aa.qkv = b.qkv; aa.q_weight = (const u16*)w.q_norm; aa.k_weight = (const u16*)w.k_norm; aa.eps = d->eps;
+    aa.rope_pos = d->rope_position; aa.inv_freq = d->inv_freq; aa.sec_h = d->sec_h; aa.sec_w = d->sec_w;
+    aa.q_rot_out = b.q_rot;
     attn_ws(b.attn_ws, aa);
-    if ((phase_mask & QD_PHASE_ATTN) && (st = qd::attention_launch<float, float>(aa, true, s))) return st;
+    if ((phase_mask & QD_PHASE_ATTN) && (st = qd::attention_partial_launch<float>(aa, s))) return st;
+    // 3. merge of the splits -> attention output [Hq*D]
+    if ((phase_mask & QD_PHASE_ATTN_MERGE) && (st = qd::attention_merge_launch<float>(aa, s))) return st;
     // 4. o_proj + residual: r = x + W_o attn
     GemvArgs g4;
     g4.x = b.attn; g4.W = (const u16*)w.o_proj; g4.residual = b.x; g4.y = b.r; g4.N = H; g4.K = qs; g4.ldw = qs;

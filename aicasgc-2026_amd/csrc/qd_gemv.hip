@@ -24,7 +24,27 @@
 
 namespace qd {
 
-template <int KCH, int R, int PRO, int EPI, typename TX, typename TY>
+// Loads the R weight rows of output group o0 (rows past N read as zero).
+template <int KCH, int R, int RO, int EPI>
+__device__ __forceinline__ void load_rows(const GemvArgs& a, long o0, long kofs, int lane, u32x4 (&wv)[R][KCH]) {
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const long oi = o0 + (r % RO);
+    const long row = (EPI == EPI_SILU && r >= RO) ? oi + a.up_offset : oi;
+    if (oi < a.N) {
+      const uint16_t* wr = a.W + row * a.ldw + kofs + lane * 8;
+#pragma unroll
+      for (int c = 0; c < KCH; ++c) wv[r][c] = ld_stream(wr + c * 512);
+    } else {
+#pragma unroll
+      for (int c = 0; c < KCH; ++c) wv[r][c] = u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+}
+
+// PIPE: issue the next row group's loads right after the dot products (only
+// worth its registers when a wave walks many row groups, i.e. the lm_head).
+template <int KCH, int R, int PRO, int EPI, typename TX, typename TY, bool PIPE = (EPI == EPI_ARGMAX)>
 __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
   constexpr int K = KCH * 512;
   constexpr int RO = (EPI == EPI_SILU) ? R / 2 : R;  // outputs per wave iteration
@@ -35,6 +55,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
   const long kofs = (long)blockIdx.y * K;  // split-K slice (gridDim.y == 1 otherwise)
   const long gw = (long)blockIdx.x * wpb + wib;
   const long nw = (long)gridDim.x * wpb;
+  const long stride = nw * RO;
+
+  // The weights do not depend on the activation: issue the first row group's
+  // loads before the activation prologue so the two latencies overlap.
+  u32x4 wv[R][KCH];
+  long o0 = gw * RO;
+  if (o0 < a.N) load_rows<KCH, R, RO, EPI>(a, o0, kofs, lane, wv);
 
   // ---- x slice -> registers (+ prologue)
   float xr[KCH][8];
@@ -85,30 +112,26 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
   float best_v = -INFINITY;
   long best_i = 0x7fffffffffffL;
 
-  // ---- row loop
-  for (long o0 = gw * RO; o0 < a.N; o0 += nw * RO) {
-    u32x4 wv[R][KCH];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const long oi = o0 + (r % RO);
-      const long row = (EPI == EPI_SILU && r >= RO) ? oi + a.up_offset : oi;
-      if (oi < a.N) {
-        const uint16_t* wr = a.W + row * a.ldw + kofs + lane * 8;
-#pragma unroll
-        for (int c = 0; c < KCH; ++c) wv[r][c] = ld_stream(wr + c * 512);
-      } else {
-#pragma unroll
-        for (int c = 0; c < KCH; ++c) wv[r][c] = u32x4{0u, 0u, 0u, 0u};
-      }
+  // ---- row loop: dot products of the resident rows, then the next group's
+  // loads are issued before the cross-lane reductions and the epilogue.
+  for (bool first = true; o0 < a.N; o0 += stride, first = false) {
+    if constexpr (!PIPE) {
+      if (!first) load_rows<KCH, R, RO, EPI>(a, o0, kofs, lane, wv);
     }
-    float acc[R];
+    float part[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       float s = 0.f;
 #pragma unroll
       for (int c = 0; c < KCH; ++c) s = dot8(wv[r][c], xr[c], s);
-      acc[r] = wave_sum(s);
+      part[r] = s;
     }
+    if constexpr (PIPE) {
+      if (o0 + stride < a.N) load_rows<KCH, R, RO, EPI>(a, o0 + stride, kofs, lane, wv);
+    }
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = wave_sum(part[r]);
 
     if constexpr (EPI == EPI_STORE) {
       if (lane == 0) {
@@ -141,10 +164,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
       }
     } else if constexpr (EPI == EPI_PARTIAL) {
       if (lane == 0) {
-        float* part = a.part_val + (long)blockIdx.y * a.N;
+        float* pv = a.part_val + (long)blockIdx.y * a.N;
 #pragma unroll
         for (int r = 0; r < R; ++r)
-          if (o0 + r < a.N) part[o0 + r] = acc[r];
+          if (o0 + r < a.N) pv[o0 + r] = acc[r];
       }
     } else {  // EPI_ARGMAX
 #pragma unroll
@@ -165,9 +188,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
   }
 
   if constexpr (EPI == EPI_ARGMAX) {
+    // per-block (max, first index); reduced by argmax_reduce_kernel in the next launch
     __shared__ float s_v[16];
     __shared__ long s_i[16];
-    __shared__ int s_last;
     if (lane == 0) {
       s_v[wib] = best_v;
       s_i[wib] = best_i;
@@ -184,44 +207,40 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
       }
       a.part_val[blockIdx.x] = bv;
       a.part_idx[blockIdx.x] = bi;
-      const unsigned prev = atomic_add_release(a.counter, 1u);
-      s_last = (prev == gridDim.x - 1);
-    }
-    __syncthreads();
-    if (s_last) {
-      fence_acquire();
-      float bv = -INFINITY;
-      long bi = 0x7fffffffffffL;
-      for (int b = threadIdx.x; b < (int)gridDim.x; b += blockDim.x) {
-        const float v = a.part_val[b];
-        const long i = a.part_idx[b];
-        if (v > bv || (v == bv && i < bi)) {
-          bv = v;
-          bi = i;
-        }
-      }
-      __shared__ float r_v[256];
-      __shared__ long r_i[256];
-      r_v[threadIdx.x] = bv;
-      r_i[threadIdx.x] = bi;
-      __syncthreads();
-      for (int s = blockDim.x / 2; s > 0; s >>= 1) {
-        if ((int)threadIdx.x < s) {
-          const float v = r_v[threadIdx.x + s];
-          const long i = r_i[threadIdx.x + s];
-          if (v > r_v[threadIdx.x] || (v == r_v[threadIdx.x] && i < r_i[threadIdx.x])) {
-            r_v[threadIdx.x] = v;
-            r_i[threadIdx.x] = i;
-          }
-        }
-        __syncthreads();
-      }
-      if (threadIdx.x == 0) {
-        a.token[0] = (int64_t)r_i[0];
-        store_relaxed(a.counter, 0u);  // self-reset for the next launch / graph replay
-      }
     }
   }
+}
+
+// One block: the first index of the maximum over n per-block partials.
+__global__ __launch_bounds__(256) void argmax_reduce_kernel(const float* part_val, const long* part_idx, int n,
+                                                            int64_t* token) {
+  __shared__ float r_v[256];
+  __shared__ long r_i[256];
+  float bv = -INFINITY;
+  long bi = 0x7fffffffffffL;
+  for (int b = threadIdx.x; b < n; b += blockDim.x) {
+    const float v = part_val[b];
+    const long i = part_idx[b];
+    if (v > bv || (v == bv && i < bi)) {
+      bv = v;
+      bi = i;
+    }
+  }
+  r_v[threadIdx.x] = bv;
+  r_i[threadIdx.x] = bi;
+  __syncthreads();
+  for (int s = blockDim.x / 2; s > 0; s >>= 1) {
+    if ((int)threadIdx.x < s) {
+      const float v = r_v[threadIdx.x + s];
+      const long i = r_i[threadIdx.x + s];
+      if (v > r_v[threadIdx.x] || (v == r_v[threadIdx.x] && i < r_i[threadIdx.x])) {
+        r_v[threadIdx.x] = v;
+        r_i[threadIdx.x] = i;
+      }
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) token[0] = (int64_t)r_i[0];
 }
 
 // Generic fallback: any K % 8 == 0; one wave per output row, x streamed from
@@ -289,11 +308,12 @@ constexpr int kWavesPerBlock = kThreads / kWave;
 long ceil_div(long a, long b) { return (a + b - 1) / b; }
 
 template <int KCH, int R, int PRO, int EPI, typename TX, typename TY>
-int launch_fixed(const GemvArgs& a, int splits, long max_blocks, hipStream_t s) {
+int launch_fixed(const GemvArgs& a, int splits, long max_blocks, hipStream_t s, long* blocks_out) {
   constexpr int RO = (EPI == EPI_SILU) ? R / 2 : R;
   long blocks = ceil_div(ceil_div(a.N, RO), kWavesPerBlock);
   if (max_blocks > 0 && blocks > max_blocks) blocks = max_blocks;
   if (blocks < 1) blocks = 1;
+  if (blocks_out != nullptr) *blocks_out = blocks;
   hipLaunchKernelGGL((gemv_kernel<KCH, R, PRO, EPI, TX, TY>), dim3((unsigned)blocks, (unsigned)splits),
                      dim3(kThreads), 0, s, a);
   return qd_host::launch_status("gemv_kernel");
@@ -301,14 +321,15 @@ int launch_fixed(const GemvArgs& a, int splits, long max_blocks, hipStream_t s) 
 
 // Dispatch on K (per split slice) to a register-resident kernel; R rows per wave.
 template <int R, int PRO, int EPI, typename TX, typename TY>
-int launch_k(const GemvArgs& a, int k_slice, int splits, long max_blocks, hipStream_t s) {
+int launch_k(const GemvArgs& a, int k_slice, int splits, long max_blocks, hipStream_t s,
+             long* blocks_out = nullptr) {
   switch (k_slice) {
-    case 512: return launch_fixed<1, R, PRO, EPI, TX, TY>(a, splits, max_blocks, s);
-    case 1024: return launch_fixed<2, R, PRO, EPI, TX, TY>(a, splits, max_blocks, s);
-    case 2048: return launch_fixed<4, R, PRO, EPI, TX, TY>(a, splits, max_blocks, s);
-    case 3072: return launch_fixed<6, (R > 2 ? 2 : R), PRO, EPI, TX, TY>(a, splits, max_blocks, s);
-    case 4096: return launch_fixed<8, (R > 2 ? 2 : R), PRO, EPI, TX, TY>(a, splits, max_blocks, s);
-    case 6144: return launch_fixed<12, (R > 2 ? 2 : R), PRO, EPI, TX, TY>(a, splits, max_blocks, s);
+    case 512: return launch_fixed<1, R, PRO, EPI, TX, TY>(a, splits, max_blocks, s, blocks_out);
+    case 1024: return launch_fixed<2, R, PRO, EPI, TX, TY>(a, splits, max_blocks, s, blocks_out);
+    case 2048: return launch_fixed<4, R, PRO, EPI, TX, TY>(a, splits, max_blocks, s, blocks_out);
+    case 3072: return launch_fixed<6, (R > 2 ? 2 : R), PRO, EPI, TX, TY>(a, splits, max_blocks, s, blocks_out);
+    case 4096: return launch_fixed<8, (R > 2 ? 2 : R), PRO, EPI, TX, TY>(a, splits, max_blocks, s, blocks_out);
+    case 6144: return launch_fixed<12, (R > 2 ? 2 : R), PRO, EPI, TX, TY>(a, splits, max_blocks, s, blocks_out);
     default: return 1;  // caller falls back
   }
 }
@@ -346,8 +367,14 @@ int gemv_silu(const GemvArgs& a, hipStream_t s) {
 template <int PRO, typename TX, typename TY>
 int gemv_argmax(const GemvArgs& a, hipStream_t s) {
   if (!has_fixed_k(a.K)) return QD_ERR_SHAPE;
-  const long max_blocks = (long)qd_host::cu_count() * 4;
-  return launch_k<4, PRO, EPI_ARGMAX, TX, TY>(a, a.K, 1, max_blocks > kMaxArgmaxBlocks ? kMaxArgmaxBlocks : max_blocks, s);
+  long max_blocks = (long)qd_host::cu_count() * 4;
+  if (max_blocks > kMaxArgmaxBlocks) max_blocks = kMaxArgmaxBlocks;
+  long blocks = 0;
+  int st = launch_k<4, PRO, EPI_ARGMAX, TX, TY>(a, a.K, 1, max_blocks, s, &blocks);
+  if (st != QD_OK) return st;
+  hipLaunchKernelGGL(argmax_reduce_kernel, dim3(1), dim3(kThreads), 0, s, a.part_val, a.part_idx, (int)blocks,
+                     a.token);
+  return qd_host::launch_status("argmax_reduce_kernel");
 }
 
 template <typename TX, typename TY>

@@ -45,7 +45,7 @@ int gemv_splitk(const GemvArgs& a, int splits, hipStream_t s);
 // ---------------------------------------------------------------- attention
 
 struct AttnArgs {
-  const void* q = nullptr;         // [Hq, 128] rows of stride q_stride (TQ)
+  const void* q = nullptr;         // [Hq, 128] rows of stride q_stride (TQ), already rotated
   long q_stride = 128;
   const uint16_t* k = nullptr;     // fp16 cache [Hkv, T, 128]
   const uint16_t* v = nullptr;
@@ -56,12 +56,23 @@ struct AttnArgs {
   int Hq = 16, Hkv = 8, n_split = 1;
   float* o_part = nullptr;         // [Hq, n_split, 128]
   float* lse = nullptr;            // [Hq, n_split]
-  unsigned* counters = nullptr;    // [Hkv] (fused merge only)
-  void* out = nullptr;             // [Hq, 128] (TO)
+  void* out = nullptr;             // [Hq, 128] (TO), merge kernel
+  // fused prologue (native step): raw qkv [Hq*D + 2*Hkv*D] (TQ) instead of q
+  const void* qkv = nullptr;
+  const uint16_t* q_weight = nullptr;
+  const uint16_t* k_weight = nullptr;
+  float eps = 1e-6f;
+  const int64_t* rope_pos = nullptr;  // int64 [3]
+  const float* inv_freq = nullptr;    // fp32 [64]
+  int sec_h = 20, sec_w = 20;
+  uint16_t* k_w = nullptr;            // writable aliases of k / v for the new row
+  uint16_t* v_w = nullptr;
+  float* q_rot_out = nullptr;         // optional fp32 [Hq, 128] copy of the rotated q
 };
 
-template <typename TQ, typename TO>
-int attention_launch(const AttnArgs& a, bool fused_merge, hipStream_t s);
+// Partials of every (kv head, split); fused prologue when a.qkv != nullptr.
+template <typename TQ>
+int attention_partial_launch(const AttnArgs& a, hipStream_t s);
 template <typename TO>
 int attention_merge_launch(const AttnArgs& a, hipStream_t s);
 

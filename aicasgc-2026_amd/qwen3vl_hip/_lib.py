@@ -22,7 +22,7 @@ QD_F16 = 0
 QD_F32 = 1
 
 # decode-step phase bits (QD_PHASE_* in include/qwen3vl_decode.h)
-PHASE = {"embed": 0x01, "qkv": 0x02, "rope_kv": 0x04, "attn": 0x08, "o_proj": 0x10, "gate_up": 0x20,
+PHASE = {"embed": 0x01, "qkv": 0x02, "attn": 0x04, "attn_merge": 0x08, "o_proj": 0x10, "gate_up": 0x20,
          "down": 0x40, "lm_head": 0x80}
 PHASE_ALL = 0xFF
 

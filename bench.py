@@ -194,6 +194,21 @@ def main() -> int:
     k_gbps = kbytes / (us_launch * 1e-6) / 1e9
     log(f"gate_up: {us_launch:.2f} us/launch, {k_gbps:.1f} GB/s")
 
+    # ---- reference stream: a plain 256 MiB device copy (known bytes; also the
+    # scale for the PMC FETCH_SIZE / WRITE_SIZE counters in profiles/)
+    src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    c0.record()
+    for _ in range(4):
+        dst.copy_(src)
+    c1.record()
+    torch.cuda.synchronize()
+    copy_gbps = 2 * src.numel() / (c0.elapsed_time(c1) / 4 * 1e-3) / 1e9
+    del src, dst
+    log(f"256 MiB device copy: {copy_gbps:.1f} GB/s (read + write)")
+
     traffic = None
     tfile = REPO / "profiles" / "gate_up_traffic.json"
     if tfile.exists():
@@ -242,6 +257,7 @@ def main() -> int:
                      "frac": round(k_gbps / PEAK_HBM_GBPS, 4), "traffic": traffic,
                      "us_per_launch": round(us_launch, 3), "bytes_per_launch": kbytes},
         "cpu_baseline": cpu,
+        "device_copy_GBps": round(copy_gbps, 1),
         "tokens_head": tokens[:8],
     }
     print(json.dumps(out), flush=True)

@@ -170,8 +170,8 @@ int qd_add_f16(const void* a, const void* b, void* out, long n, void* stream);
  *   L = min(cache_position[0] + 1, T); out[h] = softmax(q_h K[:L]^T * scale) V[:L]
  * for q head h on kv head h / (Hq/Hkv).  head_dim 128.  Each workgroup owns
  * one (kv head, split) and serves every q head of the group, so K/V is read
- * once.  Partials (normalised output + LSE) go to the workspace; the last
- * workgroup of a kv head merges them and resets its counter.
+ * once.  Partials (normalised output + LSE) go to the workspace and a second
+ * launch merges the splits (no cross-workgroup waiting inside a launch).
  * q: [Hq,128] with row stride q_stride (q_dtype); caches fp16 with head
  * stride cache_stride_h and row stride cache_stride_s; out [Hq,128] out_dtype.
  * Workspace: qd_attention_workspace_bytes(Hq, Hkv, n_split) bytes, zeroed
@@ -259,8 +259,10 @@ int qd_decode_step(const qd_model_desc* d, void* stream);
  * (cuda_decode_gemv_ops/profile.py). */
 #define QD_PHASE_EMBED 0x01u
 #define QD_PHASE_QKV 0x02u
-#define QD_PHASE_ROPE_KV 0x04u
-#define QD_PHASE_ATTN 0x08u
+/* attention partials; the q/k head RMSNorm + M-RoPE and the K/V write of the
+ * new token run in this phase's prologue */
+#define QD_PHASE_ATTN 0x04u
+#define QD_PHASE_ATTN_MERGE 0x08u
 #define QD_PHASE_O_PROJ 0x10u
 #define QD_PHASE_GATE_UP 0x20u
 #define QD_PHASE_DOWN 0x40u

@@ -96,9 +96,10 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, dtype=torch.floa
 
 
 def rope_inv_freq(shape: OracleShape = SHAPE, dtype=torch.float32) -> torch.Tensor:
-    """inv_freq[j] = theta^(-2j/d), j < d/2 (HF:340-342)."""
+    """inv_freq[j] = theta^(-2j/d), j < d/2 (HF:340-342), evaluated in ``dtype``
+    (fp32 reproduces HF's own fp32 expression bit for bit)."""
     d = shape.head_dim
-    return 1.0 / (shape.rope_theta ** (torch.arange(0, d, 2, dtype=torch.float64) / d)).to(dtype)
+    return 1.0 / (shape.rope_theta ** (torch.arange(0, d, 2, dtype=dtype) / d))
 
 
 def mrope_stream_of_slot(shape: OracleShape = SHAPE) -> list:
@@ -115,13 +116,18 @@ def mrope_stream_of_slot(shape: OracleShape = SHAPE) -> list:
     return out
 
 
-def mrope_cos_sin(position_ids: torch.Tensor, shape: OracleShape = SHAPE, dtype=torch.float32):
+def mrope_cos_sin(position_ids: torch.Tensor, shape: OracleShape = SHAPE, dtype=torch.float32,
+                  exact: bool = False):
     """cos/sin [S, d] for position ids [3, S] (T, H, W streams), HF:352-370.
 
     freqs[s, j] = pos[stream(j), s] * inv_freq[j]; emb = cat(freqs, freqs).
+    HF evaluates the angles and cos/sin in fp32 whatever the model dtype
+    (HF:363-368) and casts the result; that is the default here.  ``exact``
+    evaluates them in ``dtype`` instead (closed-form checks in fp64).
     """
-    pos = position_ids.to(torch.float64 if dtype == torch.float64 else torch.float32)
-    inv = rope_inv_freq(shape, pos.dtype)
+    work = dtype if exact else torch.float32
+    pos = position_ids.to(work)
+    inv = rope_inv_freq(shape, work)
     streams = torch.tensor(mrope_stream_of_slot(shape))
     p = pos[streams, :].T                      # [S, d/2]: position of the stream owning slot j
     freqs = p * inv[None, :]

@@ -92,8 +92,8 @@ def test_engine_phases_match_oracle_intermediates(cuda):
                                   lw["post_attn_layernorm_weight"], lw["gate_up_weight"], lw["down_proj_weight"],
                                   None, 1e-6)
     b = eng.buffers()
-    expect = [("embed", "x", x0), ("qkv", "qkv", qkv), ("rope_kv", "q_rot", q_rot.reshape(-1)),
-              ("attn", "attn", attn.reshape(-1)), ("o_proj", "r", r), ("gate_up", "hidden", hid),
+    expect = [("embed", "x", x0), ("qkv", "qkv", qkv), ("attn", "q_rot", q_rot.reshape(-1)),
+              ("attn_merge", "attn", attn.reshape(-1)), ("o_proj", "r", r), ("gate_up", "hidden", hid),
               ("down", "x", out)]
     for phase, buf, ref in expect:
         print(f"case engine phase {phase}", flush=True)
@@ -101,7 +101,7 @@ def test_engine_phases_match_oracle_intermediates(cuda):
         torch.cuda.synchronize()
         assert_close_rel(b[buf].cpu(), ref, rel=1e-4 if phase in ("embed", "qkv") else REL_ENGINE,
                          what=f"engine phase {phase}")
-        if phase == "rope_kv":
+        if phase == "attn":
             # fp32 K/V rounded to the fp16 cache: equal up to one fp16 rounding step
             assert_close_rel(eng.k_caches[0][0, :, 512].cpu(), kc[0, :, 512].float(), what="engine K row")
             assert_close_rel(eng.v_caches[0][0, :, 512].cpu(), vc[0, :, 512].float(), what="engine V row")
