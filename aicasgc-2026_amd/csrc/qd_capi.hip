@@ -6,6 +6,7 @@
 #include <string.h>
 
 #include <mutex>
+#include <string>
 #include <vector>
 
 #include "qd_common.h"
@@ -368,6 +369,8 @@ struct StepBuffers {
   float* hidden;   // [I]
   char* attn_ws;
   char* argmax_ws;
+  uint64_t* tagged;   // persistent step hand-off words
+  unsigned* control;  // persistent step: status, epoch, done
 };
 
 size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
@@ -383,6 +386,8 @@ bool step_layout(const qd_model_desc* d, int splits, StepBuffers* b, size_t* tot
   size_t o_h = off; off += align256(4 * (size_t)d->intermediate);
   size_t o_aw = off; off += align256(attn_ws_bytes(d->num_heads, d->num_kv_heads, splits));
   size_t o_gw = off; off += align256(argmax_ws_bytes());
+  size_t o_tg = off; off += align256(8 * qd::kPersistTaggedWords);
+  size_t o_ct = off; off += 256;
   *total = off;
   if (b != nullptr) {
     char* base = reinterpret_cast<char*>(d->workspace);
@@ -394,6 +399,8 @@ bool step_layout(const qd_model_desc* d, int splits, StepBuffers* b, size_t* tot
     b->hidden = reinterpret_cast<float*>(base + o_h);
     b->attn_ws = base + o_aw;
     b->argmax_ws = base + o_gw;
+    b->tagged = reinterpret_cast<uint64_t*>(base + o_tg);
+    b->control = reinterpret_cast<unsigned*>(base + o_ct);
   }
   return true;
 }
@@ -422,8 +429,140 @@ int qd_decode_workspace_layout(const qd_model_desc* d, size_t* offsets, int n) {
   return 6;
 }
 
+namespace {
+
+// Why the persistent step cannot serve this descriptor on the current device
+// (empty when it can).
+bool persistent_unsupported(const qd_model_desc* d, char* why, size_t n) {
+  why[0] = 0;
+  if (d->hidden != qd::kPersistHidden || d->num_heads != qd::kPersistHeads ||
+      d->num_kv_heads != qd::kPersistKvHeads || d->head_dim != qd::kPersistHeadDim ||
+      d->intermediate != qd::kPersistInter) {
+    snprintf(why, n, "persistent step is specialised for H=2048, 16/8 heads of 128, I=6144");
+    return true;
+  }
+  if (d->num_layers < 1 || d->num_layers > qd::kPersistMaxLayers) {
+    snprintf(why, n, "persistent step supports 1..%d layers", qd::kPersistMaxLayers);
+    return true;
+  }
+  static std::mutex mu;
+  static std::vector<int> verdict;  // per device: 0 unknown, 1 ok, 2 unsupported
+  static std::vector<std::string> reason;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    snprintf(why, n, "no current HIP device");
+    return true;
+  }
+  std::lock_guard<std::mutex> lk(mu);
+  if ((int)verdict.size() <= dev) {
+    verdict.resize(dev + 1, 0);
+    reason.resize(dev + 1);
+  }
+  if (verdict[dev] == 0) {
+    char buf[256] = "";
+    verdict[dev] = qd::decode_persistent_check_device(buf, sizeof(buf)) ? 2 : 1;
+    reason[dev] = buf;
+  }
+  if (verdict[dev] == 2) snprintf(why, n, "%s", reason[dev].c_str());
+  return verdict[dev] == 2;
+}
+
+int launch_persistent(const qd_model_desc* d, const StepBuffers& b, hipStream_t s) {
+  qd::PersistArgs p;
+  memset(&p, 0, sizeof(p));
+  for (int l = 0; l < d->num_layers; ++l) {
+    const qd_layer_weights& w = d->layers[l];
+    p.layers[l] = qd::PersistLayer{(const u16*)w.qkv,        (const u16*)w.o_proj,    (const u16*)w.gate_up,
+                                   (const u16*)w.down,       (const u16*)w.input_norm, (const u16*)w.post_norm,
+                                   (const u16*)w.q_norm,     (const u16*)w.k_norm,    (u16*)w.k_cache,
+                                   (u16*)w.v_cache};
+  }
+  p.num_layers = d->num_layers;
+  p.T = d->capacity;
+  p.vocab = d->vocab;
+  p.eps = d->eps;
+  p.scale = 1.0f / sqrtf((float)d->head_dim);
+  p.sec_h = d->sec_h;
+  p.sec_w = d->sec_w;
+  p.embed = (const u16*)d->embed;
+  p.token = d->token;
+  p.cache_position = d->cache_position;
+  p.rope_position = d->rope_position;
+  p.inv_freq = d->inv_freq;
+  uint64_t* t = b.tagged;
+  p.x_t = t; t += qd::kPersistHidden;
+  p.qkv_t = t; t += (qd::kPersistHeads + 2 * qd::kPersistKvHeads) * qd::kPersistHeadDim;
+  p.opart_t = t; t += (size_t)qd::kPersistHeads * qd::kPersistSplits * qd::kPersistHeadDim;
+  p.lse_t = t; t += qd::kPersistHeads * qd::kPersistSplits;
+  p.att_t = t; t += qd::kPersistHeads * qd::kPersistHeadDim;
+  p.r_t = t; t += qd::kPersistHidden;
+  p.hid_t = t;
+  p.x_out = b.x;
+  p.status = b.control;
+  p.epoch = b.control + 1;
+  p.done = b.control + 2;
+  return qd::decode_persistent_launch(p, s);
+}
+
+}  // namespace
+
+int qd_decode_step_mode(const qd_model_desc* d) {
+  QD_REQUIRE(d, QD_ERR_ARG, "null descriptor");
+  QD_REQUIRE(d->step_mode >= QD_STEP_AUTO && d->step_mode <= QD_STEP_PERSISTENT, QD_ERR_ARG, "bad step_mode %d",
+             d->step_mode);
+  if (d->step_mode == QD_STEP_CHAIN) return QD_STEP_CHAIN;
+  char why[256];
+  if (persistent_unsupported(d, why, sizeof(why))) {
+    if (d->step_mode == QD_STEP_PERSISTENT) {
+      qd_host::set_error("%s", why);
+      return QD_ERR_SHAPE;
+    }
+    return QD_STEP_CHAIN;
+  }
+  return QD_STEP_PERSISTENT;
+}
+
 int qd_decode_step(const qd_model_desc* d, void* stream) {
-  return qd_decode_step_phases(d, 0, d ? d->num_layers : 0, QD_PHASE_ALL, stream);
+  QD_REQUIRE(d, QD_ERR_ARG, "null descriptor");
+  const int mode = qd_decode_step_mode(d);
+  if (mode < 0) return mode;
+  if (mode == QD_STEP_CHAIN) return qd_decode_step_phases(d, 0, d->num_layers, QD_PHASE_ALL, stream);
+  int st = qd_decode_step_phases(d, 0, 0, 0, stream);  // descriptor checks only
+  if (st) return st;
+  StepBuffers b;
+  size_t total = 0;
+  step_layout(d, splits_of(d), &b, &total);
+  if ((st = launch_persistent(d, b, S(stream)))) return st;
+  return qd_decode_step_phases(d, 0, 0, QD_PHASE_LM_HEAD, stream);
+}
+
+int qd_decode_layers_persistent(const qd_model_desc* d, void* stream) {
+  QD_REQUIRE(d, QD_ERR_ARG, "null descriptor");
+  int st = qd_decode_step_phases(d, 0, 0, 0, stream);
+  if (st) return st;
+  char why[256];
+  QD_REQUIRE(!persistent_unsupported(d, why, sizeof(why)), QD_ERR_SHAPE, "%s", why);
+  StepBuffers b;
+  size_t total = 0;
+  step_layout(d, splits_of(d), &b, &total);
+  return launch_persistent(d, b, S(stream));
+}
+
+int qd_decode_status(const qd_model_desc* d, unsigned* status, int reset) {
+  QD_REQUIRE(d && d->workspace && status, QD_ERR_ARG, "null pointer");
+  StepBuffers b;
+  size_t total = 0;
+  step_layout(d, splits_of(d), &b, &total);
+  hipError_t e = hipMemcpy(status, b.control, sizeof(unsigned), hipMemcpyDeviceToHost);
+  if (e == hipSuccess && reset) {
+    const unsigned zero = 0;
+    e = hipMemcpy(b.control, &zero, sizeof(unsigned), hipMemcpyHostToDevice);
+  }
+  if (e != hipSuccess) {
+    qd_host::set_error("status read failed: %s", hipGetErrorString(e));
+    return (int)e;
+  }
+  return QD_OK;
 }
 
 int qd_decode_step_phases(const qd_model_desc* d, int first_layer, int n_layers, unsigned phase_mask,

@@ -115,4 +115,63 @@ int embed_gather_launch(const uint16_t* table, const int64_t* token, float* out,
 int decode_advance_launch(const int64_t* token, int64_t* out_tokens, int64_t* counter, int64_t* cache_position,
                           int64_t* rope_position, int max_tokens, hipStream_t s);
 
+// ---------------------------------------------------------------- persistent step
+
+constexpr int kPersistMaxLayers = 32;
+
+struct PersistLayer {
+  const uint16_t* qkv;
+  const uint16_t* o_proj;
+  const uint16_t* gate_up;
+  const uint16_t* down;
+  const uint16_t* input_norm;
+  const uint16_t* post_norm;
+  const uint16_t* q_norm;
+  const uint16_t* k_norm;
+  uint16_t* k_cache;
+  uint16_t* v_cache;
+};
+
+// Everything one persistent launch reads: passed by value, so the layer
+// table travels in the kernel arguments (no device copy of it is needed).
+struct PersistArgs {
+  PersistLayer layers[kPersistMaxLayers];
+  int num_layers;
+  int T;                          // cache rows per layer
+  long vocab;
+  float eps, scale;
+  int sec_h, sec_w;
+  const uint16_t* embed;          // fp16 [V, H]
+  const int64_t* token;           // int64 [1]
+  const int64_t* cache_position;  // int64 [1]
+  const int64_t* rope_position;   // int64 [3]
+  const float* inv_freq;          // fp32 [64]
+  // tagged hand-off buffers: (fp32 value | tag << 32)
+  uint64_t* x_t;                  // [H]
+  uint64_t* qkv_t;                // [Hq*D + 2*Hkv*D]
+  uint64_t* opart_t;              // [Hq, splits, D]
+  uint64_t* lse_t;                // [Hq, splits]
+  uint64_t* att_t;                // [Hq*D]
+  uint64_t* r_t;                  // [H]
+  uint64_t* hid_t;                // [I]
+  float* x_out;                   // fp32 [H]: last layer's output (lm_head input)
+  unsigned* status;               // bit 0: a hand-off wait ran out of its spin budget
+  unsigned* epoch;                // step counter that makes the tags unique
+  unsigned* done;                 // workgroups finished (self-resetting)
+};
+
+// Model shape the persistent kernel is specialised for, and its grid.
+constexpr int kPersistHidden = 2048, kPersistHeads = 16, kPersistKvHeads = 8, kPersistHeadDim = 128,
+              kPersistInter = 6144, kPersistBlocks = 256, kPersistSplits = kPersistBlocks / kPersistKvHeads;
+constexpr size_t kPersistTaggedWords = kPersistHidden                                              // x
+                                       + (size_t)(kPersistHeads + 2 * kPersistKvHeads) * kPersistHeadDim  // qkv
+                                       + (size_t)kPersistHeads * kPersistSplits * kPersistHeadDim    // o_part
+                                       + (size_t)kPersistHeads * kPersistSplits                      // lse
+                                       + (size_t)kPersistHeads * kPersistHeadDim                     // att
+                                       + kPersistHidden + kPersistInter;                              // r, hid
+
+int decode_persistent_launch(const PersistArgs& a, hipStream_t s);
+// 0 when the device can keep the whole persistent grid resident at once.
+int decode_persistent_check_device(char* why, size_t why_len);
+
 }  // namespace qd

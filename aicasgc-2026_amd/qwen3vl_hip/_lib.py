@@ -25,6 +25,7 @@ QD_F32 = 1
 PHASE = {"embed": 0x01, "qkv": 0x02, "attn": 0x04, "attn_merge": 0x08, "o_proj": 0x10, "gate_up": 0x20,
          "down": 0x40, "lm_head": 0x80}
 PHASE_ALL = 0xFF
+STEP_AUTO, STEP_CHAIN, STEP_PERSISTENT = 0, 1, 2
 
 P = c_void_p
 
@@ -62,6 +63,9 @@ _SIGS = {
     "qd_decode_step": (c_int, [P, P]),
     "qd_decode_step_phases": (c_int, [P, c_int, c_int, ctypes.c_uint, P]),
     "qd_decode_advance": (c_int, [P, P, P, P, P, c_int, P]),
+    "qd_decode_step_mode": (c_int, [P]),
+    "qd_decode_layers_persistent": (c_int, [P, P]),
+    "qd_decode_status": (c_int, [P, POINTER(ctypes.c_uint), c_int]),
 }
 
 EXPORTED = tuple(_SIGS)
@@ -127,7 +131,7 @@ ModelDesc._fields_ = [
     ("rope_position", c_void_p),
     ("logits_out", c_void_p),
     ("workspace", c_void_p),
-    ("attn_splits", c_int),
+    ("attn_splits", c_int), ("step_mode", c_int),
 ]
 
 __all__ = ["lib", "check", "ptr", "stream", "call", "QD_F16", "QD_F32", "ModelDesc", "LayerDesc", "EXPORTED",

@@ -35,8 +35,10 @@ def rope_inv_freq(shape: Qwen3VLTextShape = QWEN3VL_2B) -> torch.Tensor:
 class DecodeEngine:
     """Owns device weights, the static KV cache and the captured decode step."""
 
+    STEP_MODES = {"auto": _lib.STEP_AUTO, "chain": _lib.STEP_CHAIN, "persistent": _lib.STEP_PERSISTENT}
+
     def __init__(self, weights: ModelWeights, capacity: int, device="cuda", attn_splits: int = 0,
-                 keep_logits: bool = False):
+                 keep_logits: bool = False, step_mode: str = "auto"):
         if not torch.cuda.is_available():
             raise RuntimeError("DecodeEngine needs a ROCm GPU")
         self.device = torch.device(device)
@@ -88,12 +90,34 @@ class DecodeEngine:
         d.rope_position = self.rope_position.data_ptr()
         d.logits_out = self.logits.data_ptr() if self.logits is not None else None
         d.attn_splits = int(attn_splits)
+        d.step_mode = self.STEP_MODES[step_mode]
         nbytes = _lib.lib().qd_decode_workspace_bytes(ctypes.byref(d))
         self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
         d.workspace = self.workspace.data_ptr()
         self.desc = d
         self.graph = None
         self._graph_max_tokens = 0
+
+    @property
+    def step_mode(self) -> str:
+        """The mode qd_decode_step runs in on this device ("chain" or "persistent")."""
+        m = _lib.lib().qd_decode_step_mode(ctypes.byref(self.desc))
+        if m < 0:
+            _lib.check(m, "qd_decode_step_mode")
+        return "persistent" if m == _lib.STEP_PERSISTENT else "chain"
+
+    def status(self, reset: bool = True) -> int:
+        """Persistent-step status word (0: every hand-off completed)."""
+        v = ctypes.c_uint(0)
+        _lib.check(_lib.lib().qd_decode_status(ctypes.byref(self.desc), ctypes.byref(v), int(reset)),
+                   "qd_decode_status")
+        return int(v.value)
+
+    def layers_persistent(self) -> None:
+        """Enqueue embedding + all layers as one persistent launch (x left in buffers()["x"])."""
+        st = torch.cuda.current_stream(self.device).cuda_stream
+        _lib.check(_lib.lib().qd_decode_layers_persistent(ctypes.byref(self.desc), ctypes.c_void_p(st)),
+                   "qd_decode_layers_persistent")
 
     # ------------------------------------------------------------ state
     def set_state(self, token: int, cache_position: int, rope_position: int) -> None:
@@ -210,6 +234,9 @@ class DecodeEngine:
         S = prompt.length
         if S > self.capacity:
             raise ValueError("prompt longer than the static cache")
+        ids = prompt.text_ids
+        if ids.numel() and (int(ids.min()) < 0 or int(ids.max()) >= s.vocab):
+            raise ValueError(f"prompt token ids outside the vocabulary [0, {s.vocab})")
         emb = torch.cat([prompt.vision_embeds.to(dev).float(),
                          self.w.embed_tokens[prompt.text_ids.to(dev)].float()], 0)
         pos = prompt.position_ids.to(dev)

@@ -50,6 +50,17 @@ def gate_up_launch_bytes(shape) -> int:
     return 2 * n * k + 2 * k + 2 * n
 
 
+def persistent_launch_bytes(context_len: int, shape) -> int:
+    """Algorithmic bytes of one persistent launch at cache position context_len - 1:
+    every layer's weights and norms once, K/V rows [0, context_len) once per
+    layer (the new row counted as its write), the fp16 embedding row read and
+    the fp32 hidden state written for the lm_head."""
+    h, i, d = shape.hidden, shape.intermediate, shape.head_dim
+    layer_w = 2 * ((shape.q_size + 2 * shape.kv_size) * h + h * shape.q_size + 3 * i * h) + 2 * (2 * h + 2 * d)
+    kv = 2 * 2 * shape.num_kv_heads * d * context_len
+    return shape.num_layers * (layer_w + kv) + 2 * h + 4 * h
+
+
 def cpu_baseline(weights_gpu, prompt_len: int, n_steps: int, warmup: int = 2) -> dict:
     """The oracle's fp32 decode step (the reference's CPU PyTorch path restated)
     on this host, timed on a bounded sample: ``n_steps`` decode tokens at a
@@ -107,6 +118,7 @@ def main() -> int:
     ap.add_argument("--cpu-steps", type=int, default=12)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--attn-splits", type=int, default=0)
+    ap.add_argument("--step-mode", choices=["auto", "chain", "persistent"], default="auto")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -129,7 +141,7 @@ def main() -> int:
 
     n_dec = args.warmup + args.steps
     cap = prompt.length + n_dec + 1
-    eng = DecodeEngine(w, capacity=cap, attn_splits=args.attn_splits)
+    eng = DecodeEngine(w, capacity=cap, attn_splits=args.attn_splits, step_mode=args.step_mode)
     first = eng.prefill(prompt)
     eng.reserve_tokens(n_dec)
     eng.set_state(first, prompt.length, prompt.length + prompt.rope_delta)
@@ -157,7 +169,7 @@ def main() -> int:
 
     # ---- the same step around a 4096-token context (the target point)
     half = args.ctx_steps // 2
-    eng4 = DecodeEngine(w, capacity=4096 + half + 1, attn_splits=args.attn_splits)
+    eng4 = DecodeEngine(w, capacity=4096 + half + 1, attn_splits=args.attn_splits, step_mode=args.step_mode)
     for k, v in zip(eng4.k_caches, eng4.v_caches):
         k.normal_()
         v.normal_()
@@ -178,21 +190,59 @@ def main() -> int:
     del eng4
     log(f"ctx4096: {ms4:.4f} ms/token, {gbps4:.1f} GB/s")
 
-    # ---- dominant kernel: gate_up GEMV (RMSNorm prologue, SiLU*up epilogue), 28 distinct weights per pass
+    # ---- dominant kernel.  Persistent step: the one launch that runs all 28
+    # layers (algorithmic bytes = every layer weight + K/V[0:L] once, the
+    # embedding row, the fp32 hidden it leaves for the lm_head).  Kernel chain:
+    # the gate_up GEMV (RMSNorm prologue, SiLU*up epilogue), 28 distinct weights
+    # per pass.  Timed with events on the stream the kernels are launched on.
     stream = torch.cuda.current_stream()
-    eng.run_phases(["gate_up"])
-    torch.cuda.synchronize()
-    k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    k0.record(stream)
-    for _ in range(args.kernel_reps):
+    mode = eng.step_mode
+    if mode == "persistent":
+        ctx = prompt.length + n_dec
+        eng.set_state(first, ctx - 1, ctx - 1 + prompt.rope_delta)
+        eng.layers_persistent()
+        torch.cuda.synchronize()
+        k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        k0.record(stream)
+        for _ in range(args.kernel_reps):
+            eng.layers_persistent()
+        k1.record(stream)
+        torch.cuda.synchronize()
+        if eng.status() != 0:
+            raise RuntimeError("persistent step reported a failed hand-off")
+        n_launch = args.kernel_reps
+        kbytes = persistent_launch_bytes(ctx, shape)
+        kname = "decode_persistent_kernel (embedding + 28 layers, one launch)"
+        kunits = f"one decode step's 28 layers at context {ctx}"
+    else:
         eng.run_phases(["gate_up"])
-    k1.record(stream)
-    torch.cuda.synchronize()
-    n_launch = args.kernel_reps * shape.num_layers
+        torch.cuda.synchronize()
+        k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        k0.record(stream)
+        for _ in range(args.kernel_reps):
+            eng.run_phases(["gate_up"])
+        k1.record(stream)
+        torch.cuda.synchronize()
+        n_launch = args.kernel_reps * shape.num_layers
+        kbytes = gate_up_launch_bytes(shape)
+        kname = "gemv_kernel<4,4,PRO_RMSNORM,EPI_SILU,f32,f32> (gate_up)"
+        kunits = "one layer's gate_up rows (2I x H)"
     us_launch = k0.elapsed_time(k1) * 1000.0 / n_launch
-    kbytes = gate_up_launch_bytes(shape)
     k_gbps = kbytes / (us_launch * 1e-6) / 1e9
-    log(f"gate_up: {us_launch:.2f} us/launch, {k_gbps:.1f} GB/s")
+    log(f"{kname}: {us_launch:.2f} us/launch, {k_gbps:.1f} GB/s")
+
+    # ---- the lm_head + argmax phase (second largest; same stream, events)
+    eng.run_phases(["lm_head"], n_layers=0)
+    torch.cuda.synchronize()
+    h0, h1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    h0.record(stream)
+    for _ in range(args.kernel_reps):
+        eng.run_phases(["lm_head"], n_layers=0)
+    h1.record(stream)
+    torch.cuda.synchronize()
+    us_head = h0.elapsed_time(h1) * 1000.0 / args.kernel_reps
+    head_bytes = 2 * shape.vocab * shape.hidden + 2 * shape.hidden + 4 * shape.hidden
+    log(f"lm_head+argmax: {us_head:.2f} us, {head_bytes / (us_head * 1e-6) / 1e9:.1f} GB/s")
 
     # ---- reference stream: a plain 256 MiB device copy (known bytes; also the
     # scale for the PMC FETCH_SIZE / WRITE_SIZE counters in profiles/)
@@ -210,7 +260,7 @@ def main() -> int:
     log(f"256 MiB device copy: {copy_gbps:.1f} GB/s (read + write)")
 
     traffic = None
-    tfile = REPO / "profiles" / "gate_up_traffic.json"
+    tfile = REPO / "profiles" / ("persistent_traffic.json" if mode == "persistent" else "gate_up_traffic.json")
     if tfile.exists():
         try:
             traffic = json.loads(tfile.read_text()).get("bytes_per_launch")
@@ -244,6 +294,7 @@ def main() -> int:
             "generated_tokens": 1 + n_dec,
             "mean_context": round(sum(lens) / len(lens), 1),
             "attn_splits": int(eng.desc.attn_splits) or None,
+            "step_mode": eng.step_mode,
         },
         "tokens_per_s": round(1000.0 / ms, 1),
         "achieved_GBps": round(gbps, 1),
@@ -252,10 +303,12 @@ def main() -> int:
         "ctx4096": {"ms_per_token": round(ms4, 4), "tokens_per_s": round(1000.0 / ms4, 1),
                     "achieved_GBps": round(gbps4, 1), "roofline_frac": round(gbps4 / PEAK_HBM_GBPS, 4),
                     "step_bytes": int(bytes4), "roofline_ms": round(bytes4 / (PEAK_HBM_GBPS * 1e9) * 1e3, 4)},
-        "roofline": {"bound": "hbm", "kernel": "gemv_kernel<4,4,PRO_RMSNORM,EPI_SILU,f32,f32> (gate_up)",
+        "roofline": {"bound": "hbm", "kernel": kname, "units_per_launch": kunits,
                      "achieved": round(k_gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": round(k_gbps / PEAK_HBM_GBPS, 4), "traffic": traffic,
                      "us_per_launch": round(us_launch, 3), "bytes_per_launch": kbytes},
+        "lm_head": {"us_per_launch": round(us_head, 3), "bytes_per_launch": head_bytes,
+                    "achieved_GBps": round(head_bytes / (us_head * 1e-6) / 1e9, 1)},
         "cpu_baseline": cpu,
         "device_copy_GBps": round(copy_gbps, 1),
         "tokens_head": tokens[:8],

@@ -233,7 +233,19 @@ typedef struct qd_model_desc {
   void* logits_out;            /* fp16 [V] or NULL */
   void* workspace;             /* qd_decode_workspace_bytes() bytes, zeroed once */
   int attn_splits;             /* 0 = qd_attention_default_splits(capacity) */
+  int step_mode;               /* QD_STEP_AUTO / QD_STEP_CHAIN / QD_STEP_PERSISTENT */
 } qd_model_desc;
+
+/* How qd_decode_step runs the 28 layers.
+ *   QD_STEP_CHAIN       one kernel per phase (6 per layer), any supported shape;
+ *   QD_STEP_PERSISTENT  one persistent kernel for all layers (Qwen3-VL-2B text
+ *                       shape, needs 256 resident workgroups of 512 threads);
+ *   QD_STEP_AUTO        persistent when possible, else the chain.
+ * The attention of the persistent kernel always uses 32 splits per kv head;
+ * attn_splits applies to the chain. */
+#define QD_STEP_AUTO 0
+#define QD_STEP_CHAIN 1
+#define QD_STEP_PERSISTENT 2
 
 size_t qd_decode_workspace_bytes(const qd_model_desc* d);
 
@@ -270,6 +282,26 @@ int qd_decode_step(const qd_model_desc* d, void* stream);
 #define QD_PHASE_ALL 0xFFu
 int qd_decode_step_phases(const qd_model_desc* d, int first_layer, int n_layers,
                           unsigned phase_mask, void* stream);
+
+/* The mode qd_decode_step will use for this descriptor on the current device
+ * (QD_STEP_CHAIN or QD_STEP_PERSISTENT), or a negative status when
+ * step_mode == QD_STEP_PERSISTENT cannot be honoured (the message says why). */
+int qd_decode_step_mode(const qd_model_desc* d);
+
+/* Embedding + all layers as ONE persistent launch: 256 workgroups stay
+ * resident and hand activations to each other through tagged words in the
+ * workspace (no grid barrier, no kernel boundary between layers).  Leaves the
+ * final hidden state (before the final norm) in the workspace's residual vector
+ * x (first offset of qd_decode_workspace_layout); the lm_head phase of
+ * qd_decode_step_phases continues from there.  Replaces the same span of the
+ * reference's captured step as qd_decode_step (OptimizedDecoderLayer.forward x
+ * 28, optimized_layer.py:108-469). */
+int qd_decode_layers_persistent(const qd_model_desc* d, void* stream);
+
+/* Synchronously reads the persistent step's status word (0 = every hand-off
+ * completed; bit 0 = a wait exhausted its spin budget, results of that step
+ * are invalid) and clears it when reset != 0. */
+int qd_decode_status(const qd_model_desc* d, unsigned* status, int reset);
 
 /* Device-side end of a generation step (single thread):
  *   out_tokens[*counter] = *token (when *counter < max_tokens); ++*counter;

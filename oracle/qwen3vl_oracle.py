@@ -44,7 +44,6 @@ own Qwen3-VL modules, closed forms and invariants, brute force on tiny inputs).
 
 from __future__ import annotations
 
-import math
 from dataclasses import dataclass
 
 import torch
@@ -388,6 +387,3 @@ def roofline_bytes_step(context_len: int, shape: OracleShape = SHAPE) -> int:
     kv = 2 * 2 * shape.num_kv_heads * d * context_len
     return shape.num_layers * (layer_w + kv) + 2 * shape.vocab * h + 2 * h + 2 * h
 
-
-def math_isclose_margin(a: float, b: float) -> bool:  # pragma: no cover - helper for logs
-    return math.isclose(a, b, rel_tol=1e-6)

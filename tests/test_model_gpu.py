@@ -23,7 +23,8 @@ pytestmark = pytest.mark.gpu
 GOLDEN = Path(__file__).resolve().parent / "golden" / "config3_tokens.json"
 
 
-def test_two_layer_model_greedy_matches_oracle(cuda):
+@pytest.mark.parametrize("step_mode", ["chain", "persistent"])
+def test_two_layer_model_greedy_matches_oracle(cuda, step_mode):
     from qwen3vl_hip import synthetic as syn
     from qwen3vl_hip.engine import DecodeEngine
 
@@ -31,7 +32,7 @@ def test_two_layer_model_greedy_matches_oracle(cuda):
     prompt = syn.multimodal_prompt(21, grid_h=4, grid_w=8, n_text=16)
     n = 24
     cap = prompt.length + n + 8
-    eng = DecodeEngine(w, capacity=cap)
+    eng = DecodeEngine(w, capacity=cap, step_mode=step_mode)
     toks = eng.generate(prompt, n, use_graph=True)
     # prefill K/V against the oracle's prefill
     caches = [(torch.zeros(1, 8, cap, 128, dtype=torch.float16), torch.zeros(1, 8, cap, 128, dtype=torch.float16))
@@ -44,17 +45,26 @@ def test_two_layer_model_greedy_matches_oracle(cuda):
     print(f"gpu {toks}\noracle {ref}\nmin margin {min(margins):.4g}", flush=True)
     assert toks == ref
     # eager decode from the same state gives the same tokens as graph replay
-    eng2 = DecodeEngine(w.to(cuda), capacity=cap)
+    eng2 = DecodeEngine(w.to(cuda), capacity=cap, step_mode=step_mode)
     first = eng2.prefill(prompt)
     assert eng2.decode(first, prompt.length, prompt.rope_delta, n - 1, use_graph=False) == toks[1:]
 
 
-def test_full_model_config3_first_64_tokens(cuda):
+@pytest.fixture(scope="module")
+def config3_weights(cuda):
+    from qwen3vl_hip import synthetic as syn
+
+    gold = json.loads(GOLDEN.read_text())
+    return syn.model_weights(gold["weight_seed"], device=cuda)
+
+
+@pytest.mark.parametrize("step_mode", ["persistent", "chain"])
+def test_full_model_config3_first_64_tokens(cuda, config3_weights, step_mode):
     from qwen3vl_hip import synthetic as syn
     from qwen3vl_hip.engine import DecodeEngine
 
     gold = json.loads(GOLDEN.read_text())
-    w = syn.model_weights(gold["weight_seed"], device=cuda)
+    w = config3_weights
     fp = {
         "embed_sum": float(w.embed_tokens[:64].double().sum()),
         "layer0_qkv_sum": float(w.layers[0].qkv_weight[:64].double().sum()),
@@ -66,8 +76,10 @@ def test_full_model_config3_first_64_tokens(cuda):
     prompt = syn.multimodal_prompt(gold["prompt_seed"])
     assert prompt.length == gold["prompt_length"] and prompt.rope_delta == gold["rope_delta"]
     n = 64
-    eng = DecodeEngine(w, capacity=prompt.length + 256)
+    eng = DecodeEngine(w, capacity=prompt.length + 256, step_mode=step_mode)
     toks = eng.generate(prompt, n, use_graph=True)
+    if step_mode == "persistent":
+        assert eng.status() == 0
     ref = gold["tokens"][:n]
     first_bad = next((i for i, (a, b) in enumerate(zip(toks, ref)) if a != b), None)
     print(f"first mismatch: {first_bad}; margins there: "
