@@ -87,10 +87,18 @@ struct Spin {
   unsigned* err;
 };
 
-// Waits until every word v[k] (already loaded from base[idx[k]]) carries `tag`,
-// re-polling only the words that do not.
+// Tagged word at byte offset `off` of a buffer: a uniform base plus a 32-bit
+// per-lane offset, so the loads use scalar-base addressing and no 64-bit
+// per-lane address has to be kept.
+__device__ __forceinline__ const uint64_t* word_at(const uint64_t* base, unsigned off) {
+  return reinterpret_cast<const uint64_t*>(reinterpret_cast<const char*>(base) + off);
+}
+
+// Waits until every word v[k] (loaded from word_at(base, off0 + k * step))
+// carries `tag`.  A lane that is still waiting re-polls all of its words
+// (branch-free: one wait per poll instead of one per word).
 template <int N>
-__device__ __forceinline__ void await_tags(const uint64_t* base, const unsigned (&idx)[N], uint64_t (&v)[N],
+__device__ __forceinline__ void await_tags(const uint64_t* base, unsigned off0, unsigned step, uint64_t (&v)[N],
                                            unsigned tag, Spin& sp) {
 #pragma clang loop unroll(disable)
   while (true) {
@@ -105,8 +113,7 @@ __device__ __forceinline__ void await_tags(const uint64_t* base, const unsigned 
     --sp.left;
     __builtin_amdgcn_s_sleep(1);
 #pragma unroll
-    for (int k = 0; k < N; ++k)
-      if ((unsigned)(v[k] >> 32) != tag) v[k] = peek(base + idx[k]);
+    for (int k = 0; k < N; ++k) v[k] = peek(word_at(base, off0 + k * step));
   }
 }
 
@@ -114,27 +121,28 @@ __device__ __forceinline__ float value_of(uint64_t v) { return __builtin_bit_cas
 
 // Value of the tagged word base[i] once its tag matches (bounded wait).
 __device__ __forceinline__ float take1(const uint64_t* base, unsigned i, unsigned tag, Spin& sp) {
-  const unsigned idx[1] = {i};
-  uint64_t v[1] = {peek(base + i)};
-  await_tags<1>(base, idx, v, tag, sp);
+  uint64_t v[1] = {peek(word_at(base, i * 8u))};
+  await_tags<1>(base, i * 8u, 0u, v, tag, sp);
   return value_of(v[0]);
 }
 
-// All 512 threads of the workgroup gather N_PER * 512 tagged values src[i]
-// into dst[i]; every load is issued before the first wait.
-template <int N_PER>
+// THREADS threads (consecutive ids from thread t) gather N * THREADS tagged
+// values src[i] into dst[i], i = t + k * THREADS; every load is issued before
+// the first wait.
+template <int N, int THREADS>
+__device__ __forceinline__ void gather_n(const uint64_t* src, float* dst, unsigned t, unsigned tag, Spin& sp) {
+  uint64_t v[N];
+#pragma unroll
+  for (int k = 0; k < N; ++k) v[k] = peek(word_at(src, (t + k * THREADS) * 8u));
+  await_tags<N>(src, t * 8u, THREADS * 8u, v, tag, sp);
+#pragma unroll
+  for (int k = 0; k < N; ++k) dst[t + k * THREADS] = value_of(v[k]);
+}
+
+// Whole workgroup (512 threads).
+template <int N>
 __device__ __forceinline__ void gather(const uint64_t* src, float* dst, unsigned tag, Spin& sp) {
-  const unsigned t = fresh(threadIdx.x);
-  unsigned idx[N_PER];
-  uint64_t v[N_PER];
-#pragma unroll
-  for (int k = 0; k < N_PER; ++k) {
-    idx[k] = t + k * NW * kWave;
-    v[k] = peek(src + idx[k]);
-  }
-  await_tags<N_PER>(src, idx, v, tag, sp);
-#pragma unroll
-  for (int k = 0; k < N_PER; ++k) dst[idx[k]] = value_of(v[k]);
+  gather_n<N, NW * kWave>(src, dst, fresh(threadIdx.x), tag, sp);
 }
 
 template <int KCH>
@@ -165,26 +173,53 @@ __device__ __forceinline__ float lds_rstd(const float* s, int lane, float eps) {
   return rsqrtf(wave_sum(ss) / (float)(KCH * 512) + eps);
 }
 
-// y[r] = W_r . x for R rows held in registers, x streamed chunk by chunk from
-// LDS; with gamma != nullptr x is RMS-normalised on the fly (x * rstd * gamma).
+// The dot products below read x from LDS one chunk ahead of its use and keep
+// the scheduler from hoisting further reads (sched_barrier): left alone it
+// issues every chunk's LDS reads up front, and with the prefetched weights of
+// the next phases also live the registers run out.
+
+// y[r] = W_r . x for R rows held in registers, x streamed chunk by chunk from LDS.
 template <int KCH, int R>
-__device__ __forceinline__ void rows_dot(const u32x4 (&w)[R][KCH], const float* s, const uint16_t* gamma, float rstd,
-                                         int lane, float (&y)[R]) {
+__device__ __forceinline__ void rows_dot(const u32x4 (&w)[R][KCH], const float* s, int lane, float (&y)[R]) {
   float acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = 0.f;
+  float x[8], xn[8];
+  lds8(s, 0, lane, x);
 #pragma unroll
   for (int c = 0; c < KCH; ++c) {
-    float x[8];
-    lds8(s, c, lane, x);
-    if (gamma != nullptr) {
-      float g[8];
-      unpack8(ld16(gamma + c * 512 + lane * 8), g);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) x[i] = (x[i] * rstd) * g[i];
-    }
+    if (c + 1 < KCH) lds8(s, c + 1, lane, xn);
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = dot8(w[r][c], x, acc[r]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = xn[i];
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) y[r] = wave_sum(acc[r]);
+}
+
+// y[r] = W_r . (x * rstd * gamma); the lane's gamma chunks already in registers.
+template <int KCH, int R>
+__device__ __forceinline__ void rows_dot_norm(const u32x4 (&w)[R][KCH], const float* s, const u32x4 (&g)[KCH],
+                                              float rstd, int lane, float (&y)[R]) {
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.f;
+  float x[8], xn[8];
+  lds8(s, 0, lane, x);
+#pragma unroll
+  for (int c = 0; c < KCH; ++c) {
+    if (c + 1 < KCH) lds8(s, c + 1, lane, xn);
+    float gf[8];
+    unpack8(g[c], gf);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = (x[i] * rstd) * gf[i];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = dot8(w[r][c], x, acc[r]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = xn[i];
+    __builtin_amdgcn_sched_barrier(0);
   }
 #pragma unroll
   for (int r = 0; r < R; ++r) y[r] = wave_sum(acc[r]);
@@ -200,14 +235,27 @@ __device__ __forceinline__ void head_norm_rope_p(float x0, float x1, const uint1
   o1 = n1 * c + n0 * s;
 }
 
+// Weight streaming.  A wave's vector-memory loads complete in issue order, so a
+// wave that polls a hand-off must have no load outstanding that the phase after
+// the hand-off does not need (it would wait for it first).  The schedule:
+//   after DOWN's input      : next layer's W_qkv rows + input-norm gamma   (all waves)
+//   after QKV compute       : K/V rows, W_o row, q/k-norm weights          (all waves)
+//   after attention compute : W_gate/up rows + post-norm gamma             (waves 1..7)
+//   after O_PROJ's input    : the same for wave 0, which polls the split partials
+//                             (MERGE) and the merged output (O_PROJ input) alone
+//   after GATE_UP's input   : W_down row                                    (all waves)
+// so every load is in flight across at least one hand-off and no poll waits for
+// a load of a later phase.
+
 }  // namespace
 
 __global__ __launch_bounds__(512) void decode_persistent_kernel(const PersistArgs a) {
   const int b = blockIdx.x;
-  const int w = threadIdx.x / kWave;
-  const int lane = lane_id();
-  const int tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform: branches on it are scalar
+  int lane = lane_id();
+  int tid = threadIdx.x;
   const int gw = b * NW + w;
+  const bool poller = (w == 0);
   const unsigned ep = a.epoch[0];
   Spin sp{kSpinLimit, a.status};
 
@@ -220,9 +268,6 @@ __global__ __launch_bounds__(512) void decode_persistent_kernel(const PersistArg
   const int chunk = (L + NS - 1) / NS;
   const int t0 = split * chunk;
   const int t1 = min(t0 + chunk, L);
-  const int row_off = lane >> 4;                 // 16-lane row inside the wave
-  const int slot = w * 4 + row_off;
-  const int dl = (lane & 15) * 8;
   const int mh = b / (D / MERGE_DIMS);           // merged q head of this workgroup
   const int md0 = (b % (D / MERGE_DIMS)) * MERGE_DIMS;
 
@@ -238,18 +283,38 @@ __global__ __launch_bounds__(512) void decode_persistent_kernel(const PersistArg
   __shared__ float s_l[SLOTS][2];
   __shared__ float s_mw[NS][MERGE_DIMS + 1];
 
-  // first layer's QKV rows
-  u32x4 wq[2][4];
+  // M-RoPE angle of rotary pair `lane` (the same for every layer of the step)
+  float rc, rs;
   {
-    const uint16_t* W = a.layers[0].qkv;
-    load_row<4>(W + (long)(2 * gw) * H, lane, wq[0]);
-    load_row<4>(W + (long)(2 * gw + 1) * H, lane, wq[1]);
+    int stream = 0;
+    if (lane % 3 == 1 && lane < 3 * a.sec_h) stream = 1;
+    else if (lane % 3 == 2 && lane < 3 * a.sec_w) stream = 2;
+    sincosf((float)a.rope_position[stream] * a.inv_freq[lane], &rs, &rc);
   }
+
+  u32x4 wq[2][4], gq[4];
+  {
+    const PersistLayer& L0 = a.layers[0];
+    load_row<4>(L0.qkv + (long)(2 * gw) * H, lane, wq[0]);
+    load_row<4>(L0.qkv + (long)(2 * gw + 1) * H, lane, wq[1]);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) gq[c] = ld16(L0.input_norm + c * 512 + lane * 8);
+  }
+
+  // Lane-derived values are re-derived in every phase: otherwise the compiler
+  // hoists the per-lane address arithmetic of all phases out of the layer loop
+  // and the registers they occupy run out.
+#define QD_FRESH_LANE() \
+  do {                  \
+    lane = (int)fresh((unsigned)lane); \
+    tid = (int)fresh((unsigned)tid);   \
+  } while (0)
 
   for (int l = 0; l < a.num_layers; ++l) {
     const PersistLayer& Lw = a.layers[l];
 
     // ================================================================ QKV
+    QD_FRESH_LANE();
     if (l == 0) {
       long tok = a.token[0];
       if (tok < 0 || tok >= a.vocab) tok = 0;
@@ -261,7 +326,7 @@ __global__ __launch_bounds__(512) void decode_persistent_kernel(const PersistArg
     __syncthreads();
     {
       float y[2];
-      rows_dot<4, 2>(wq, s_x, Lw.input_norm, lds_rstd<4>(s_x, lane, a.eps), lane, y);
+      rows_dot_norm<4, 2>(wq, s_x, gq, lds_rstd<4>(s_x, lane, a.eps), lane, y);
       if (lane == 0) {
         const unsigned tg = tag_of(ep, l, PH_QKV);
         put(a.qkv_t + 2 * gw, tg, y[0]);
@@ -269,7 +334,12 @@ __global__ __launch_bounds__(512) void decode_persistent_kernel(const PersistArg
       }
     }
 
-    // prefetch: this workgroup's K/V rows (first batch) and this wave's o_proj row
+    QD_FRESH_LANE();
+    // issue: this workgroup's K/V rows (first batch), this wave's o_proj row,
+    // the q/k head-norm weights of the rotary pair `lane`
+    int row_off = lane >> 4;  // 16-lane row inside the wave
+    int slot = w * 4 + row_off;
+    int dl = (lane & 15) * 8;
     const uint16_t* kb = Lw.k_cache + (long)kvh * a.T * D + dl;
     const uint16_t* vb = Lw.v_cache + (long)kvh * a.T * D + dl;
     u32x4 kk[KU], vv[KU];
@@ -285,8 +355,11 @@ __global__ __launch_bounds__(512) void decode_persistent_kernel(const PersistArg
     }
     u32x4 wo[1][4];
     load_row<4>(Lw.o_proj + (long)gw * H, lane, wo[0]);
+    const uint16_t* nw = (w == 2) ? Lw.k_norm : Lw.q_norm;
+    const uint16_t nw0 = nw[lane], nw1 = nw[lane + 64];
 
     // ================================================================ ATTN
+    QD_FRESH_LANE();
     {
       // raw q (2 heads), k, v of kv head kvh: 512 tagged values, one per thread
       int src;
@@ -298,37 +371,35 @@ __global__ __launch_bounds__(512) void decode_persistent_kernel(const PersistArg
     __syncthreads();
     if (w < 4) {
       const int j = lane;
-      int stream = 0;
-      if (j % 3 == 1 && j < 3 * a.sec_h) stream = 1;
-      else if (j % 3 == 2 && j < 3 * a.sec_w) stream = 2;
-      float cs, sn;
-      sincosf((float)a.rope_position[stream] * a.inv_freq[j], &sn, &cs);
-      if (w < 2) {
-        float o0, o1;
-        head_norm_rope_p(s_raw[w][j], s_raw[w][j + 64], Lw.q_norm, a.eps, cs, sn, j, o0, o1);
-        s_q[w][j] = o0;
-        s_q[w][j + 64] = o1;
-      } else if (w == 2) {
-        float o0, o1;
-        head_norm_rope_p(s_raw[2][j], s_raw[2][j + 64], Lw.k_norm, a.eps, cs, sn, j, o0, o1);
-        s_kv[0][j] = f2h(o0);
-        s_kv[0][j + 64] = f2h(o1);
-        if (pos >= t0 && pos < t1) {
-          uint16_t* dst = Lw.k_cache + (long)kvh * a.T * D + pos * D;
-          dst[j] = s_kv[0][j];
-          dst[j + 64] = s_kv[0][j + 64];
+      const float x0 = s_raw[w][j], x1 = s_raw[w][j + 64];
+      if (w < 3) {
+        const float ss = wave_sum(x0 * x0 + x1 * x1);
+        const float rstd = rsqrtf(ss / (float)D + a.eps);
+        const float n0 = (x0 * rstd) * h2f(nw0);
+        const float n1 = (x1 * rstd) * h2f(nw1);
+        const float o0 = n0 * rc - n1 * rs;
+        const float o1 = n1 * rc + n0 * rs;
+        if (w < 2) {
+          s_q[w][j] = o0;
+          s_q[w][j + 64] = o1;
+        } else {
+          s_kv[0][j] = f2h(o0);
+          s_kv[0][j + 64] = f2h(o1);
         }
       } else {
-        s_kv[1][j] = f2h(s_raw[3][j]);
-        s_kv[1][j + 64] = f2h(s_raw[3][j + 64]);
-        if (pos >= t0 && pos < t1) {
-          uint16_t* dst = Lw.v_cache + (long)kvh * a.T * D + pos * D;
-          dst[j] = s_kv[1][j];
-          dst[j + 64] = s_kv[1][j + 64];
-        }
+        s_kv[1][j] = f2h(x0);
+        s_kv[1][j + 64] = f2h(x1);
+      }
+      if (w >= 2 && pos >= t0 && pos < t1) {
+        uint16_t* dst = (w == 2 ? Lw.k_cache : Lw.v_cache) + (long)kvh * a.T * D + pos * D;
+        dst[j] = s_kv[w - 2][j];
+        dst[j + 64] = s_kv[w - 2][j + 64];
       }
     }
     __syncthreads();
+    row_off = lane >> 4;
+    slot = w * 4 + row_off;
+    dl = (lane & 15) * 8;
     {
       float q[2][8];
 #pragma unroll
@@ -393,14 +464,7 @@ __global__ __launch_bounds__(512) void decode_persistent_kernel(const PersistArg
         }
       }
     }
-    // prefetch: this wave's three gate/up row pairs
-    u32x4 wgu[6][4];
-#pragma unroll
-    for (int p = 0; p < 3; ++p) {
-      const long o = (long)gw * 3 + p;
-      load_row<4>(Lw.gate_up + o * H, lane, wgu[p]);
-      load_row<4>(Lw.gate_up + (o + I) * H, lane, wgu[3 + p]);
-    }
+    QD_FRESH_LANE();
     __syncthreads();
     if (tid < 2 * D) {
       const int g = tid / D;
@@ -423,26 +487,23 @@ __global__ __launch_bounds__(512) void decode_persistent_kernel(const PersistArg
       if (d == 0) put(a.lse_t + (long)hq * NS + split, tg, den > 0.f ? M + __logf(den) : -INFINITY);
     }
 
-    // ================================================================ MERGE (wave 0)
-    if (w == 0) {
+    // ================================================================ MERGE + O_PROJ input (wave 0)
+    QD_FRESH_LANE();
+    if (poller) {
       const unsigned tg = tag_of(ep, l, PH_ATTN);
       // lanes 0..31: LSE of split `lane`; every lane: dims (lane / 32) * 4 .. +4 of split lane % 32
       const int s = lane % NS;
       const int k0 = (lane / NS) * 4;
-      const unsigned lo = fresh((unsigned)((mh * NS + s) * D + md0 + k0));
-      const unsigned idx[4] = {lo, lo + 1, lo + 2, lo + 3};
+      const unsigned lo = fresh((unsigned)((mh * NS + s) * D + md0 + k0)) * 8u;
       uint64_t ov[4];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) ov[k] = peek(a.opart_t + idx[k]);
+      for (int k = 0; k < 4; ++k) ov[k] = peek(word_at(a.opart_t, lo + k * 8u));
       const float lse = take1(a.lse_t, (unsigned)(mh * NS + s), tg, sp);
-      await_tags<4>(a.opart_t, idx, ov, tg, sp);
-      float o[4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) o[k] = value_of(ov[k]);
+      await_tags<4>(a.opart_t, lo, 8u, ov, tg, sp);
       const float M = wave_max(lse);
       const float wgt = (M == -INFINITY) ? 0.f : __expf(lse - M);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) s_mw[s][k0 + k] = wgt * o[k];
+      for (int k = 0; k < 4; ++k) s_mw[s][k0 + k] = wgt * value_of(ov[k]);
       if (lane < NS) s_mw[s][MERGE_DIMS] = wgt;
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -454,26 +515,39 @@ __global__ __launch_bounds__(512) void decode_persistent_kernel(const PersistArg
         }
         put(a.att_t + mh * D + md0 + lane, tag_of(ep, l, PH_MERGE), den > 0.f ? num / den : 0.f);
       }
+      gather_n<H / kWave, kWave>(a.att_t, s_att, (unsigned)lane, tag_of(ep, l, PH_MERGE), sp);
     }
+    // issue: this wave's gate/up row pairs and the post-attention norm gamma
+    // (waves 1..7 right after the partials, wave 0 after its two polls)
+    QD_FRESH_LANE();
+    u32x4 wgu[6][4], gp[4];
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+      const long o = (long)gw * 3 + p;
+      load_row<4>(Lw.gate_up + o * H, lane, wgu[p]);
+      load_row<4>(Lw.gate_up + (o + I) * H, lane, wgu[3 + p]);
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) gp[c] = ld16(Lw.post_norm + c * 512 + lane * 8);
+    __syncthreads();
 
     // ================================================================ O_PROJ
-    gather<H / (NW * kWave)>(a.att_t, s_att, tag_of(ep, l, PH_MERGE), sp);
-    __syncthreads();
+    QD_FRESH_LANE();
     {
       float y[1];
-      rows_dot<4, 1>(wo, s_att, nullptr, 0.f, lane, y);
+      rows_dot<4, 1>(wo, s_att, lane, y);
       if (lane == 0) put(a.r_t + gw, tag_of(ep, l, PH_OPROJ), y[0] + s_x[gw]);
     }
-    // prefetch: this wave's down_proj row
-    u32x4 wd[1][12];
-    load_row<12>(Lw.down + (long)gw * I, lane, wd[0]);
 
     // ================================================================ GATE_UP
+    QD_FRESH_LANE();
     gather<H / (NW * kWave)>(a.r_t, s_r, tag_of(ep, l, PH_OPROJ), sp);
     __syncthreads();
+    u32x4 wd[1][12];
+    load_row<12>(Lw.down + (long)gw * I, lane, wd[0]);
     {
       float gu[6];
-      rows_dot<4, 6>(wgu, s_r, Lw.post_norm, lds_rstd<4>(s_r, lane, a.eps), lane, gu);
+      rows_dot_norm<4, 6>(wgu, s_r, gp, lds_rstd<4>(s_r, lane, a.eps), lane, gu);
       if (lane == 0) {
         const unsigned tg = tag_of(ep, l, PH_GATEUP);
 #pragma unroll
@@ -483,19 +557,21 @@ __global__ __launch_bounds__(512) void decode_persistent_kernel(const PersistArg
         }
       }
     }
-    // prefetch: next layer's QKV rows
-    if (l + 1 < a.num_layers) {
-      const uint16_t* W = a.layers[l + 1].qkv;
-      load_row<4>(W + (long)(2 * gw) * H, lane, wq[0]);
-      load_row<4>(W + (long)(2 * gw + 1) * H, lane, wq[1]);
-    }
 
     // ================================================================ DOWN
+    QD_FRESH_LANE();
     gather<I / (NW * kWave)>(a.hid_t, s_h, tag_of(ep, l, PH_GATEUP), sp);
     __syncthreads();
+    if (l + 1 < a.num_layers) {
+      const PersistLayer& Ln = a.layers[l + 1];
+      load_row<4>(Ln.qkv + (long)(2 * gw) * H, lane, wq[0]);
+      load_row<4>(Ln.qkv + (long)(2 * gw + 1) * H, lane, wq[1]);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) gq[c] = ld16(Ln.input_norm + c * 512 + lane * 8);
+    }
     {
       float y[1];
-      rows_dot<12, 1>(wd, s_h, nullptr, 0.f, lane, y);
+      rows_dot<12, 1>(wd, s_h, lane, y);
       if (lane == 0) {
         const float v = y[0] + s_r[gw];
         put(a.x_t + gw, tag_of(ep, l, PH_DOWN), v);
@@ -503,6 +579,8 @@ __global__ __launch_bounds__(512) void decode_persistent_kernel(const PersistArg
       }
     }
   }
+
+#undef QD_FRESH_LANE
 
   // The last workgroup to finish advances the epoch for the next launch.  Every
   // workgroup read the epoch before it produced anything, so none can read the
