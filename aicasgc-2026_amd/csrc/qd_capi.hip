@@ -369,7 +369,7 @@ struct StepBuffers {
   float* hidden;   // [I]
   char* attn_ws;
   char* argmax_ws;
-  uint64_t* tagged;   // persistent step hand-off words
+  unsigned* tagged;   // persistent step hand-off words
   unsigned* control;  // persistent step: status, epoch, done
 };
 
@@ -386,7 +386,7 @@ bool step_layout(const qd_model_desc* d, int splits, StepBuffers* b, size_t* tot
   size_t o_h = off; off += align256(4 * (size_t)d->intermediate);
   size_t o_aw = off; off += align256(attn_ws_bytes(d->num_heads, d->num_kv_heads, splits));
   size_t o_gw = off; off += align256(argmax_ws_bytes());
-  size_t o_tg = off; off += align256(8 * qd::kPersistTaggedWords);
+  size_t o_tg = off; off += align256(4 * qd::kPersistTaggedWords);
   size_t o_ct = off; off += 256;
   *total = off;
   if (b != nullptr) {
@@ -399,7 +399,7 @@ bool step_layout(const qd_model_desc* d, int splits, StepBuffers* b, size_t* tot
     b->hidden = reinterpret_cast<float*>(base + o_h);
     b->attn_ws = base + o_aw;
     b->argmax_ws = base + o_gw;
-    b->tagged = reinterpret_cast<uint64_t*>(base + o_tg);
+    b->tagged = reinterpret_cast<unsigned*>(base + o_tg);
     b->control = reinterpret_cast<unsigned*>(base + o_ct);
   }
   return true;
@@ -489,7 +489,7 @@ int launch_persistent(const qd_model_desc* d, const StepBuffers& b, hipStream_t 
   p.cache_position = d->cache_position;
   p.rope_position = d->rope_position;
   p.inv_freq = d->inv_freq;
-  uint64_t* t = b.tagged;
+  unsigned* t = b.tagged;
   p.x_t = t; t += qd::kPersistHidden;
   p.qkv_t = t; t += (qd::kPersistHeads + 2 * qd::kPersistKvHeads) * qd::kPersistHeadDim;
   p.opart_t = t; t += (size_t)qd::kPersistHeads * qd::kPersistSplits * qd::kPersistHeadDim;

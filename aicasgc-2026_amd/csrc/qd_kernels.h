@@ -146,14 +146,14 @@ struct PersistArgs {
   const int64_t* cache_position;  // int64 [1]
   const int64_t* rope_position;   // int64 [3]
   const float* inv_freq;          // fp32 [64]
-  // tagged hand-off buffers: (fp32 value | tag << 32)
-  uint64_t* x_t;                  // [H]
-  uint64_t* qkv_t;                // [Hq*D + 2*Hkv*D]
-  uint64_t* opart_t;              // [Hq, splits, D]
-  uint64_t* lse_t;                // [Hq, splits]
-  uint64_t* att_t;                // [Hq*D]
-  uint64_t* r_t;                  // [H]
-  uint64_t* hid_t;                // [I]
+  // hand-off buffers: fp32 words whose mantissa LSB carries the write parity
+  unsigned* x_t;                  // [H]
+  unsigned* qkv_t;                // [Hq*D + 2*Hkv*D]
+  unsigned* opart_t;              // [Hq, splits, D]
+  unsigned* lse_t;                // [Hq, splits]
+  unsigned* att_t;                // [Hq*D]
+  unsigned* r_t;                  // [H]
+  unsigned* hid_t;                // [I]
   float* x_out;                   // fp32 [H]: last layer's output (lm_head input)
   unsigned* status;               // bit 0: a hand-off wait ran out of its spin budget
   unsigned* epoch;                // step counter that makes the tags unique

@@ -16,18 +16,24 @@
 // of its rows for the NEXT phase before it waits for that phase's input: the
 // HBM stream of phase p+1 overlaps the hand-off latency of phase p.
 //
-// Hand-off between workgroups is fence-free: every produced value is written
-// as one 64-bit word (fp32 value | 32-bit tag) with a relaxed agent-scope
-// atomic store, and consumers poll with relaxed agent-scope 64-bit atomic
-// loads until every word they need carries the expected tag.  A word is
-// single-copy atomic, so a matching tag implies the matching value; no
-// release/acquire (L2 write-back / invalidate) is ever issued.  Tags are
-// unique per (step epoch, layer, phase); the epoch advances once per step.
+// Hand-off between workgroups is fence-free.  Every produced value is one
+// 32-bit word: the fp32 value with its mantissa LSB replaced by the parity of
+// the write (a change of at most one ulp), stored with a relaxed agent-scope
+// atomic store.  Consumers read 16 bytes per lane with device-coherent (sc1)
+// buffer loads and poll until every word shows the parity they expect; no
+// release/acquire (L2 write-back / invalidate) is ever issued.  Each buffer is
+// written once per layer and every reader reads the same words at every layer,
+// so the parity alternates between consecutive writes and a reader, having
+// seen the previous write, can only see that write (wrong parity) or the one
+// it waits for: one bit is a complete tag.  A wave waits for its own stores to
+// complete before it polls; polling with a store in flight is several times
+// slower on this part.
 //
 // Every wait is bounded: a thread polls at most kSpinLimit times per launch,
 // then records an error in the status word and continues, so the grid always
 // drains.
 
+#include <float.h>
 #include <math.h>
 #include <stdio.h>
 
@@ -43,6 +49,7 @@ constexpr int H = kPersistHidden, HQ = kPersistHeads, HKV = kPersistKvHeads, D =
 constexpr int NB = kPersistBlocks;      // workgroups, one per CU
 constexpr int NW = 8;                   // waves per workgroup
 constexpr int NTH = NB * NW;            // waves in the grid
+constexpr int NA = 4;                   // waves 0..NA-1 poll the hand-offs; the others only stream
 constexpr int NS = kPersistSplits;      // attention splits per kv head
 constexpr int SLOTS = NW * 4;           // position slots per workgroup (4 rows of 16 lanes per wave)
 constexpr int KU = 4;                   // K/V rows per slot per batch
@@ -54,20 +61,48 @@ static_assert(H == NTH, "o_proj / down: one row per wave");
 static_assert(I == 3 * NTH, "gate_up: three row pairs per wave");
 static_assert(MERGE_DIMS == 8, "merge: 8 dims per workgroup");
 
-enum Phase { PH_QKV = 0, PH_ATTN = 1, PH_MERGE = 2, PH_OPROJ = 3, PH_GATEUP = 4, PH_DOWN = 5 };
-
-__device__ __forceinline__ unsigned tag_of(unsigned ep, int layer, int phase) {
-  return ep * 256u + (unsigned)(layer * 8 + phase) + 1u;
+// Parity of the words written at layer l of the launch with epoch ep.  It
+// alternates from layer to layer and across launches (the epoch advances once
+// per launch); the +1 makes the first write differ from a zeroed workspace.
+__device__ __forceinline__ unsigned parity_of(unsigned ep, int num_layers, int l) {
+  return (ep * (unsigned)num_layers + (unsigned)l + 1u) & 1u;
 }
 
-__device__ __forceinline__ void put(uint64_t* p, unsigned tag, float v) {
-  const uint64_t word = ((uint64_t)tag << 32) | (uint64_t)__builtin_bit_cast(unsigned, v);
-  __hip_atomic_store(p, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ unsigned word_of(float v, unsigned par) {
+  return (__builtin_bit_cast(unsigned, v) & ~1u) | par;
 }
 
-__device__ __forceinline__ uint64_t peek(const uint64_t* p) {
-  return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void put(unsigned* p, unsigned par, float v) {
+  __hip_atomic_store(p, word_of(v, par), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+
+// Two adjacent words (p 8-byte aligned) in one store.
+__device__ __forceinline__ void put2(unsigned* p, unsigned par, float v0, float v1) {
+  const uint64_t w = (uint64_t)word_of(v0, par) | ((uint64_t)word_of(v1, par) << 32);
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Wait until this wave's stores have completed (vmcnt(0)).
+__device__ __forceinline__ void puts_done() { __builtin_amdgcn_s_waitcnt(0x0f70); }
+
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+constexpr int kDeviceCoherent = 16;  // buffer-load cache policy: sc1 (device scope)
+
+__device__ __forceinline__ Rsrc rsrc_of(const unsigned* base, unsigned words) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned*>(base), (short)0, (int)(words * 4u), 0x00020000);
+}
+__device__ __forceinline__ u32x4 peek4(Rsrc r, unsigned off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kDeviceCoherent);
+}
+__device__ __forceinline__ unsigned peek1(Rsrc r, unsigned off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kDeviceCoherent);
+}
+__device__ __forceinline__ bool parity_ok(u32x4 v, unsigned par) {
+  return (((v.x ^ par) | (v.y ^ par) | (v.z ^ par) | (v.w ^ par)) & 1u) == 0u;
+}
+// Whole-vector cast: casting the elements one by one (bit_cast of v.y, ...)
+// is folded to v.x by this compiler.
+__device__ __forceinline__ f32x4 values_of(u32x4 v) { return __builtin_bit_cast(f32x4, v); }
 
 // A per-lane value the compiler must treat as new at this point: keeps it from
 // hoisting per-lane address arithmetic out of the layer loop (where it would
@@ -87,24 +122,17 @@ struct Spin {
   unsigned* err;
 };
 
-// Tagged word at byte offset `off` of a buffer: a uniform base plus a 32-bit
-// per-lane offset, so the loads use scalar-base addressing and no 64-bit
-// per-lane address has to be kept.
-__device__ __forceinline__ const uint64_t* word_at(const uint64_t* base, unsigned off) {
-  return reinterpret_cast<const uint64_t*>(reinterpret_cast<const char*>(base) + off);
-}
-
-// Waits until every word v[k] (loaded from word_at(base, off0 + k * step))
-// carries `tag`.  A lane that is still waiting re-polls all of its words
-// (branch-free: one wait per poll instead of one per word).
+// Waits until every word of v[k] (16 bytes loaded from byte offset
+// off0 + k * step) shows parity `par`.  A lane that is still waiting re-polls
+// all of its words (branch-free: one wait per poll instead of one per word).
 template <int N>
-__device__ __forceinline__ void await_tags(const uint64_t* base, unsigned off0, unsigned step, uint64_t (&v)[N],
-                                           unsigned tag, Spin& sp) {
+__device__ __forceinline__ void await4(Rsrc r, unsigned off0, unsigned step, u32x4 (&v)[N], unsigned par,
+                                       Spin& sp) {
 #pragma clang loop unroll(disable)
   while (true) {
     bool ok = true;
 #pragma unroll
-    for (int k = 0; k < N; ++k) ok &= (unsigned)(v[k] >> 32) == tag;
+    for (int k = 0; k < N; ++k) ok &= parity_ok(v[k], par);
     if (ok) break;
     if (sp.left == 0) {
       __hip_atomic_fetch_or(sp.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -113,36 +141,37 @@ __device__ __forceinline__ void await_tags(const uint64_t* base, unsigned off0, 
     --sp.left;
     __builtin_amdgcn_s_sleep(1);
 #pragma unroll
-    for (int k = 0; k < N; ++k) v[k] = peek(word_at(base, off0 + k * step));
+    for (int k = 0; k < N; ++k) v[k] = peek4(r, off0 + k * step);
   }
 }
 
-__device__ __forceinline__ float value_of(uint64_t v) { return __builtin_bit_cast(float, (unsigned)v); }
-
-// Value of the tagged word base[i] once its tag matches (bounded wait).
-__device__ __forceinline__ float take1(const uint64_t* base, unsigned i, unsigned tag, Spin& sp) {
-  uint64_t v[1] = {peek(word_at(base, i * 8u))};
-  await_tags<1>(base, i * 8u, 0u, v, tag, sp);
-  return value_of(v[0]);
+// Value of word i once it shows parity `par` (bounded wait).
+__device__ __forceinline__ float take1(Rsrc r, unsigned i, unsigned par, Spin& sp) {
+  unsigned v = peek1(r, i * 4u);
+#pragma clang loop unroll(disable)
+  while (((v ^ par) & 1u) != 0u) {
+    if (sp.left == 0) {
+      __hip_atomic_fetch_or(sp.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      break;
+    }
+    --sp.left;
+    __builtin_amdgcn_s_sleep(1);
+    v = peek1(r, i * 4u);
+  }
+  return __builtin_bit_cast(float, v);
 }
 
-// THREADS threads (consecutive ids from thread t) gather N * THREADS tagged
-// values src[i] into dst[i], i = t + k * THREADS; every load is issued before
-// the first wait.
+// THREADS threads (ids t = 0..THREADS-1) gather N * THREADS * 4 words into
+// dst: thread t takes words 4 (t + k THREADS) .. +4; every load is issued
+// before the first wait.
 template <int N, int THREADS>
-__device__ __forceinline__ void gather_n(const uint64_t* src, float* dst, unsigned t, unsigned tag, Spin& sp) {
-  uint64_t v[N];
+__device__ __forceinline__ void gather4(Rsrc r, float* dst, unsigned t, unsigned par, Spin& sp) {
+  u32x4 v[N];
 #pragma unroll
-  for (int k = 0; k < N; ++k) v[k] = peek(word_at(src, (t + k * THREADS) * 8u));
-  await_tags<N>(src, t * 8u, THREADS * 8u, v, tag, sp);
+  for (int k = 0; k < N; ++k) v[k] = peek4(r, (t + k * THREADS) * 16u);
+  await4<N>(r, t * 16u, THREADS * 16u, v, par, sp);
 #pragma unroll
-  for (int k = 0; k < N; ++k) dst[t + k * THREADS] = value_of(v[k]);
-}
-
-// Whole workgroup (512 threads).
-template <int N>
-__device__ __forceinline__ void gather(const uint64_t* src, float* dst, unsigned tag, Spin& sp) {
-  gather_n<N, NW * kWave>(src, dst, fresh(threadIdx.x), tag, sp);
+  for (int k = 0; k < N; ++k) *reinterpret_cast<f32x4*>(dst + (t + k * THREADS) * 4) = values_of(v[k]);
 }
 
 template <int KCH>
@@ -199,9 +228,9 @@ __device__ __forceinline__ void rows_dot(const u32x4 (&w)[R][KCH], const float* 
   for (int r = 0; r < R; ++r) y[r] = wave_sum(acc[r]);
 }
 
-// y[r] = W_r . (x * rstd * gamma); the lane's gamma chunks already in registers.
+// y[r] = W_r . (x * rstd * gamma), gamma (fp16) staged in LDS.
 template <int KCH, int R>
-__device__ __forceinline__ void rows_dot_norm(const u32x4 (&w)[R][KCH], const float* s, const u32x4 (&g)[KCH],
+__device__ __forceinline__ void rows_dot_norm(const u32x4 (&w)[R][KCH], const float* s, const uint16_t* g,
                                               float rstd, int lane, float (&y)[R]) {
   float acc[R];
 #pragma unroll
@@ -212,7 +241,7 @@ __device__ __forceinline__ void rows_dot_norm(const u32x4 (&w)[R][KCH], const fl
   for (int c = 0; c < KCH; ++c) {
     if (c + 1 < KCH) lds8(s, c + 1, lane, xn);
     float gf[8];
-    unpack8(g[c], gf);
+    unpack8(*reinterpret_cast<const u32x4*>(g + c * 512 + lane * 8), gf);
 #pragma unroll
     for (int i = 0; i < 8; ++i) x[i] = (x[i] * rstd) * gf[i];
 #pragma unroll
@@ -236,70 +265,74 @@ __device__ __forceinline__ void head_norm_rope_p(float x0, float x1, const uint1
 }
 
 // Weight streaming.  A wave's vector-memory loads complete in issue order, so a
-// wave that polls a hand-off must have no load outstanding that the phase after
-// the hand-off does not need (it would wait for it first).  The schedule:
-//   after DOWN's input      : next layer's W_qkv rows + input-norm gamma   (all waves)
-//   after QKV compute       : K/V rows, W_o row, q/k-norm weights          (all waves)
-//   after attention compute : W_gate/up rows + post-norm gamma             (waves 1..7)
-//   after O_PROJ's input    : the same for wave 0, which polls the split partials
-//                             (MERGE) and the merged output (O_PROJ input) alone
-//   after GATE_UP's input   : W_down row                                    (all waves)
-// so every load is in flight across at least one hand-off and no poll waits for
-// a load of a later phase.
+// wave that polls a hand-off waits for every load it issued before the poll.
+// The waves therefore split into two groups:
+//   pollers (waves 0-3) gather every hand-off into LDS (wave 0 alone gathers
+//     the split partials and the merged attention output) and issue each
+//     phase's weights only after the poll that precedes the phase;
+//   streamers (waves 4-7) never poll, wait only at workgroup barriers and issue
+//     weights one phase earlier: W_gate/up after QKV, W_down after attention,
+//     the next layer's W_qkv, K/V and W_o after GATE_UP.
+// Both groups hold the same number of rows, so a phase ends when the pollers'
+// later loads land; the streamers keep HBM busy across the hand-offs.
 
-}  // namespace
+// LDS of one workgroup.
+struct __align__(16) Smem {
+  float x[H];                 // layer input (residual of o_proj)
+  float att[H];               // merged attention output
+  float r[H];                 // post-attention residual
+  float h[I];                 // SiLU(gate) * up
+  float raw[4][D];            // raw q0, q1, k, v of this kv head
+  float q[2][D];              // rotated q
+  uint16_t kv[2][D];          // new K_rot / V rows, fp16 as cached
+  float acc[SLOTS][2][D];     // per-slot attention partials
+  float m[SLOTS][2];
+  float l[SLOTS][2];
+  float mw[NS][MERGE_DIMS + 1];
+  uint16_t gin[H];            // input RMSNorm weight of the current / next layer
+  uint16_t gpost[H];          // post-attention RMSNorm weight of the current layer
+};
 
-__global__ __launch_bounds__(512) void decode_persistent_kernel(const PersistArgs a) {
-  const int b = blockIdx.x;
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform: branches on it are scalar
+// Per-workgroup constants of a launch.
+struct Ctx {
+  int w, gw, kvh, split, t0, t1, mh, md0;
+  long pos;
+  unsigned ep;
+  float rc, rs;               // M-RoPE cos / sin of rotary pair `lane`
+};
+
+// The layer loop of one wave group.  Pollers (waves 0..NA-1) and streamers
+// run separate instances: their weight loads are issued at different points,
+// and in one shared loop the compiler would have to keep each group's
+// loop-carried weight registers live on the other group's path as well.
+// Both instances execute the same sequence of workgroup barriers.
+template <bool STREAM>
+__device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& cx, Smem& sm, Spin& sp) {
+  const int w = cx.w, gw = cx.gw, kvh = cx.kvh, split = cx.split, t0 = cx.t0, t1 = cx.t1, mh = cx.mh,
+            md0 = cx.md0;
+  const long pos = cx.pos;
+  const unsigned ep = cx.ep;
+  const float rc = cx.rc, rs = cx.rs;
+  constexpr bool streamer = STREAM;
+  const bool poller = (w == 0);     // polls the split partials (MERGE) and the merged output
   int lane = lane_id();
   int tid = threadIdx.x;
-  const int gw = b * NW + w;
-  const bool poller = (w == 0);
-  const unsigned ep = a.epoch[0];
-  Spin sp{kSpinLimit, a.status};
-
-  const long pos = a.cache_position[0];
-  long Ll = pos + 1 < (long)a.T ? pos + 1 : (long)a.T;
-  if (Ll < 0) Ll = 0;
-  const int L = (int)Ll;
-  const int kvh = b % HKV;
-  const int split = b / HKV;
-  const int chunk = (L + NS - 1) / NS;
-  const int t0 = split * chunk;
-  const int t1 = min(t0 + chunk, L);
-  const int mh = b / (D / MERGE_DIMS);           // merged q head of this workgroup
-  const int md0 = (b % (D / MERGE_DIMS)) * MERGE_DIMS;
-
-  __shared__ __align__(16) float s_x[H];         // layer input (residual of o_proj)
-  __shared__ __align__(16) float s_att[H];       // merged attention output
-  __shared__ __align__(16) float s_r[H];         // post-attention residual
-  __shared__ __align__(16) float s_h[I];         // SiLU(gate) * up
-  __shared__ __align__(16) float s_raw[4][D];    // raw q0, q1, k, v of this kv head
-  __shared__ __align__(16) float s_q[2][D];      // rotated q
-  __shared__ __align__(16) uint16_t s_kv[2][D];  // new K_rot / V rows, fp16 as cached
-  __shared__ __align__(16) float s_acc[SLOTS][2][D];
-  __shared__ float s_m[SLOTS][2];
-  __shared__ float s_l[SLOTS][2];
-  __shared__ float s_mw[NS][MERGE_DIMS + 1];
-
-  // M-RoPE angle of rotary pair `lane` (the same for every layer of the step)
-  float rc, rs;
-  {
-    int stream = 0;
-    if (lane % 3 == 1 && lane < 3 * a.sec_h) stream = 1;
-    else if (lane % 3 == 2 && lane < 3 * a.sec_w) stream = 2;
-    sincosf((float)a.rope_position[stream] * a.inv_freq[lane], &rs, &rc);
-  }
-
-  u32x4 wq[2][4], gq[4];
-  {
-    const PersistLayer& L0 = a.layers[0];
-    load_row<4>(L0.qkv + (long)(2 * gw) * H, lane, wq[0]);
-    load_row<4>(L0.qkv + (long)(2 * gw + 1) * H, lane, wq[1]);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) gq[c] = ld16(L0.input_norm + c * 512 + lane * 8);
-  }
+  const Rsrc r_x = rsrc_of(a.x_t, H), r_qkv = rsrc_of(a.qkv_t, NQKV), r_op = rsrc_of(a.opart_t, HQ * NS * D),
+             r_lse = rsrc_of(a.lse_t, HQ * NS), r_att = rsrc_of(a.att_t, HQ * D), r_r = rsrc_of(a.r_t, H),
+             r_hid = rsrc_of(a.hid_t, I);
+  float(&s_x)[H] = sm.x;
+  float(&s_att)[H] = sm.att;
+  float(&s_r)[H] = sm.r;
+  float(&s_h)[I] = sm.h;
+  float(&s_raw)[4][D] = sm.raw;
+  float(&s_q)[2][D] = sm.q;
+  uint16_t(&s_kv)[2][D] = sm.kv;
+  float(&s_acc)[SLOTS][2][D] = sm.acc;
+  float(&s_m)[SLOTS][2] = sm.m;
+  float(&s_l)[SLOTS][2] = sm.l;
+  float(&s_mw)[NS][MERGE_DIMS + 1] = sm.mw;
+  uint16_t(&s_gin)[H] = sm.gin;
+  uint16_t(&s_gpost)[H] = sm.gpost;
 
   // Lane-derived values are re-derived in every phase: otherwise the compiler
   // hoists the per-lane address arithmetic of all phases out of the layer loop
@@ -310,39 +343,25 @@ __global__ __launch_bounds__(512) void decode_persistent_kernel(const PersistArg
     tid = (int)fresh((unsigned)tid);   \
   } while (0)
 
-  for (int l = 0; l < a.num_layers; ++l) {
-    const PersistLayer& Lw = a.layers[l];
+  // Per-wave weight registers.  Those a streamer loads one layer ahead live
+  // across the layer loop; W_gate/up and W_down are loaded and consumed within
+  // one layer on every path, so they are declared in the loop body (a
+  // declaration outside would keep the previous layer's values live around
+  // the loop on the paths the compiler cannot rule out).
+  u32x4 wq[2][4];                 // W_qkv rows 2gw, 2gw+1
+  u32x4 kk[KU], vv[KU];           // first batch of K/V rows of the lane's position slot
+  u32x4 wo[1][4];                 // W_o row gw
+  uint16_t nw0 = 0, nw1 = 0;      // q/k head-norm weights of rotary pair `lane`
 
-    // ================================================================ QKV
-    QD_FRESH_LANE();
-    if (l == 0) {
-      long tok = a.token[0];
-      if (tok < 0 || tok >= a.vocab) tok = 0;
-      const uint16_t* row = a.embed + tok * (long)H;
-      for (int i = tid; i < H; i += NW * kWave) s_x[i] = h2f(row[i]);
-    } else {
-      gather<H / (NW * kWave)>(a.x_t, s_x, tag_of(ep, l - 1, PH_DOWN), sp);
-    }
-    __syncthreads();
-    {
-      float y[2];
-      rows_dot_norm<4, 2>(wq, s_x, gq, lds_rstd<4>(s_x, lane, a.eps), lane, y);
-      if (lane == 0) {
-        const unsigned tg = tag_of(ep, l, PH_QKV);
-        put(a.qkv_t + 2 * gw, tg, y[0]);
-        put(a.qkv_t + 2 * gw + 1, tg, y[1]);
-      }
-    }
-
-    QD_FRESH_LANE();
-    // issue: this workgroup's K/V rows (first batch), this wave's o_proj row,
-    // the q/k head-norm weights of the rotary pair `lane`
-    int row_off = lane >> 4;  // 16-lane row inside the wave
-    int slot = w * 4 + row_off;
-    int dl = (lane & 15) * 8;
-    const uint16_t* kb = Lw.k_cache + (long)kvh * a.T * D + dl;
-    const uint16_t* vb = Lw.v_cache + (long)kvh * a.T * D + dl;
-    u32x4 kk[KU], vv[KU];
+  auto issue_qkv = [&](const PersistLayer& Lx) {
+    load_row<4>(Lx.qkv + (long)(2 * gw) * H, lane, wq[0]);
+    load_row<4>(Lx.qkv + (long)(2 * gw + 1) * H, lane, wq[1]);
+  };
+  auto issue_kvwo = [&](const PersistLayer& Lx) {
+    const int slot = w * 4 + (lane >> 4);
+    const int dl = (lane & 15) * 8;
+    const uint16_t* kb = Lx.k_cache + (long)kvh * a.T * D + dl;
+    const uint16_t* vb = Lx.v_cache + (long)kvh * a.T * D + dl;
 #pragma unroll
     for (int u = 0; u < KU; ++u) {
       const int tt = t0 + slot + u * SLOTS;
@@ -353,20 +372,78 @@ __global__ __launch_bounds__(512) void decode_persistent_kernel(const PersistArg
         vv[u] = ld_stream(vb + (long)tt * D);
       }
     }
-    u32x4 wo[1][4];
-    load_row<4>(Lw.o_proj + (long)gw * H, lane, wo[0]);
-    const uint16_t* nw = (w == 2) ? Lw.k_norm : Lw.q_norm;
-    const uint16_t nw0 = nw[lane], nw1 = nw[lane + 64];
+    load_row<4>(Lx.o_proj + (long)gw * H, lane, wo[0]);
+    const uint16_t* nw = (w == 2) ? Lx.k_norm : Lx.q_norm;
+    nw0 = nw[lane];
+    nw1 = nw[lane + 64];
+  };
+  auto issue_gu = [&](const PersistLayer& Lx, u32x4 (&wgu)[6][4]) {
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+      const long o = (long)gw * 3 + p;
+      load_row<4>(Lx.gate_up + o * H, lane, wgu[p]);
+      load_row<4>(Lx.gate_up + (o + I) * H, lane, wgu[3 + p]);
+    }
+  };
+  auto issue_wd = [&](const PersistLayer& Lx, u32x4 (&wd)[1][12]) {
+    load_row<12>(Lx.down + (long)gw * I, lane, wd[0]);
+  };
+
+  // RMSNorm weights of a layer are staged in LDS by the polling waves: 16 bytes
+  // of each vector per thread, loaded together with their W_down rows of the
+  // previous layer and written after the DOWN hand-off.
+  if (!streamer) {
+    const u32x4 gi = ld16(a.layers[0].input_norm + tid * 8);
+    const u32x4 gp = ld16(a.layers[0].post_norm + tid * 8);
+    *reinterpret_cast<u32x4*>(s_gin + tid * 8) = gi;
+    *reinterpret_cast<u32x4*>(s_gpost + tid * 8) = gp;
+  }
+  issue_qkv(a.layers[0]);
+  if (streamer) issue_kvwo(a.layers[0]);
+
+  for (int l = 0; l < a.num_layers; ++l) {
+    const PersistLayer& Lw = a.layers[l];
+    const unsigned par = parity_of(ep, a.num_layers, l);
+    // The next layer's weights are issued unconditionally (the last layer
+    // re-issues its own, unused): a conditional issue would leave the previous
+    // values live to the end of the iteration on the path that skips it.
+    const PersistLayer& Ln = a.layers[l + 1 < a.num_layers ? l + 1 : l];
+    u32x4 wgu[6][4];              // W_gate/up rows 3gw..3gw+2 (+I)
+    u32x4 wd[1][12];              // W_down row gw
+
+    // ================================================================ QKV
+    QD_FRESH_LANE();
+    if (l == 0) {
+      long tok = a.token[0];
+      if (tok < 0 || tok >= a.vocab) tok = 0;
+      const uint16_t* row = a.embed + tok * (long)H;
+      for (int i = tid; i < H; i += NW * kWave) s_x[i] = h2f(row[i]);
+    } else if (!streamer) {
+      gather4<H / (4 * NA * kWave), NA * kWave>(r_x, s_x, (unsigned)tid, par ^ 1u, sp);
+    }
+    __syncthreads();
+    QD_FRESH_LANE();
+    if (!streamer) issue_kvwo(Lw);
+    {
+      float y[2];
+      rows_dot_norm<4, 2>(wq, s_x, s_gin, lds_rstd<4>(s_x, lane, a.eps), lane, y);
+      if (lane == 0) put2(a.qkv_t + 2 * gw, par, y[0], y[1]);
+      if (!streamer) puts_done();
+    }
+    QD_FRESH_LANE();
+    if (streamer) issue_gu(Lw, wgu);
 
     // ================================================================ ATTN
     QD_FRESH_LANE();
-    {
-      // raw q (2 heads), k, v of kv head kvh: 512 tagged values, one per thread
-      int src;
-      if (tid < 2 * D) src = kvh * 2 * D + tid;
-      else if (tid < 3 * D) src = HQ * D + kvh * D + (tid - 2 * D);
-      else src = (HQ + HKV) * D + kvh * D + (tid - 3 * D);
-      s_raw[tid / D][tid % D] = take1(a.qkv_t, (unsigned)src, tag_of(ep, l, PH_QKV), sp);
+    if (tid < D) {
+      // raw q (2 heads), k, v of kv head kvh: 512 words, 4 per thread of waves 0-1
+      unsigned src;
+      if (tid < D / 2) src = kvh * 2 * D + tid * 4;
+      else if (tid < 3 * D / 4) src = HQ * D + kvh * D + (tid - D / 2) * 4;
+      else src = (HQ + HKV) * D + kvh * D + (tid - 3 * D / 4) * 4;
+      u32x4 v[1] = {peek4(r_qkv, src * 4u)};
+      await4<1>(r_qkv, src * 4u, 0u, v, par, sp);
+      *reinterpret_cast<f32x4*>(&s_raw[0][0] + tid * 4) = values_of(v[0]);
     }
     __syncthreads();
     if (w < 4) {
@@ -397,10 +474,13 @@ __global__ __launch_bounds__(512) void decode_persistent_kernel(const PersistArg
       }
     }
     __syncthreads();
-    row_off = lane >> 4;
-    slot = w * 4 + row_off;
-    dl = (lane & 15) * 8;
+    QD_FRESH_LANE();
     {
+      const int row_off = lane >> 4;  // 16-lane row inside the wave
+      const int slot = w * 4 + row_off;
+      const int dl = (lane & 15) * 8;
+      const uint16_t* kb = Lw.k_cache + (long)kvh * a.T * D + dl;
+      const uint16_t* vb = Lw.v_cache + (long)kvh * a.T * D + dl;
       float q[2][8];
 #pragma unroll
       for (int g = 0; g < 2; ++g)
@@ -465,6 +545,7 @@ __global__ __launch_bounds__(512) void decode_persistent_kernel(const PersistArg
       }
     }
     QD_FRESH_LANE();
+    if (streamer) issue_wd(Lw, wd);
     __syncthreads();
     if (tid < 2 * D) {
       const int g = tid / D;
@@ -482,28 +563,28 @@ __global__ __launch_bounds__(512) void decode_persistent_kernel(const PersistArg
         }
       }
       const int hq = kvh * 2 + g;
-      const unsigned tg = tag_of(ep, l, PH_ATTN);
-      put(a.opart_t + ((long)hq * NS + split) * D + d, tg, den > 0.f ? num / den : 0.f);
-      if (d == 0) put(a.lse_t + (long)hq * NS + split, tg, den > 0.f ? M + __logf(den) : -INFINITY);
+      // an empty split reports lse = -FLT_MAX (finite: the parity bit must not turn -inf into a NaN)
+      put(a.opart_t + ((long)hq * NS + split) * D + d, par, den > 0.f ? num / den : 0.f);
+      if (d == 0) put(a.lse_t + (long)hq * NS + split, par, den > 0.f ? M + __logf(den) : -FLT_MAX);
     }
 
     // ================================================================ MERGE + O_PROJ input (wave 0)
     QD_FRESH_LANE();
     if (poller) {
-      const unsigned tg = tag_of(ep, l, PH_ATTN);
+      puts_done();
       // lanes 0..31: LSE of split `lane`; every lane: dims (lane / 32) * 4 .. +4 of split lane % 32
       const int s = lane % NS;
       const int k0 = (lane / NS) * 4;
-      const unsigned lo = fresh((unsigned)((mh * NS + s) * D + md0 + k0)) * 8u;
-      uint64_t ov[4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) ov[k] = peek(word_at(a.opart_t, lo + k * 8u));
-      const float lse = take1(a.lse_t, (unsigned)(mh * NS + s), tg, sp);
-      await_tags<4>(a.opart_t, lo, 8u, ov, tg, sp);
+      const unsigned lo = fresh((unsigned)((mh * NS + s) * D + md0 + k0)) * 4u;
+      u32x4 ov[1] = {peek4(r_op, lo)};
+      const float lse = take1(r_lse, (unsigned)(mh * NS + s), par, sp);
+      await4<1>(r_op, lo, 0u, ov, par, sp);
+      const f32x4 o4 = values_of(ov[0]);
+      const float o[4] = {o4.x, o4.y, o4.z, o4.w};
       const float M = wave_max(lse);
-      const float wgt = (M == -INFINITY) ? 0.f : __expf(lse - M);
+      const float wgt = __expf(lse - M);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) s_mw[s][k0 + k] = wgt * value_of(ov[k]);
+      for (int k = 0; k < 4; ++k) s_mw[s][k0 + k] = wgt * o[k];
       if (lane < NS) s_mw[s][MERGE_DIMS] = wgt;
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -513,22 +594,14 @@ __global__ __launch_bounds__(512) void decode_persistent_kernel(const PersistArg
           num += s_mw[t][lane];
           den += s_mw[t][MERGE_DIMS];
         }
-        put(a.att_t + mh * D + md0 + lane, tag_of(ep, l, PH_MERGE), den > 0.f ? num / den : 0.f);
+        put(a.att_t + mh * D + md0 + lane, par, den > 0.f ? num / den : 0.f);
       }
-      gather_n<H / kWave, kWave>(a.att_t, s_att, (unsigned)lane, tag_of(ep, l, PH_MERGE), sp);
+      puts_done();
+      gather4<H / (4 * kWave), kWave>(r_att, s_att, (unsigned)lane, par, sp);
     }
-    // issue: this wave's gate/up row pairs and the post-attention norm gamma
-    // (waves 1..7 right after the partials, wave 0 after its two polls)
+    // waves 1-3 right after the partials, wave 0 after its two polls
     QD_FRESH_LANE();
-    u32x4 wgu[6][4], gp[4];
-#pragma unroll
-    for (int p = 0; p < 3; ++p) {
-      const long o = (long)gw * 3 + p;
-      load_row<4>(Lw.gate_up + o * H, lane, wgu[p]);
-      load_row<4>(Lw.gate_up + (o + I) * H, lane, wgu[3 + p]);
-    }
-#pragma unroll
-    for (int c = 0; c < 4; ++c) gp[c] = ld16(Lw.post_norm + c * 512 + lane * 8);
+    if (!streamer) issue_gu(Lw, wgu);
     __syncthreads();
 
     // ================================================================ O_PROJ
@@ -536,51 +609,100 @@ __global__ __launch_bounds__(512) void decode_persistent_kernel(const PersistArg
     {
       float y[1];
       rows_dot<4, 1>(wo, s_att, lane, y);
-      if (lane == 0) put(a.r_t + gw, tag_of(ep, l, PH_OPROJ), y[0] + s_x[gw]);
+      if (lane == 0) put(a.r_t + gw, par, y[0] + s_x[gw]);
+      if (!streamer) puts_done();
     }
 
     // ================================================================ GATE_UP
     QD_FRESH_LANE();
-    gather<H / (NW * kWave)>(a.r_t, s_r, tag_of(ep, l, PH_OPROJ), sp);
+    if (!streamer) gather4<H / (4 * NA * kWave), NA * kWave>(r_r, s_r, (unsigned)tid, par, sp);
     __syncthreads();
-    u32x4 wd[1][12];
-    load_row<12>(Lw.down + (long)gw * I, lane, wd[0]);
+    QD_FRESH_LANE();
+    u32x4 gi_next, gp_next;
+    if (!streamer) {
+      gi_next = ld16(Ln.input_norm + tid * 8);
+      gp_next = ld16(Ln.post_norm + tid * 8);
+      issue_wd(Lw, wd);
+    }
     {
       float gu[6];
-      rows_dot_norm<4, 6>(wgu, s_r, gp, lds_rstd<4>(s_r, lane, a.eps), lane, gu);
+      rows_dot_norm<4, 6>(wgu, s_r, s_gpost, lds_rstd<4>(s_r, lane, a.eps), lane, gu);
       if (lane == 0) {
-        const unsigned tg = tag_of(ep, l, PH_GATEUP);
 #pragma unroll
         for (int p = 0; p < 3; ++p) {
           const float g = gu[p];
-          put(a.hid_t + (long)gw * 3 + p, tg, (g / (1.0f + __expf(-g))) * gu[3 + p]);
+          put(a.hid_t + (long)gw * 3 + p, par, (g / (1.0f + __expf(-g))) * gu[3 + p]);
         }
       }
+      if (!streamer) puts_done();
+    }
+    QD_FRESH_LANE();
+    if (streamer) {
+      issue_qkv(Ln);
+      issue_kvwo(Ln);
     }
 
     // ================================================================ DOWN
     QD_FRESH_LANE();
-    gather<I / (NW * kWave)>(a.hid_t, s_h, tag_of(ep, l, PH_GATEUP), sp);
+    if (!streamer) gather4<I / (4 * NA * kWave), NA * kWave>(r_hid, s_h, (unsigned)tid, par, sp);
     __syncthreads();
-    if (l + 1 < a.num_layers) {
-      const PersistLayer& Ln = a.layers[l + 1];
-      load_row<4>(Ln.qkv + (long)(2 * gw) * H, lane, wq[0]);
-      load_row<4>(Ln.qkv + (long)(2 * gw + 1) * H, lane, wq[1]);
-#pragma unroll
-      for (int c = 0; c < 4; ++c) gq[c] = ld16(Ln.input_norm + c * 512 + lane * 8);
+    QD_FRESH_LANE();
+    if (!streamer) {
+      // every wave finished this layer's norms before the barrier above
+      *reinterpret_cast<u32x4*>(s_gin + tid * 8) = gi_next;
+      *reinterpret_cast<u32x4*>(s_gpost + tid * 8) = gp_next;
+      issue_qkv(Ln);
     }
     {
       float y[1];
       rows_dot<12, 1>(wd, s_h, lane, y);
       if (lane == 0) {
         const float v = y[0] + s_r[gw];
-        put(a.x_t + gw, tag_of(ep, l, PH_DOWN), v);
+        put(a.x_t + gw, par, v);
         if (l + 1 == a.num_layers) a.x_out[gw] = v;
       }
+      if (!streamer) puts_done();
     }
   }
 
 #undef QD_FRESH_LANE
+}
+
+}  // namespace
+
+__global__ __launch_bounds__(512) void decode_persistent_kernel(const PersistArgs a) {
+  const int b = blockIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform: branches on it are scalar
+  const int lane = lane_id();
+  const int tid = threadIdx.x;
+  Spin sp{kSpinLimit, a.status};
+  __shared__ Smem sm;
+
+  Ctx cx;
+  cx.w = w;
+  cx.gw = b * NW + w;
+  cx.ep = a.epoch[0];
+  cx.pos = a.cache_position[0];
+  long Ll = cx.pos + 1 < (long)a.T ? cx.pos + 1 : (long)a.T;
+  if (Ll < 0) Ll = 0;
+  const int L = (int)Ll;
+  cx.kvh = b % HKV;
+  cx.split = b / HKV;
+  const int chunk = (L + NS - 1) / NS;
+  cx.t0 = cx.split * chunk;
+  cx.t1 = min(cx.t0 + chunk, L);
+  cx.mh = b / (D / MERGE_DIMS);               // merged q head of this workgroup
+  cx.md0 = (b % (D / MERGE_DIMS)) * MERGE_DIMS;
+  {
+    // M-RoPE angle of rotary pair `lane` (the same for every layer of the step)
+    int stream = 0;
+    if (lane % 3 == 1 && lane < 3 * a.sec_h) stream = 1;
+    else if (lane % 3 == 2 && lane < 3 * a.sec_w) stream = 2;
+    sincosf((float)a.rope_position[stream] * a.inv_freq[lane], &cx.rs, &cx.rc);
+  }
+
+  if (w >= NA) persist_layers<true>(a, cx, sm, sp);
+  else persist_layers<false>(a, cx, sm, sp);
 
   // The last workgroup to finish advances the epoch for the next launch.  Every
   // workgroup read the epoch before it produced anything, so none can read the
@@ -590,7 +712,7 @@ __global__ __launch_bounds__(512) void decode_persistent_kernel(const PersistArg
     const unsigned n = __hip_atomic_fetch_add(a.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (n == NB - 1) {
       __hip_atomic_store(a.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(a.epoch, ep + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(a.epoch, cx.ep + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
