@@ -198,7 +198,9 @@ def main() -> int:
     stream = torch.cuda.current_stream()
     mode = eng.step_mode
     if mode == "persistent":
-        ctx = prompt.length + n_dec
+        # fixed context (cache position prompt_len + 4), the one the committed
+        # PMC traffic figures in profiles/persistent_traffic.json were taken at
+        ctx = min(prompt.length + 5, cap)
         eng.set_state(first, ctx - 1, ctx - 1 + prompt.rope_delta)
         eng.layers_persistent()
         torch.cuda.synchronize()
@@ -263,7 +265,9 @@ def main() -> int:
     tfile = REPO / "profiles" / ("persistent_traffic.json" if mode == "persistent" else "gate_up_traffic.json")
     if tfile.exists():
         try:
-            traffic = json.loads(tfile.read_text()).get("bytes_per_launch")
+            tj = json.loads(tfile.read_text())
+            if mode != "persistent" or tj.get("context_rows") == ctx:
+                traffic = tj.get("bytes_per_launch")
         except (ValueError, OSError):
             traffic = None
 
