@@ -399,7 +399,7 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
     *reinterpret_cast<u32x4*>(s_gpost + tid * 8) = gp;
   }
   issue_qkv(a.layers[0]);
-  if (streamer) issue_kvwo(a.layers[0]);
+  issue_kvwo(a.layers[0]);
 
   for (int l = 0; l < a.num_layers; ++l) {
     const PersistLayer& Lw = a.layers[l];
@@ -423,7 +423,6 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
     }
     __syncthreads();
     QD_FRESH_LANE();
-    if (!streamer) issue_kvwo(Lw);
     {
       float y[2];
       rows_dot_norm<4, 2>(wq, s_x, s_gin, lds_rstd<4>(s_x, lane, a.eps), lane, y);
@@ -661,7 +660,11 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
         put(a.x_t + gw, par, v);
         if (l + 1 == a.num_layers) a.x_out[gw] = v;
       }
-      if (!streamer) puts_done();
+      if (!streamer) {
+        puts_done();
+        // the next layer's K/V rows and W_o row: in flight across the x hand-off
+        issue_kvwo(Ln);
+      }
     }
   }
 
