@@ -109,8 +109,21 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
   const int split = blockIdx.x % a.n_split;
   const int slot = threadIdx.x >> 4;
   const int dl = (threadIdx.x & 15) * 8;
+  // sequence of a batch (grid y); every per-sequence pointer is offset here
+  const int bq = blockIdx.y;
+  const TQ* q_in = reinterpret_cast<const TQ*>(a.q) + bq * a.bs_q;
+  const TQ* qkv = reinterpret_cast<const TQ*>(a.qkv) + bq * a.bs_q;
+  const uint16_t* kc = a.k + bq * a.bs_cache;
+  const uint16_t* vc = a.v + bq * a.bs_cache;
+  uint16_t* kw = a.k_w + bq * a.bs_cache;
+  uint16_t* vw = a.v_w + bq * a.bs_cache;
+  const int64_t* rope_pos = a.rope_pos + 3 * bq;
+  const long part0 = (long)bq * a.Hq * a.n_split;
+  float* o_part = a.o_part + part0 * kD;
+  float* lse_out = a.lse + part0;
+  float* q_rot_out = a.q_rot_out == nullptr ? nullptr : a.q_rot_out + (long)bq * a.Hq * kD;
 
-  const long pos = a.cache_position[0];
+  const long pos = a.cache_position[bq];
   long Ll = pos + 1 < (long)a.T ? pos + 1 : (long)a.T;
   if (Ll < 0) Ll = 0;
   const int L = (int)Ll;
@@ -121,8 +134,8 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
   // The cache rows do not depend on the prologue: the first batch of K/V loads
   // is issued before it (the new position, if in this batch, is patched in from
   // LDS afterwards).
-  const uint16_t* kb = a.k + (long)kvh * a.stride_h + dl;
-  const uint16_t* vb = a.v + (long)kvh * a.stride_h + dl;
+  const uint16_t* kb = kc + (long)kvh * a.stride_h + dl;
+  const uint16_t* vb = vc + (long)kvh * a.stride_h + dl;
   // The wave's four slots advance together (trip count uniform per wave).
   const int wave_t0 = t0 + (threadIdx.x / kWave) * 4;
   const int row_off = slot - (threadIdx.x / kWave) * 4;
@@ -135,9 +148,8 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
   if constexpr (FUSED_ROPE) {
     const int w = threadIdx.x / kWave;
     const int j = lane_id();
-    const TQ* qkv = reinterpret_cast<const TQ*>(a.qkv);
     float c, s;
-    mrope_cs(a.rope_pos, a.inv_freq, a.sec_h, a.sec_w, j, c, s);
+    mrope_cs(rope_pos, a.inv_freq, a.sec_h, a.sec_w, j, c, s);
     for (int item = w; item < G + 2; item += 4) {
       if (item < G) {
         const TQ* src = qkv + (long)(kvh * G + item) * kD;
@@ -161,13 +173,13 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
     // the split holding the new position stores it into the static cache
     if (pos >= t0 && pos < t1) {
       const int t = threadIdx.x;
-      uint16_t* dst = (t < kD ? a.k_w : a.v_w) + (long)kvh * a.stride_h + pos * a.stride_s;
+      uint16_t* dst = (t < kD ? kw : vw) + (long)kvh * a.stride_h + pos * a.stride_s;
       dst[t & (kD - 1)] = s_kv[t >> 7][t & (kD - 1)];
     }
     // rotated q for inspection by the host (first split of each kv head)
-    if (split == 0 && a.q_rot_out != nullptr) {
+    if (split == 0 && q_rot_out != nullptr) {
       for (int i = threadIdx.x; i < G * kD; i += blockDim.x)
-        a.q_rot_out[(long)kvh * G * kD + i] = s_q[i / kD][i % kD];
+        q_rot_out[(long)kvh * G * kD + i] = s_q[i / kD][i % kD];
     }
   }
 
@@ -178,7 +190,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) q[g][i] = s_q[g][dl + i];
     } else {
-      load_act8(reinterpret_cast<const TQ*>(a.q), (long)(kvh * G + g) * a.q_stride + dl, q[g]);
+      load_act8(q_in, (long)(kvh * G + g) * a.q_stride + dl, q[g]);
     }
   }
 
@@ -238,8 +250,8 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
       }
     }
     const int h = kvh * G + g;
-    a.o_part[((long)h * a.n_split + split) * kD + d] = den > 0.f ? num / den : 0.f;
-    if (d == 0) a.lse[(long)h * a.n_split + split] = den > 0.f ? M + __logf(den) : -INFINITY;
+    o_part[((long)h * a.n_split + split) * kD + d] = den > 0.f ? num / den : 0.f;
+    if (d == 0) lse_out[(long)h * a.n_split + split] = den > 0.f ? M + __logf(den) : -INFINITY;
   }
 }
 
@@ -257,7 +269,8 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnArgs a) {
   __shared__ float s_red[4];
   const int h = blockIdx.x;
   const int S = a.n_split;
-  const float* lse = a.lse + (long)h * S;
+  const long bq = blockIdx.y;   // sequence of a batch
+  const float* lse = a.lse + (bq * a.Hq + h) * S;
   float mx = -INFINITY;
   for (int s = threadIdx.x; s < S; s += blockDim.x) {
     const float v = lse[s];
@@ -273,7 +286,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnArgs a) {
   __syncthreads();
   const int d = threadIdx.x & (kD - 1);
   const int half = threadIdx.x >> 7;
-  const float* op = a.o_part + (long)h * S * kD + d;
+  const float* op = a.o_part + (bq * a.Hq + h) * S * kD + d;
   float num = 0.f;
   for (int s0 = half; s0 < S; s0 += 2 * kMergeUnroll) {
     float v[kMergeUnroll];
@@ -294,13 +307,13 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnArgs a) {
     float den = 0.f;
     for (int s = 0; s < S; ++s) den += s_w[s];
     num += s_num[d];
-    store_act(reinterpret_cast<TO*>(a.out), (long)h * kD + d, den > 0.f ? num / den : 0.f);
+    store_act(reinterpret_cast<TO*>(a.out), (bq * a.Hq + h) * kD + d, den > 0.f ? num / den : 0.f);
   }
 }
 
 template <typename TQ, bool FUSED>
 static int launch_partial_g(const AttnArgs& a, hipStream_t s) {
-  const dim3 grid((unsigned)(a.Hkv * a.n_split));
+  const dim3 grid((unsigned)(a.Hkv * a.n_split), (unsigned)a.batch);
   switch (a.Hq / a.Hkv) {
     case 1: hipLaunchKernelGGL((attn_partial_kernel<1, TQ, FUSED>), grid, dim3(256), 0, s, a); break;
     case 2: hipLaunchKernelGGL((attn_partial_kernel<2, TQ, FUSED>), grid, dim3(256), 0, s, a); break;
@@ -318,7 +331,7 @@ int attention_partial_launch(const AttnArgs& a, hipStream_t s) {
 template <typename TO>
 int attention_merge_launch(const AttnArgs& a, hipStream_t s) {
   if (a.n_split > kMergeMaxSplits) return QD_ERR_SHAPE;
-  hipLaunchKernelGGL((attn_merge_kernel<TO>), dim3((unsigned)a.Hq), dim3(256), 0, s, a);
+  hipLaunchKernelGGL((attn_merge_kernel<TO>), dim3((unsigned)a.Hq, (unsigned)a.batch), dim3(256), 0, s, a);
   return qd_host::launch_status("attn_merge_kernel");
 }
 

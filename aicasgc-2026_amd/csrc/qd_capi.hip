@@ -371,23 +371,37 @@ struct StepBuffers {
   char* argmax_ws;
   unsigned* tagged;   // persistent step hand-off words
   unsigned* control;  // persistent step: status, epoch, done
+  float* xn;          // batch step: final-norm output [B][H]
+  float* part_val;    // batch step: lm_head argmax partials [V/16][8]
+  long* part_idx;
 };
+
+int batch_of(const qd_model_desc* d) { return d->batch > 1 ? d->batch : 1; }
 
 size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
+// Per-sequence buffers are [B][n] (B = batch, 1 for the batch-1 step).
 bool step_layout(const qd_model_desc* d, int splits, StepBuffers* b, size_t* total) {
+  const size_t B = (size_t)batch_of(d);
   const size_t qkv_rows = (size_t)d->num_heads * d->head_dim + 2 * (size_t)d->num_kv_heads * d->head_dim;
   size_t off = 0;
-  size_t o_x = off; off += align256(4 * (size_t)d->hidden);
-  size_t o_qkv = off; off += align256(4 * qkv_rows);
-  size_t o_q = off; off += align256(4 * (size_t)d->num_heads * d->head_dim);
-  size_t o_a = off; off += align256(4 * (size_t)d->num_heads * d->head_dim);
-  size_t o_r = off; off += align256(4 * (size_t)d->hidden);
-  size_t o_h = off; off += align256(4 * (size_t)d->intermediate);
-  size_t o_aw = off; off += align256(attn_ws_bytes(d->num_heads, d->num_kv_heads, splits));
+  size_t o_x = off; off += align256(4 * B * (size_t)d->hidden);
+  size_t o_qkv = off; off += align256(4 * B * qkv_rows);
+  size_t o_q = off; off += align256(4 * B * (size_t)d->num_heads * d->head_dim);
+  size_t o_a = off; off += align256(4 * B * (size_t)d->num_heads * d->head_dim);
+  size_t o_r = off; off += align256(4 * B * (size_t)d->hidden);
+  size_t o_h = off; off += align256(4 * B * (size_t)d->intermediate);
+  size_t o_aw = off; off += align256(256 + B * (attn_ws_bytes(d->num_heads, d->num_kv_heads, splits) - 256));
   size_t o_gw = off; off += align256(argmax_ws_bytes());
   size_t o_tg = off; off += align256(4 * qd::kPersistTaggedWords);
   size_t o_ct = off; off += 256;
+  size_t o_xn = off, o_pv = off, o_pi = off;
+  if (B > 1) {
+    const size_t groups = (size_t)qd::gemv8_row_groups(d->vocab);
+    o_xn = off; off += align256(4 * B * (size_t)d->hidden);
+    o_pv = off; off += align256(4 * groups * qd::kBatchMax);
+    o_pi = off; off += align256(8 * groups * qd::kBatchMax);
+  }
   *total = off;
   if (b != nullptr) {
     char* base = reinterpret_cast<char*>(d->workspace);
@@ -401,6 +415,9 @@ bool step_layout(const qd_model_desc* d, int splits, StepBuffers* b, size_t* tot
     b->argmax_ws = base + o_gw;
     b->tagged = reinterpret_cast<unsigned*>(base + o_tg);
     b->control = reinterpret_cast<unsigned*>(base + o_ct);
+    b->xn = reinterpret_cast<float*>(base + o_xn);
+    b->part_val = reinterpret_cast<float*>(base + o_pv);
+    b->part_idx = reinterpret_cast<long*>(base + o_pi);
   }
   return true;
 }
@@ -435,6 +452,10 @@ namespace {
 // (empty when it can).
 bool persistent_unsupported(const qd_model_desc* d, char* why, size_t n) {
   why[0] = 0;
+  if (batch_of(d) > 1) {
+    snprintf(why, n, "the persistent step runs batch 1 only (batch %d)", d->batch);
+    return true;
+  }
   if (d->hidden != qd::kPersistHidden || d->num_heads != qd::kPersistHeads ||
       d->num_kv_heads != qd::kPersistKvHeads || d->head_dim != qd::kPersistHeadDim ||
       d->intermediate != qd::kPersistInter) {
@@ -512,6 +533,13 @@ int qd_decode_step_mode(const qd_model_desc* d) {
              d->step_mode);
   if (d->step_mode == QD_STEP_CHAIN) return QD_STEP_CHAIN;
   char why[256];
+  if (batch_of(d) > 1) {
+    if (d->step_mode == QD_STEP_PERSISTENT) {
+      qd_host::set_error("the persistent step runs batch 1 only (batch %d requested)", d->batch);
+      return QD_ERR_SHAPE;
+    }
+    return QD_STEP_CHAIN;
+  }
   if (persistent_unsupported(d, why, sizeof(why))) {
     if (d->step_mode == QD_STEP_PERSISTENT) {
       qd_host::set_error("%s", why);
@@ -522,10 +550,78 @@ int qd_decode_step_mode(const qd_model_desc* d) {
   return QD_STEP_PERSISTENT;
 }
 
+namespace {
+
+// Batch step (batch 2..8): the kernel chain with MFMA batch GEMVs and the
+// split-KV attention run per sequence (grid y), every sequence at its own cache
+// position.
+int batch_step(const qd_model_desc* d, hipStream_t s) {
+  const int B = batch_of(d);
+  QD_REQUIRE(B <= qd::kBatchMax, QD_ERR_SHAPE, "batch %d > %d", B, qd::kBatchMax);
+  QD_REQUIRE(d->hidden == 2048 && d->num_heads * d->head_dim == 2048 &&
+                 (d->intermediate == 2048 || d->intermediate == 6144) && d->vocab % 16 == 0,
+             QD_ERR_SHAPE, "batch step supports H = Hq*D = 2048, I in {2048, 6144}, vocab %% 16 == 0");
+  const int splits = splits_of(d);
+  StepBuffers b;
+  size_t total = 0;
+  step_layout(d, splits, &b, &total);
+  const int H = d->hidden, D = d->head_dim, Hq = d->num_heads, Hkv = d->num_kv_heads, I = d->intermediate;
+  const long qkv_rows = (long)Hq * D + 2L * Hkv * D;
+  int st = QD_OK;
+  if ((st = qd::embed8_launch((const u16*)d->embed, d->token, b.x, H, d->vocab, B, s))) return st;
+  for (int li = 0; li < d->num_layers; ++li) {
+    const qd_layer_weights& w = d->layers[li];
+    qd::Gemv8Args g;
+    g.nseq = B; g.eps = d->eps;
+    g.x = b.x; g.ldx = H; g.gamma = (const u16*)w.input_norm; g.W = (const u16*)w.qkv; g.ldw = H;
+    g.N = qkv_rows; g.K = H; g.y = b.qkv; g.ldy = qkv_rows;
+    if ((st = qd::gemv8_launch(g, true, qd::EPI_STORE, s))) return st;
+    qd::AttnArgs aa;
+    aa.k = (const u16*)w.k_cache; aa.v = (const u16*)w.v_cache; aa.k_w = (u16*)w.k_cache; aa.v_w = (u16*)w.v_cache;
+    aa.stride_h = (long)d->capacity * D; aa.stride_s = D; aa.T = d->capacity; aa.cache_position = d->cache_position;
+    aa.scale = 1.0f / sqrtf((float)D); aa.Hq = Hq; aa.Hkv = Hkv; aa.n_split = splits; aa.out = b.attn;
+    aa.qkv = b.qkv; aa.q_weight = (const u16*)w.q_norm; aa.k_weight = (const u16*)w.k_norm; aa.eps = d->eps;
+    aa.rope_pos = d->rope_position; aa.inv_freq = d->inv_freq; aa.sec_h = d->sec_h; aa.sec_w = d->sec_w;
+    aa.q_rot_out = b.q_rot;
+    aa.batch = B; aa.bs_q = qkv_rows; aa.bs_cache = (long)Hkv * d->capacity * D;
+    attn_ws(b.attn_ws, aa);
+    aa.lse = aa.o_part + (size_t)B * Hq * splits * 128;
+    if ((st = qd::attention_partial_launch<float>(aa, s))) return st;
+    if ((st = qd::attention_merge_launch<float>(aa, s))) return st;
+    qd::Gemv8Args go;
+    go.nseq = B; go.x = b.attn; go.ldx = (long)Hq * D; go.W = (const u16*)w.o_proj; go.ldw = (long)Hq * D;
+    go.N = H; go.K = (long)Hq * D; go.residual = b.x; go.ldr = H; go.y = b.r; go.ldy = H;
+    if ((st = qd::gemv8_launch(go, false, qd::EPI_STORE, s))) return st;
+    qd::Gemv8Args gu;
+    gu.nseq = B; gu.eps = d->eps; gu.x = b.r; gu.ldx = H; gu.gamma = (const u16*)w.post_norm;
+    gu.W = (const u16*)w.gate_up; gu.ldw = H; gu.N = I; gu.up_offset = I; gu.K = H; gu.y = b.hidden; gu.ldy = I;
+    if ((st = qd::gemv8_launch(gu, true, qd::EPI_SILU, s))) return st;
+    qd::Gemv8Args gd;
+    gd.nseq = B; gd.x = b.hidden; gd.ldx = I; gd.W = (const u16*)w.down; gd.ldw = I; gd.N = H; gd.K = I;
+    gd.residual = b.r; gd.ldr = H; gd.y = b.x; gd.ldy = H;
+    if ((st = qd::gemv8_launch(gd, false, qd::EPI_STORE, s))) return st;
+  }
+  // final RMSNorm, tied lm_head, per-sequence argmax
+  if ((st = qd::rmsnorm8_launch(b.x, H, (const u16*)d->final_norm, d->eps, H, b.xn, H, B, s))) return st;
+  qd::Gemv8Args gl;
+  gl.nseq = B; gl.x = b.xn; gl.ldx = H; gl.W = (const u16*)d->embed; gl.ldw = H; gl.N = d->vocab; gl.K = H;
+  gl.y = reinterpret_cast<float*>(d->logits_out); gl.ldy = d->vocab; gl.part_val = b.part_val;
+  gl.part_idx = b.part_idx;
+  if ((st = qd::gemv8_launch(gl, false, qd::EPI_ARGMAX, s))) return st;
+  return qd::argmax8_reduce_launch(b.part_val, b.part_idx, qd::gemv8_row_groups(d->vocab), d->token, B, s);
+}
+
+}  // namespace
+
 int qd_decode_step(const qd_model_desc* d, void* stream) {
   QD_REQUIRE(d, QD_ERR_ARG, "null descriptor");
   const int mode = qd_decode_step_mode(d);
   if (mode < 0) return mode;
+  if (batch_of(d) > 1) {
+    int st = qd_decode_step_phases(d, 0, 0, 0, stream);  // descriptor checks only
+    if (st) return st;
+    return batch_step(d, S(stream));
+  }
   if (mode == QD_STEP_CHAIN) return qd_decode_step_phases(d, 0, d->num_layers, QD_PHASE_ALL, stream);
   int st = qd_decode_step_phases(d, 0, 0, 0, stream);  // descriptor checks only
   if (st) return st;
@@ -575,6 +671,10 @@ int qd_decode_step_phases(const qd_model_desc* d, int first_layer, int n_layers,
              QD_ERR_SHAPE, "unsupported model shape");
   QD_REQUIRE(first_layer >= 0 && n_layers >= 0 && first_layer + n_layers <= d->num_layers, QD_ERR_ARG,
              "layer range [%d, %d) outside the model", first_layer, first_layer + n_layers);
+  QD_REQUIRE(d->batch >= 0 && d->batch <= qd::kBatchMax, QD_ERR_SHAPE, "batch %d outside 0..%d", d->batch,
+             qd::kBatchMax);
+  QD_REQUIRE(batch_of(d) == 1 || (n_layers == 0 && phase_mask == 0), QD_ERR_ARG,
+             "phase-wise execution is batch 1 only (batch %d)", d->batch);
   hipStream_t s = S(stream);
   const int splits = splits_of(d);
   StepBuffers b;
@@ -634,6 +734,32 @@ int qd_decode_advance(const int64_t* token, int64_t* out_tokens, int64_t* counte
   QD_REQUIRE(token && counter && cache_position && rope_position, QD_ERR_ARG, "null pointer");
   return qd::decode_advance_launch(token, out_tokens, counter, cache_position, rope_position, max_tokens,
                                    S(stream));
+}
+
+int qd_decode_advance_batch(const int64_t* token, int64_t* out_tokens, int64_t* counter, int64_t* cache_position,
+                            int64_t* rope_position, int max_tokens, int batch, void* stream) {
+  QD_REQUIRE(token && counter && cache_position && rope_position, QD_ERR_ARG, "null pointer");
+  QD_REQUIRE(batch >= 1 && batch <= qd::kBatchMax, QD_ERR_SHAPE, "batch %d outside 1..%d", batch, qd::kBatchMax);
+  return qd::advance8_launch(token, out_tokens, counter, cache_position, rope_position, max_tokens, batch,
+                             S(stream));
+}
+
+int qd_batch_gemv(const float* x, long ldx, const void* gamma, float eps, const void* W, long ldw, long N, long K,
+                  long up_offset, const float* residual, long ldr, float* y, long ldy, int nseq, int epilogue,
+                  void* stream) {
+  QD_REQUIRE(x && W && y, QD_ERR_ARG, "null pointer");
+  QD_REQUIRE(nseq >= 1 && nseq <= qd::kBatchMax, QD_ERR_SHAPE, "nseq %d outside 1..%d", nseq, qd::kBatchMax);
+  QD_REQUIRE(epilogue == QD_BATCH_EPI_STORE || epilogue == QD_BATCH_EPI_SILU, QD_ERR_ARG, "bad epilogue %d",
+             epilogue);
+  QD_REQUIRE((K == 2048 || K == 6144) && N % 16 == 0 && ldx % 4 == 0 && a16(x) && a16(W) && ldw % 8 == 0,
+             QD_ERR_SHAPE, "need K in {2048, 6144}, N %% 16 == 0 and 16-byte aligned rows");
+  qd::Gemv8Args g;
+  g.x = x; g.ldx = ldx; g.gamma = (const u16*)gamma; g.eps = eps; g.W = (const u16*)W; g.ldw = ldw; g.N = N;
+  g.K = K; g.up_offset = epilogue == QD_BATCH_EPI_SILU ? up_offset : 0; g.residual = residual; g.ldr = ldr;
+  g.y = y; g.ldy = ldy; g.nseq = nseq;
+  if (epilogue == QD_BATCH_EPI_SILU) QD_REQUIRE(up_offset == N, QD_ERR_ARG, "SiLU epilogue: up_offset must equal N");
+  return qd::gemv8_launch(g, gamma != nullptr, epilogue == QD_BATCH_EPI_SILU ? qd::EPI_SILU : qd::EPI_STORE,
+                          S(stream));
 }
 
 }  // extern "C"

@@ -68,6 +68,10 @@ struct AttnArgs {
   uint16_t* k_w = nullptr;            // writable aliases of k / v for the new row
   uint16_t* v_w = nullptr;
   float* q_rot_out = nullptr;         // optional fp32 [Hq, 128] copy of the rotated q
+  // batch (grid y = sequence): per-sequence element strides of q / qkv, of the
+  // caches, of o_part / lse / out / q_rot_out; cache_position[b], rope_pos[3b..]
+  int batch = 1;
+  long bs_q = 0, bs_cache = 0;
 };
 
 // Partials of every (kv head, split); fused prologue when a.qkv != nullptr.
@@ -171,6 +175,41 @@ constexpr size_t kPersistTaggedWords = kPersistHidden                           
                                        + kPersistHidden + kPersistInter;                              // r, hid
 
 int decode_persistent_launch(const PersistArgs& a, hipStream_t s);
+
+// ---------------------------------------------------------------- batch step
+
+constexpr int kBatchMax = 8;
+
+// Batch GEMV y[b][r] = W[r] . x'[b] for b < nseq (x' = RMSNorm(x) * gamma when
+// gamma is given), K in {2048, 6144}, rows a multiple of 16.
+struct Gemv8Args {
+  const float* x = nullptr;        // fp32 [nseq][ldx]
+  long ldx = 0;
+  const uint16_t* gamma = nullptr; // fp16 [K]
+  float eps = 1e-6f;
+  const uint16_t* W = nullptr;     // fp16 [rows][ldw]
+  long ldw = 0;
+  long N = 0;                      // output rows (EPI_SILU: gate rows == up rows == up_offset)
+  long K = 0;
+  long up_offset = 0;
+  const float* residual = nullptr; // fp32 [nseq][ldr] added in EPI_STORE, or null
+  long ldr = 0;
+  float* y = nullptr;              // fp32 [nseq][ldy] (EPI_ARGMAX: optional logits)
+  long ldy = 0;
+  int nseq = 0;
+  float* part_val = nullptr;       // EPI_ARGMAX: [row groups][8]
+  long* part_idx = nullptr;
+};
+
+int gemv8_launch(const Gemv8Args& a, bool norm, int epi, hipStream_t s);
+int gemv8_row_groups(long N);
+int argmax8_reduce_launch(const float* part_val, const long* part_idx, int nblk, int64_t* token, int nseq,
+                          hipStream_t s);
+int rmsnorm8_launch(const float* x, long ldx, const uint16_t* gamma, float eps, int K, float* y, long ldy, int nseq,
+                    hipStream_t s);
+int embed8_launch(const uint16_t* table, const int64_t* token, float* out, int H, long V, int nseq, hipStream_t s);
+int advance8_launch(const int64_t* token, int64_t* out_tokens, int64_t* counter, int64_t* cache_position,
+                    int64_t* rope_position, int max_tokens, int nseq, hipStream_t s);
 // 0 when the device can keep the whole persistent grid resident at once.
 int decode_persistent_check_device(char* why, size_t why_len);
 

@@ -66,6 +66,9 @@ _SIGS = {
     "qd_decode_step_mode": (c_int, [P]),
     "qd_decode_layers_persistent": (c_int, [P, P]),
     "qd_decode_status": (c_int, [P, POINTER(ctypes.c_uint), c_int]),
+    "qd_batch_gemv": (c_int, [P, c_long, P, c_float, P, c_long, c_long, c_long, c_long, P, c_long, P, c_long, c_int,
+                              c_int, P]),
+    "qd_decode_advance_batch": (c_int, [P, P, P, P, P, c_int, c_int, P]),
 }
 
 EXPORTED = tuple(_SIGS)
@@ -131,7 +134,7 @@ ModelDesc._fields_ = [
     ("rope_position", c_void_p),
     ("logits_out", c_void_p),
     ("workspace", c_void_p),
-    ("attn_splits", c_int), ("step_mode", c_int),
+    ("attn_splits", c_int), ("step_mode", c_int), ("batch", c_int),
 ]
 
 __all__ = ["lib", "check", "ptr", "stream", "call", "QD_F16", "QD_F32", "ModelDesc", "LayerDesc", "EXPORTED",

@@ -19,7 +19,7 @@ PKG_ROOT = Path(__file__).resolve().parent.parent          # aicasgc-2026_amd/
 CSRC = PKG_ROOT / "csrc"
 LIB_NAME = "libqwen3vl_decode.so"
 LIB_PATH = PKG_ROOT / LIB_NAME
-SOURCES = ["qd_gemv.hip", "qd_attention.hip", "qd_small_ops.hip", "qd_persistent.hip", "qd_capi.hip"]
+SOURCES = ["qd_gemv.hip", "qd_attention.hip", "qd_small_ops.hip", "qd_persistent.hip", "qd_batch.hip", "qd_capi.hip"]
 ARCH = os.environ.get("QD_OFFLOAD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [

@@ -283,6 +283,158 @@ class DecodeEngine:
         return [first] + rest
 
 
+class BatchDecodeEngine:
+    """Greedy decoding of B (2..8) independent sequences per step (config 4).
+
+    Every sequence has its own static cache rows ``[B, Hkv, T, D]`` per layer
+    and its own cache / rope position, so ragged lengths need no padding.  The
+    step is ``qd_decode_step`` with ``batch = B`` (MFMA batch GEMVs, per-sequence
+    split-KV attention, per-sequence argmax) followed by
+    ``qd_decode_advance_batch``, captured once into a HIP graph.  The reference
+    has no batch decode path (it rejects batch != 1, evaluation_wrapper.py:110-111).
+    """
+
+    def __init__(self, weights: ModelWeights, batch: int, capacity: int, device="cuda", attn_splits: int = 0,
+                 keep_logits: bool = False):
+        if not torch.cuda.is_available():
+            raise RuntimeError("BatchDecodeEngine needs a ROCm GPU")
+        if not 2 <= batch <= 8:
+            raise ValueError("batch must be 2..8")
+        self.device = torch.device(device)
+        if self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
+        self.shape = s = weights.shape
+        self.batch = B = int(batch)
+        self.capacity = int(capacity)
+        self.w = weights if weights.embed_tokens.device == self.device else weights.to(self.device)
+        dev = self.device
+        self.k_caches = [torch.zeros(B, s.num_kv_heads, self.capacity, s.head_dim, dtype=torch.float16, device=dev)
+                         for _ in self.w.layers]
+        self.v_caches = [torch.zeros_like(k) for k in self.k_caches]
+        self.token = torch.zeros(B, dtype=torch.int64, device=dev)
+        self.cache_position = torch.zeros(B, dtype=torch.int64, device=dev)
+        self.rope_position = torch.zeros(B, 3, dtype=torch.int64, device=dev)
+        self.step_counter = torch.zeros(1, dtype=torch.int64, device=dev)
+        self.out_tokens = torch.zeros(1, B, dtype=torch.int64, device=dev)
+        self.inv_freq = rope_inv_freq(s).to(dev)
+        self.logits = torch.empty(B, s.vocab, dtype=torch.float32, device=dev) if keep_logits else None
+        layers = (_lib.LayerDesc * len(self.w.layers))()
+        for i, lw in enumerate(self.w.layers):
+            L = layers[i]
+            L.qkv, L.o_proj = lw.qkv_weight.data_ptr(), lw.o_proj_weight.data_ptr()
+            L.gate_up, L.down = lw.gate_up_weight.data_ptr(), lw.down_proj_weight.data_ptr()
+            L.input_norm, L.post_norm = lw.input_layernorm_weight.data_ptr(), lw.post_attn_layernorm_weight.data_ptr()
+            L.q_norm, L.k_norm = lw.q_norm_weight.data_ptr(), lw.k_norm_weight.data_ptr()
+            L.k_cache, L.v_cache = self.k_caches[i].data_ptr(), self.v_caches[i].data_ptr()
+        self._layers = layers
+        d = _lib.ModelDesc()
+        d.num_layers = len(self.w.layers)
+        d.hidden, d.num_heads, d.num_kv_heads = s.hidden, s.num_heads, s.num_kv_heads
+        d.head_dim, d.intermediate, d.vocab = s.head_dim, s.intermediate, s.vocab
+        d.capacity = self.capacity
+        d.eps = s.rms_eps
+        d.sec_t, d.sec_h, d.sec_w = s.mrope_section
+        d.inv_freq = self.inv_freq.data_ptr()
+        d.layers = ctypes.cast(layers, ctypes.POINTER(_lib.LayerDesc))
+        d.embed = self.w.embed_tokens.data_ptr()
+        d.final_norm = self.w.final_norm_weight.data_ptr()
+        d.token = self.token.data_ptr()
+        d.cache_position = self.cache_position.data_ptr()
+        d.rope_position = self.rope_position.data_ptr()
+        d.logits_out = self.logits.data_ptr() if self.logits is not None else None
+        d.attn_splits = int(attn_splits)
+        d.step_mode = _lib.STEP_CHAIN
+        d.batch = B
+        nbytes = _lib.lib().qd_decode_workspace_bytes(ctypes.byref(d))
+        self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+        d.workspace = self.workspace.data_ptr()
+        self.desc = d
+        self.graph = None
+
+    def set_state(self, tokens, cache_positions, rope_positions) -> None:
+        self.token.copy_(torch.as_tensor(tokens, dtype=torch.int64))
+        self.cache_position.copy_(torch.as_tensor(cache_positions, dtype=torch.int64))
+        rp = torch.as_tensor(rope_positions, dtype=torch.int64).view(-1, 1).expand(self.batch, 3)
+        self.rope_position.copy_(rp)
+
+    def reserve_tokens(self, n: int) -> None:
+        if self.out_tokens.shape[0] < n:
+            self.out_tokens = torch.zeros(n, self.batch, dtype=torch.int64, device=self.device)
+            self.graph = None
+
+    def step_eager(self) -> None:
+        st = ctypes.c_void_p(torch.cuda.current_stream(self.device).cuda_stream)
+        _lib.check(_lib.lib().qd_decode_step(ctypes.byref(self.desc), st), "qd_decode_step (batch)")
+        _lib.check(_lib.lib().qd_decode_advance_batch(
+            ctypes.c_void_p(self.token.data_ptr()), ctypes.c_void_p(self.out_tokens.data_ptr()),
+            ctypes.c_void_p(self.step_counter.data_ptr()), ctypes.c_void_p(self.cache_position.data_ptr()),
+            ctypes.c_void_p(self.rope_position.data_ptr()), int(self.out_tokens.shape[0]), self.batch, st),
+            "qd_decode_advance_batch")
+
+    def capture(self) -> None:
+        """Capture step + advance into a HIP graph (warm-up on a side stream, state restored)."""
+        saved = [t.clone() for t in (self.token, self.cache_position, self.rope_position, self.step_counter)]
+        rows = self._snapshot_rows()
+        side = torch.cuda.Stream(self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(side):
+            self.step_eager()
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        torch.cuda.synchronize(self.device)
+        for t, v in zip((self.token, self.cache_position, self.rope_position, self.step_counter), saved):
+            t.copy_(v)
+        self._restore_rows(rows)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.step_eager()
+        torch.cuda.synchronize(self.device)
+        self.graph = g
+
+    def _snapshot_rows(self):
+        pos = self.cache_position.tolist()
+        snap = []
+        for k, v in zip(self.k_caches, self.v_caches):
+            snap.append([(k[b, :, p].clone(), v[b, :, p].clone()) if 0 <= p < self.capacity else None
+                         for b, p in enumerate(pos)])
+        return pos, snap
+
+    def _restore_rows(self, rows) -> None:
+        pos, snap = rows
+        for (k, v), per in zip(zip(self.k_caches, self.v_caches), snap):
+            for b, (p, kv) in enumerate(zip(pos, per)):
+                if kv is not None:
+                    k[b, :, p].copy_(kv[0])
+                    v[b, :, p].copy_(kv[1])
+
+    def decode(self, first_tokens, start_positions, rope_positions, n_steps: int, use_graph: bool = True):
+        """n_steps greedy steps; returns a [n_steps][B] list of token ids."""
+        if max(int(p) for p in start_positions) + n_steps > self.capacity:
+            raise ValueError("static cache too small for the requested generation")
+        if min(int(t) for t in first_tokens) < 0 or max(int(t) for t in first_tokens) >= self.shape.vocab:
+            raise ValueError("token ids outside the vocabulary")
+        self.reserve_tokens(n_steps)
+        self.set_state(first_tokens, start_positions, rope_positions)
+        self.step_counter.zero_()
+        if use_graph and self.graph is None:
+            self.capture()
+        for _ in range(n_steps):
+            if use_graph:
+                self.graph.replay()
+            else:
+                self.step_eager()
+        torch.cuda.synchronize(self.device)
+        return self.out_tokens[:n_steps].tolist()
+
+
+def roofline_bytes_batch_step(context_lens, shape: Qwen3VLTextShape = QWEN3VL_2B) -> int:
+    """Algorithmic HBM bytes of one batch decode step: every weight once (shared
+    by the batch), K/V[0:L_b] of every layer once per sequence, B embedding rows."""
+    h, i, d = shape.hidden, shape.intermediate, shape.head_dim
+    layer_w = 2 * ((shape.q_size + 2 * shape.kv_size) * h + h * shape.q_size + 3 * i * h) + 2 * (2 * h + 2 * d)
+    kv = 2 * 2 * shape.num_kv_heads * d * int(sum(int(x) for x in context_lens))
+    return shape.num_layers * layer_w + kv * shape.num_layers + 2 * shape.vocab * h + 2 * h + 2 * h * len(context_lens)
+
+
 def _rms(x, w, eps):
     xf = x.float()
     return xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * w.float()

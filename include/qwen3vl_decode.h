@@ -234,6 +234,9 @@ typedef struct qd_model_desc {
   void* workspace;             /* qd_decode_workspace_bytes() bytes, zeroed once */
   int attn_splits;             /* 0 = qd_attention_default_splits(capacity) */
   int step_mode;               /* QD_STEP_AUTO / QD_STEP_CHAIN / QD_STEP_PERSISTENT */
+  int batch;                   /* sequences per step: 0 or 1 = batch 1; 2..8 = batch step, then
+                                  token [B], cache_position [B], rope_position [B][3], each layer's
+                                  k_cache / v_cache [B, Hkv, T, D] and logits_out fp32 [B][V] */
 } qd_model_desc;
 
 /* How qd_decode_step runs the 28 layers.
@@ -302,6 +305,31 @@ int qd_decode_layers_persistent(const qd_model_desc* d, void* stream);
  * completed; bit 0 = a wait exhausted its spin budget, results of that step
  * are invalid) and clears it when reset != 0. */
 int qd_decode_status(const qd_model_desc* d, unsigned* status, int reset);
+
+/* Batch decoding (batch 2..8 in qd_model_desc.batch).  qd_decode_step runs
+ * the batch step: per layer an MFMA batch GEMV (v_mfma_f32_16x16x32_f16; the
+ * activation enters as fp16 value + fp16 rounding residual, so the product is
+ * fp32-accurate) for RMSNorm+QKV, o_proj+residual, RMSNorm+gate_up+SiLU*up and
+ * down+residual, and the split-KV attention with each sequence at its own cache
+ * position; then final RMSNorm, lm_head and an argmax per sequence.  The
+ * reference has no batch path: it rejects batch != 1 in its decode runner
+ * (evaluation_wrapper.py:110-111) and falls back to HF generate; this is the
+ * batch-8 workload of the benchmark configurations (config 4). */
+#define QD_BATCH_EPI_STORE 0   /* y = W x' (+ residual) */
+#define QD_BATCH_EPI_SILU 1    /* y = silu(W_gate x') * (W_up x'), W_up = rows [N, 2N) */
+
+/* Batch GEMV for up to 8 sequences: y[b][r] = W[r] . x'[b] for b < nseq, with
+ * x' = RMSNorm(x[b]) * gamma when gamma != NULL (eps), else x.  x, residual, y
+ * fp32 with row strides ldx / ldr / ldy; W fp16 [rows, ldw]; K in {2048, 6144};
+ * N a multiple of 16; for QD_BATCH_EPI_SILU up_offset == N. */
+int qd_batch_gemv(const float* x, long ldx, const void* gamma, float eps, const void* W, long ldw, long N,
+                  long K, long up_offset, const float* residual, long ldr, float* y, long ldy, int nseq,
+                  int epilogue, void* stream);
+
+/* qd_decode_advance for a batch: out_tokens [max_tokens][batch]. */
+int qd_decode_advance_batch(const int64_t* token, int64_t* out_tokens, int64_t* counter,
+                            int64_t* cache_position, int64_t* rope_position, int max_tokens, int batch,
+                            void* stream);
 
 /* Device-side end of a generation step (single thread):
  *   out_tokens[*counter] = *token (when *counter < max_tokens); ++*counter;

@@ -1,0 +1,209 @@
+"""Batch decoding (config 4 shape: up to 8 sequences, ragged cache positions)
+on the GPU against the oracle.
+
+* the MFMA batch GEMV (qkv / o_proj / gate_up / down shapes, RMSNorm prologue,
+  residual and SiLU*up epilogues, 8 and 5 live sequences) against the oracle's
+  fp32 GEMV per sequence;
+* a 2-layer batch step (real vocabulary tail cut to 8192) with ragged cache
+  positions: logits, greedy tokens and the written K/V rows against the
+  oracle's per-sequence batch-1 steps, eager and as graph replays;
+* the full 28-layer model, 8 sequences, two steps: tokens and logits against
+  the oracle.
+"""
+
+from __future__ import annotations
+
+import types
+
+import pytest
+import torch
+
+from conftest import assert_close_rel
+from oracle import qwen3vl_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _gemv(x, W, gamma, residual, nseq, epi, up_offset, cuda):
+    from qwen3vl_hip import _lib
+
+    N = up_offset if epi == 1 else W.shape[0]
+    K = W.shape[1]
+    xd = x.to(cuda).contiguous()
+    Wd = W.to(cuda).contiguous()
+    gd = gamma.to(cuda).contiguous() if gamma is not None else None
+    rd = residual.to(cuda).contiguous() if residual is not None else None
+    y = torch.full((8, N), float("nan"), dtype=torch.float32, device=cuda)
+    _lib.check(_lib.lib().qd_batch_gemv(
+        _lib.ptr(xd), K, _lib.ptr(gd), ctypes_float(1e-6), _lib.ptr(Wd), K, N, K, up_offset, _lib.ptr(rd),
+        N, _lib.ptr(y), N, nseq, epi, _lib.stream()), "qd_batch_gemv")
+    torch.cuda.synchronize()
+    return y.cpu()
+
+
+def ctypes_float(v):
+    import ctypes
+
+    return ctypes.c_float(v)
+
+
+@pytest.mark.parametrize("name,N,K,norm,resid,silu", [
+    ("qkv", 4096, 2048, True, False, False),
+    ("o_proj", 2048, 2048, False, True, False),
+    ("gate_up", 6144, 2048, True, False, True),
+    ("down", 2048, 6144, False, True, False),
+])
+@pytest.mark.parametrize("nseq", [8, 5])
+def test_batch_gemv_matches_oracle(cuda, name, N, K, norm, resid, silu, nseq):
+    from qwen3vl_hip import synthetic as syn
+
+    print(f"case batch gemv {name} nseq={nseq}", flush=True)
+    rows = 2 * N if silu else N
+    sid = {"qkv": 1, "o_proj": 2, "gate_up": 3, "down": 4}[name]
+    W = syn.normal(31, ("W", sid), (rows, K), std=0.02)
+    x = syn.normal(31, ("x", sid), (8, K), dtype=torch.float32)
+    x[3] *= 40.0      # a row with large values: the rounding residual must carry it
+    gamma = syn.normal(31, ("input_layernorm", sid), (K,), std=0.02, mean=1.0) if norm else None
+    residual = syn.normal(31, ("residual", sid), (8, N), dtype=torch.float32) if resid else None
+    y = _gemv(x, W, gamma, residual, nseq, 1 if silu else 0, N if silu else 0, cuda)
+    for b in range(8):
+        if b >= nseq:
+            assert torch.isnan(y[b]).all(), "rows beyond nseq must not be written"
+            continue
+        xb = O.rms_norm(x[b], gamma, 1e-6) if norm else x[b]
+        ref = O.gemv(xb, W)
+        if silu:
+            ref = O.silu_mul(ref[:N], ref[N:])
+        if resid:
+            ref = ref + residual[b]
+        assert_close_rel(y[b], ref, rel=1e-4, what=f"batch gemv {name} seq {b}")
+
+
+def test_batch_gemv_rejects_bad_shapes(cuda):
+    from qwen3vl_hip import _lib
+
+    z = torch.zeros(8, 1024, device=cuda)
+    W = torch.zeros(64, 1024, dtype=torch.float16, device=cuda)
+    y = torch.zeros(8, 64, device=cuda)
+    st = _lib.lib().qd_batch_gemv(_lib.ptr(z), 1024, None, ctypes_float(1e-6), _lib.ptr(W), 1024, 64, 1024, 0, None,
+                                  64, _lib.ptr(y), 64, 8, 0, _lib.stream())
+    assert st != 0 and "K in" in _lib.last_error()
+    st = _lib.lib().qd_batch_gemv(_lib.ptr(z), 1024, None, ctypes_float(1e-6), _lib.ptr(W), 1024, 64, 2048, 0, None,
+                                  64, _lib.ptr(y), 64, 9, 0, _lib.stream())
+    assert st != 0 and "nseq" in _lib.last_error()
+
+
+VOCAB = 8192
+
+
+@pytest.fixture(scope="module")
+def two_layer_weights():
+    from qwen3vl_hip import synthetic as syn
+    from qwen3vl_hip.config import Qwen3VLTextShape
+
+    return syn.model_weights(17, shape=Qwen3VLTextShape(num_layers=2, vocab=VOCAB))
+
+
+def _fill_caches(eng, positions, seed):
+    from qwen3vl_hip import synthetic as syn
+
+    cap = eng.capacity
+    caches = []
+    for li, (kc, vc) in enumerate(zip(eng.k_caches, eng.v_caches)):
+        k = torch.full((eng.batch, 8, cap, 128), 3.0, dtype=torch.float16)
+        v = torch.full((eng.batch, 8, cap, 128), -3.0, dtype=torch.float16)
+        for b, p in enumerate(positions):
+            if p:
+                k[b, :, :p] = syn.normal(seed, ("k", li, b), (8, p, 128))
+                v[b, :, :p] = syn.normal(seed, ("v", li, b), (8, p, 128))
+        kc.copy_(k)
+        vc.copy_(v)
+        caches.append((k, v))
+    return caches
+
+
+def test_batch_step_two_layers_matches_oracle(cuda, two_layer_weights):
+    from qwen3vl_hip.engine import BatchDecodeEngine
+
+    w = two_layer_weights
+    positions = [5, 17, 0, 63, 100, 33, 1, 77]
+    rope = [p + 11 for p in positions]
+    tokens = [123, 4000, 7, 8191, 55, 1024, 2048, 3]
+    eng = BatchDecodeEngine(w, batch=8, capacity=128, keep_logits=True)
+    caches = _fill_caches(eng, positions, 19)
+    out = eng.decode(tokens, positions, rope, 1, use_graph=False)
+    ref_caches = [(k.clone(), v.clone()) for k, v in caches]
+    logits, toks = O.decode_step_batch(w, tokens, ref_caches, positions, rope, shape=O.OracleShape(num_layers=2,
+                                                                                                    vocab=VOCAB))
+    assert_close_rel(eng.logits.cpu(), logits, what="batch step logits")
+    for li in range(2):
+        for b, p in enumerate(positions):
+            assert_close_rel(eng.k_caches[li][b, :, p].cpu(), ref_caches[li][0][b, :, p].float(),
+                             what=f"K row layer {li} seq {b}")
+            mask = torch.ones(128, dtype=torch.bool)
+            mask[p] = False
+            assert torch.equal(eng.k_caches[li][b, :, mask].cpu(), caches[li][0][b, :, mask])
+    print(f"gpu {out[0]} oracle {toks}", flush=True)
+    assert out[0] == toks
+
+
+def test_batch_graph_generation_matches_oracle(cuda, two_layer_weights):
+    from qwen3vl_hip.engine import BatchDecodeEngine
+
+    w = two_layer_weights
+    positions = [40, 3, 90, 12, 64, 27, 100, 8]
+    tokens = [11, 22, 33, 44, 55, 66, 77, 88]
+    n = 12
+    eng = BatchDecodeEngine(w, batch=8, capacity=128)
+    caches = _fill_caches(eng, positions, 23)
+    got = eng.decode(tokens, positions, positions, n, use_graph=True)
+    ref_caches = [(k.clone(), v.clone()) for k, v in caches]
+    cur, pos, ref = list(tokens), list(positions), []
+    for _ in range(n):
+        _, cur = O.decode_step_batch(w, cur, ref_caches, pos, pos, shape=O.OracleShape(num_layers=2, vocab=VOCAB))
+        ref.append(list(cur))
+        pos = [p + 1 for p in pos]
+    print(f"gpu {got}\noracle {ref}", flush=True)
+    assert got == ref
+
+
+def test_batch_step_partial_batch(cuda, two_layer_weights):
+    """Batch 3: only three sequences are stepped."""
+    from qwen3vl_hip.engine import BatchDecodeEngine
+
+    w = two_layer_weights
+    positions = [7, 50, 21]
+    tokens = [100, 200, 300]
+    eng = BatchDecodeEngine(w, batch=3, capacity=64, keep_logits=True)
+    caches = _fill_caches(eng, positions, 29)
+    out = eng.decode(tokens, positions, positions, 1, use_graph=False)
+    ref_caches = [(k.clone(), v.clone()) for k, v in caches]
+    logits, toks = O.decode_step_batch(w, tokens, ref_caches, positions, positions,
+                                       shape=O.OracleShape(num_layers=2, vocab=VOCAB))
+    assert_close_rel(eng.logits.cpu(), logits, what="batch-3 logits")
+    assert out[0] == toks
+
+
+def test_batch_full_model_two_steps(cuda):
+    from qwen3vl_hip import synthetic as syn
+    from qwen3vl_hip.engine import BatchDecodeEngine
+
+    w = syn.model_weights(3, device=cuda)
+    positions = [150, 37, 220, 96, 5, 180, 64, 128]
+    tokens = [99327, 74931, 74000, 12, 98789, 41501, 65727, 146052]
+    eng = BatchDecodeEngine(w, batch=8, capacity=256, keep_logits=True)
+    caches = _fill_caches(eng, positions, 31)
+    got = eng.decode(tokens, positions, positions, 2, use_graph=True)
+    gpu_logits = eng.logits.cpu()
+    f32 = types.SimpleNamespace(
+        embed_tokens=w.embed_tokens.float().cpu(), final_norm_weight=w.final_norm_weight.float().cpu(),
+        layers=[{k: v.float().cpu() for k, v in lw.tensors().items()} for lw in w.layers])
+    ref_caches = [(k.clone(), v.clone()) for k, v in caches]
+    cur, pos, ref, logits = list(tokens), list(positions), [], None
+    for _ in range(2):
+        logits, cur = O.decode_step_batch(f32, cur, ref_caches, pos, pos)
+        ref.append(list(cur))
+        pos = [p + 1 for p in pos]
+    assert_close_rel(gpu_logits, logits, what="28-layer batch logits (second step)")
+    print(f"gpu {got}\noracle {ref}", flush=True)
+    assert got == ref
