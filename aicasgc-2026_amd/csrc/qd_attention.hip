@@ -307,7 +307,11 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnArgs a) {
     float den = 0.f;
     for (int s = 0; s < S; ++s) den += s_w[s];
     num += s_num[d];
-    store_act(reinterpret_cast<TO*>(a.out), (bq * a.Hq + h) * kD + d, den > 0.f ? num / den : 0.f);
+    const float o = den > 0.f ? num / den : 0.f;
+    if (a.out_img != nullptr)
+      bimg_store(a.out_img, (int)bq, (long)h * kD + d, o);
+    else
+      store_act(reinterpret_cast<TO*>(a.out), (bq * a.Hq + h) * kD + d, o);
   }
 }
 

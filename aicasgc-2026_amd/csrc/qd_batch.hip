@@ -1,22 +1,31 @@
 // Batch-8 decode GEMVs on MFMA (gfx950 v_mfma_f32_16x16x32_f16), plus the
-// batch step's small kernels (final RMSNorm, per-sequence argmax, embedding
+// batch step's small kernels (operand images, per-sequence argmax, embedding
 // rows, position advance).
 //
-// y[b][r] = W[r] . x[b] for the 8 sequences of a decode batch.  A workgroup
-// (8 waves) owns 16 rows (the MFMA M dimension; 16 gate + 16 up rows for the
-// SiLU epilogue); wave w owns the K slice [w K/8, (w+1) K/8) and walks it in
-// 32-wide K tiles.  Per tile and lane: one 16-byte load of W (row = lane % 16,
-// k = 8 (lane / 16) .. +8: exactly the A operand of the MFMA) and the B
-// operand for batch column n = lane % 16 built from x in registers:
-//   n < 8  : fp16(x[n][k])                      (the value, rounded)
-//   n >= 8 : fp16(x[n-8][k] - fp16(x[n-8][k]))  (the rounding residual)
-// so C[r][n] + C[r][n+8] = W[r] . x[n] with the activation carried to ~22
-// bits: the 16 MFMA columns hold the 8 sequences twice over instead of being
-// padding.  The K-slice partials of the 8 waves are summed through LDS.
+// y[b][r] = f[b] (W[r] . u[b]) for the (up to) 8 sequences of a decode batch.
+// The activation u enters as its operand image (qd_common.h): per K tile of 32
+// and lane, one 16-byte load gives the lane's 8 B-operand values, fp16 value
+// columns 0..7 and fp16 rounding-residual columns 8..15, so C[r][n] + C[r][n+8]
+// = W[r] . u[n] with u carried to ~22 bits.  The producer of an activation
+// writes the image in its epilogue, already multiplied by the consumer's
+// RMSNorm weight and by a per-sequence scale s that keeps it in fp16 range;
+// the consumer's factor f = rstd / s applies the RMSNorm, rstd coming from
+// per-row-group partial sums of squares written by the same producer.
 //
-// The weights are loaded once per batch step (every weight byte serves all 8
-// sequences), which is what makes batch decoding cheaper per token than batch 1;
-// the work stays bound by HBM (16 flops per 2-byte weight).
+// A workgroup (8 waves) owns 16 rows (the MFMA M dimension; 16 gate + 16 up
+// rows for the SiLU epilogue) and a K range of KW (1024, 2048 or 3072); wave w owns
+// the slice [w KW/8, (w+1) KW/8) and keeps its image tiles in registers.  W is
+// loaded in coalesced 128-byte row pieces and moved into the MFMA A layout
+// (row lane % 16, k 8 (lane / 16) .. +8) with ds_bpermute: loading the A layout
+// directly would make every lane of a load touch a different row.  The 8
+// K-slice partials are summed through LDS.  When K > KW the
+// row group's K ranges run in separate workgroups (grid y); each publishes its
+// partial and the last to arrive sums them in a fixed order and runs the
+// epilogue.  The lm_head (EPI_ARGMAX) grid loops over row groups, loading the
+// next group's weights before it reduces the current one.
+//
+// Weights are loaded once per batch step (every weight byte serves all 8
+// sequences); the work is bound by HBM (16 flops per 2-byte weight).
 
 #include <float.h>
 #include <math.h>
@@ -30,167 +39,320 @@ namespace {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 
-constexpr int kB = kBatchMax;   // sequences per batch step (8)
-constexpr int kRG = 16;         // rows per workgroup (MFMA M)
-constexpr int kWaves = 8;       // K slices per workgroup
-constexpr int kKT = 32;         // K per MFMA
+constexpr int kB = kBatchMax;     // sequences per batch step (8)
+constexpr int kRG = 16;           // rows per row group (MFMA M)
+constexpr int kWaves = 8;         // K slices per workgroup
+constexpr int kKT = 32;           // K per MFMA
+constexpr int kOut = kRG * kB;    // outputs of one row group
 
-// row_ror:8 within each 16-lane row: lane i reads lane i ^ 8.
-__device__ __forceinline__ float swap8(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xf, 0xf,
-                                                               false));
+// Agent-coherent float store / load (written through to, and read past, the
+// XCD-private L2), and a wait for this thread's outstanding memory operations.
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void stores_done() { __builtin_amdgcn_s_waitcnt(0x0f70); }   // vmcnt(0)
+
+// Lane permutation of a 16-byte register quad: lane d receives lane addr/4's.
+__device__ __forceinline__ u32x4 bpermute4(int addr, const u32x4& v) {
+  return u32x4{(unsigned)__builtin_amdgcn_ds_bpermute(addr, (int)v.x), (unsigned)__builtin_amdgcn_ds_bpermute(addr, (int)v.y),
+               (unsigned)__builtin_amdgcn_ds_bpermute(addr, (int)v.z), (unsigned)__builtin_amdgcn_ds_bpermute(addr, (int)v.w)};
 }
 
-// B operand of this lane for K offset k: 8 values of x[seq][k..k+8] (optionally
-// RMS-normalised), as their fp16 value (lo == false) or fp16 rounding residual.
-template <bool NORM>
-__device__ __forceinline__ h8 b_operand(const float* xrow, const uint16_t* gamma, float rstd, int k, bool lo) {
-  const f32x4 a = *reinterpret_cast<const f32x4*>(xrow + k);
-  const f32x4 b = *reinterpret_cast<const f32x4*>(xrow + k + 4);
-  float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-  if constexpr (NORM) {
-    float g[8];
-    unpack8(ld16(gamma + k), g);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = (v[i] * rstd) * g[i];
-  }
-  h8 r;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const _Float16 hi = (_Float16)v[i];
-    r[i] = lo ? (_Float16)(v[i] - (float)hi) : hi;
-  }
-  return r;
+// rstd of sequence seq from `parts` partial sums of squares ([parts][8]) over
+// n elements; every lane of the calling wave gets the same value.
+__device__ __forceinline__ float seq_rstd(const float* ss, int parts, int seq, float n, float eps) {
+  float q = 0.f;
+  for (int p = lane_id(); p < parts; p += kWave) q += ss[(long)p * kB + seq];
+  return rsqrtf(wave_sum(q) / n + eps);
 }
 
-// rsqrt(mean(x[w]^2) + eps) of sequence w into s_rstd[w] (one wave per sequence).
-template <int K>
-__device__ __forceinline__ void batch_rstd(const float* x, long ldx, float eps, int nseq, float* s_rstd) {
-  const int w = threadIdx.x / kWave;
-  const int lane = lane_id();
-  if (w < nseq) {
-    const float* row = x + (long)w * ldx;
-    float ss = 0.f;
-#pragma unroll 4
-    for (int k = lane * 4; k < K; k += kWave * 4) {
-      const f32x4 v = *reinterpret_cast<const f32x4*>(row + k);
-      ss = __builtin_fmaf(v.x, v.x, ss);
-      ss = __builtin_fmaf(v.y, v.y, ss);
-      ss = __builtin_fmaf(v.z, v.z, ss);
-      ss = __builtin_fmaf(v.w, v.w, ss);
-    }
-    ss = wave_sum(ss);
-    if (lane == 0) s_rstd[w] = rsqrtf(ss / (float)K + eps);
-  }
-}
-
-// One wave: the MFMA sum of its K slice for 16 rows of W (and of W_up).
-template <int K, bool NORM, bool DUAL>
-__device__ __forceinline__ void slice_mfma(const Gemv8Args& a, const float* s_rstd, long r0, f32x4& acc,
-                                           f32x4& acc2) {
-  constexpr int KS = K / kWaves;
+template <int KW, int EPI>
+__global__ __launch_bounds__(512) void gemv8_kernel(const Gemv8Args a) {
+  constexpr int KS = KW / kWaves;
   constexpr int NT = KS / kKT;
-  const int w = threadIdx.x / kWave;
+  constexpr bool DUAL = EPI == EPI_SILU;
+  constexpr bool ARGMAX = EPI == EPI_ARGMAX;
+  constexpr int NA = DUAL ? 2 : 1;
+  constexpr int NW2 = DUAL ? NT : 1;
+  __shared__ float s_fac[kB], s_osc[kB];
+  __shared__ float s_part[NA][kWaves][kB][kRG];
+  __shared__ int s_last;
+
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int lane = lane_id();
   const int m = lane & 15;
   const int kg = (lane >> 4) * 8;
-  const int kb = w * KS;
-  const uint16_t* wrow = a.W + (r0 + m) * a.ldw + kb + kg;
-  const uint16_t* wrow2 = a.W + (r0 + a.up_offset + m) * a.ldw + kb + kg;
-  u32x4 wt[NT], wt2[DUAL ? NT : 1];
-#pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    wt[t] = ld_stream(wrow + t * kKT);
-    if constexpr (DUAL) wt2[t] = ld_stream(wrow2 + t * kKT);
-  }
-  const int seq = m & 7;
-  const bool lo = m >= 8;
-  const bool live = seq < a.nseq;
-  const float* xrow = a.x + (long)(live ? seq : 0) * a.ldx;
-  const float rstd = NORM ? s_rstd[live ? seq : 0] : 1.f;
-  acc = f32x4{0.f, 0.f, 0.f, 0.f};
-  acc2 = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    h8 bop = b_operand<NORM>(xrow, a.gamma, rstd, kb + kg + t * kKT, lo);
-    if (!live) bop = h8{};
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, wt[t]), bop, acc, 0, 0, 0);
-    if constexpr (DUAL)
-      acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, wt2[t]), bop, acc2, 0, 0, 0);
-  }
-}
-
-// C[r][n] + C[r][n+8] for the lanes holding n < 8, written as the wave's
-// partial into part[w][row][seq].
-__device__ __forceinline__ void slice_partial(const f32x4& acc, float (*part)[kRG][kB]) {
-  const int w = threadIdx.x / kWave;
-  const int lane = lane_id();
-  const int n = lane & 15;
-  const int g = lane >> 4;
-  const float c[4] = {acc.x, acc.y, acc.z, acc.w};
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const float v = c[j] + swap8(c[j]);
-    if (n < kB) part[w][4 * g + j][n] = v;
-  }
-}
-
-template <int K, bool NORM, int EPI>
-__global__ __launch_bounds__(512) void gemv8_kernel(const Gemv8Args a) {
-  __shared__ float s_rstd[kB];
-  __shared__ float s_part[kWaves][kRG][kB];
-  __shared__ float s_part2[(EPI == EPI_SILU) ? kWaves : 1][kRG][kB];
-  const long r0 = (long)blockIdx.x * kRG;
-  if constexpr (NORM) {
-    batch_rstd<K>(a.x, a.ldx, a.eps, a.nseq, s_rstd);
-    __syncthreads();
-  }
-  f32x4 acc, acc2;
-  slice_mfma<K, NORM, EPI == EPI_SILU>(a, s_rstd, r0, acc, acc2);
-  slice_partial(acc, s_part);
-  if constexpr (EPI == EPI_SILU) slice_partial(acc2, s_part2);
-  __syncthreads();
   const int t = threadIdx.x;
-  const int rl = t / kB;
-  const int seq = t % kB;
-  const long row = r0 + rl;
-  float v = 0.f;
-  if (t < kRG * kB) {
+  const long kb = (long)blockIdx.y * KW + (long)w * KS;
+  const long rows = DUAL ? a.up_offset : a.N;
+  const int nrg = (int)(rows / kRG);
+
+  // Weight loads are coalesced 128-byte row pieces: for the tile pair (2j, 2j+1)
+  // (64 K values) load h covers rows 8h..8h+7 with 8 lanes x 16 bytes per row
+  // (lane: row 8h + lane / 8, k 8 (lane % 8)).  pair_to_mfma() moves the pair
+  // into the MFMA A layout with ds_bpermute (lane d = row r + 16 c of tile 2j+q
+  // takes row r, k 32q + 8c: load r / 8, source lane 8 (r % 8) + 4q + c).
+  static_assert(NT % 2 == 0, "tile pairs");
+  auto load_w = [&](int rg, u32x4 (&wt)[NT], u32x4 (&wt2)[NW2]) {
+    const uint16_t* p = a.W + ((long)rg * kRG + (lane >> 3)) * a.ldw + kb + (lane & 7) * 8;
+    const long h8row = 8 * a.ldw;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) v += s_part[w][rl][seq];
+    for (int i = 0; i < NT; i += 2) {
+      wt[i] = ld_stream(p + i * kKT);
+      wt[i + 1] = ld_stream(p + h8row + i * kKT);
+    }
+    if constexpr (DUAL) {
+      const uint16_t* p2 = p + a.up_offset * a.ldw;
+#pragma unroll
+      for (int i = 0; i < NT; i += 2) {
+        wt2[i] = ld_stream(p2 + i * kKT);
+        wt2[i + 1] = ld_stream(p2 + h8row + i * kKT);
+      }
+    }
+  };
+  const int src0 = (8 * (m & 7) + (lane >> 4)) * 4;   // byte lane addresses for ds_bpermute
+  const int src1 = src0 + 16;
+  const bool upper = m >= 8;
+  auto pair_to_mfma = [&](const u32x4& l0, const u32x4& l1, u32x4& t0, u32x4& t1) {
+    const u32x4 a0 = bpermute4(src0, l0), b0 = bpermute4(src0, l1);
+    const u32x4 a1 = bpermute4(src1, l0), b1 = bpermute4(src1, l1);
+    t0 = upper ? b0 : a0;
+    t1 = upper ? b1 : a1;
+  };
+
+  int rg = blockIdx.x;
+  u32x4 wt[NT], wt2[NW2];
+  load_w(rg, wt, wt2);
+  // the wave's image tiles: read once (L2-resident), used for every row group
+  u32x4 bt[NT];
+  {
+    const u32x4* src = reinterpret_cast<const u32x4*>(a.xb) + (kb / kKT) * kWave + lane;
+#pragma unroll
+    for (int i = 0; i < NT; ++i) bt[i] = src[i * kWave];
   }
-  if constexpr (EPI == EPI_SILU) {
-    if (t < kRG * kB && seq < a.nseq) {
-      float u = 0.f;
+  // wave w: factors of sequence w
+  {
+    float f = 1.f, o = 1.f;
+    if (a.in_ss != nullptr) f = seq_rstd(a.in_ss, a.in_parts, w, (float)a.K, a.eps);
+    if (a.in_scale != nullptr) f /= a.in_scale[w];
+    if (w >= a.nseq) f = 0.f;
+    if (a.pre_ss != nullptr) o = seq_rstd(a.pre_ss, a.pre_parts, w, (float)a.N, a.eps);
+    if (lane == 0) {
+      s_fac[w] = f;
+      s_osc[w] = o;
+    }
+  }
+  const int rl = t & 15;    // epilogue thread: row rl of the group, sequence seq
+  const int seq = (t >> 4) & (kB - 1);
+  const bool live = seq < a.nseq;
+  float best = -INFINITY;
+  int best_i = 0x7fffffff;
+
+  for (;;) {
+    const int nxt = rg + (int)gridDim.x;
+    u32x4 wn[ARGMAX ? NT : 1], wn2[1];
+    if constexpr (ARGMAX) {
+      if (nxt < nrg) load_w(nxt, wn, wn2);
+    }
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f}, acc2 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) u += s_part2[w][rl][seq];
-      a.y[(long)seq * a.ldy + row] = (v / (1.0f + __expf(-v))) * u;
+    for (int i = 0; i < NT; i += 2) {
+      u32x4 t0, t1;
+      pair_to_mfma(wt[i], wt[i + 1], t0, t1);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, t0), __builtin_bit_cast(h8, bt[i]), acc, 0, 0,
+                                                   0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, t1), __builtin_bit_cast(h8, bt[i + 1]), acc,
+                                                   0, 0, 0);
+      if constexpr (DUAL) {
+        pair_to_mfma(wt2[i], wt2[i + 1], t0, t1);
+        acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, t0), __builtin_bit_cast(h8, bt[i]), acc2,
+                                                      0, 0, 0);
+        acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, t1), __builtin_bit_cast(h8, bt[i + 1]),
+                                                      acc2, 0, 0, 0);
+      }
     }
-  } else if constexpr (EPI == EPI_ARGMAX) {
-    // per-sequence (max, first index) over the workgroup's 16 rows
-    __shared__ float s_v[kRG][kB];
-    if (t < kRG * kB) {
-      s_v[rl][seq] = v;
-      if (a.y != nullptr && seq < a.nseq) a.y[(long)seq * a.ldy + row] = v;
-    }
-    __syncthreads();
-    if (t < kB) {
-      float bv = s_v[0][t];
-      long bi = r0;
-      for (int r = 1; r < kRG; ++r) {
-        if (s_v[r][t] > bv) {
-          bv = s_v[r][t];
-          bi = r0 + r;
+    {
+      // lanes n < 8 of each 16-lane row: C[r][n] + C[r][n+8], rows 4 (lane / 16) + j
+      const int g = lane >> 4;
+      const float c[4] = {acc.x, acc.y, acc.z, acc.w};
+      const float c2[4] = {acc2.x, acc2.y, acc2.z, acc2.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float v = c[j] + dpp<kDppRowRor8>(c[j]);
+        if (m < kB) s_part[0][w][m][4 * g + j] = v;
+        if constexpr (DUAL) {
+          const float v2 = c2[j] + dpp<kDppRowRor8>(c2[j]);
+          if (m < kB) s_part[NA - 1][w][m][4 * g + j] = v2;
         }
       }
-      a.part_val[(long)blockIdx.x * kB + t] = bv;
-      a.part_idx[(long)blockIdx.x * kB + t] = bi;
     }
+    __syncthreads();
+    float v = 0.f, v2 = 0.f;
+    if (t < kOut) {
+#pragma unroll
+      for (int q = 0; q < kWaves; ++q) v += s_part[0][q][seq][rl];
+      if constexpr (DUAL) {
+#pragma unroll
+        for (int q = 0; q < kWaves; ++q) v2 += s_part[NA - 1][q][seq][rl];
+      }
+    }
+    if constexpr (!ARGMAX) {
+      if (a.ksplit > 1) {
+        // publish this K range's partials (coherent stores, completed before the
+        // arrival count); the last workgroup of the row group sums them in K order
+        float* kp = a.kpart + (long)rg * a.ksplit * (NA * kOut);
+        if (t < kOut) {
+          store_coherent(kp + (long)blockIdx.y * (NA * kOut) + t, v);
+          if constexpr (DUAL) store_coherent(kp + (long)blockIdx.y * (NA * kOut) + kOut + t, v2);
+        }
+        stores_done();
+        __syncthreads();
+        if (t == 0) {
+          const unsigned old = __hip_atomic_fetch_add(a.kcount + rg, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          const int last = old == (unsigned)(a.ksplit - 1);
+          if (last) __hip_atomic_store(a.kcount + rg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          s_last = last;
+        }
+        __syncthreads();
+        if (!s_last) return;
+        if (t < kOut) {
+          v = 0.f;
+          v2 = 0.f;
+          for (int q = 0; q < a.ksplit; ++q) {
+            v += load_coherent(kp + (long)q * (NA * kOut) + t);
+            if constexpr (DUAL) v2 += load_coherent(kp + (long)q * (NA * kOut) + kOut + t);
+          }
+        }
+      }
+    }
+    if (t < kOut) {
+      const long row = (long)rg * kRG + rl;
+      v *= s_fac[seq];
+      if constexpr (ARGMAX) {
+        if (a.y != nullptr && live) a.y[(long)seq * a.ldy + row] = v;
+        // (max, first row) over the group's 16 rows: 16 consecutive lanes
+        float bv = v;
+        int bi = (int)row;
+#pragma unroll
+        for (int off = 1; off < 16; off <<= 1) {
+          const float ov = __shfl_xor(bv, off);
+          const int oi = __shfl_xor(bi, off);
+          if (ov > bv || (ov == bv && oi < bi)) {
+            bv = ov;
+            bi = oi;
+          }
+        }
+        if (bv > best) {   // row groups ascend: ties keep the earlier row
+          best = bv;
+          best_i = bi;
+        }
+      } else {
+        if constexpr (DUAL) {
+          v2 *= s_fac[seq];
+          v = (v / (1.0f + __expf(-v))) * v2;
+        } else {
+          if (a.residual != nullptr && live) v += a.residual[(long)seq * a.ldr + row];
+        }
+        if (!live) v = 0.f;
+        if (a.y != nullptr && live) a.y[(long)seq * a.ldy + row] = v;
+        if (a.yb != nullptr)
+          bimg_store(a.yb, seq, row, v * (a.yb_gamma != nullptr ? h2f(a.yb_gamma[row]) : 1.f) * s_osc[seq]);
+        if (a.yss != nullptr) {
+          const float q = row16_sum(v * v);
+          if (rl == 0) a.yss[(long)rg * kB + seq] = q;
+        }
+        if (a.out_scale != nullptr && rg == 0 && rl == 0) a.out_scale[seq] = s_osc[seq];
+      }
+    }
+    if constexpr (!ARGMAX) {
+      break;
+    } else {
+      if (nxt >= nrg) break;
+      __syncthreads();   // s_part is rewritten by the next group
+#pragma unroll
+      for (int i = 0; i < NT; ++i) wt[i] = wn[i];
+      rg = nxt;
+    }
+  }
+  if constexpr (ARGMAX) {
+    if (t < kOut && rl == 0) {
+      a.part_val[(long)blockIdx.x * kB + seq] = best;
+      a.part_idx[(long)blockIdx.x * kB + seq] = best_i;
+    }
+  }
+}
+
+// Image of 8 consecutive values u[0..7] at K index k0 (k0 % 8 == 0): one
+// 16-byte store for the value column, one for the residual column.
+__device__ __forceinline__ void bimg_store8(uint16_t* img, int seq, long k0, const float* u) {
+  unsigned hi[4], lo[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const _Float16 h0 = (_Float16)u[2 * i], h1 = (_Float16)u[2 * i + 1];
+    const _Float16 l0 = (_Float16)(u[2 * i] - (float)h0), l1 = (_Float16)(u[2 * i + 1] - (float)h1);
+    hi[i] = (unsigned)__builtin_bit_cast(uint16_t, h0) | ((unsigned)__builtin_bit_cast(uint16_t, h1) << 16);
+    lo[i] = (unsigned)__builtin_bit_cast(uint16_t, l0) | ((unsigned)__builtin_bit_cast(uint16_t, l1) << 16);
+  }
+  *reinterpret_cast<u32x4*>(img + bimg_index(seq, k0)) = u32x4{hi[0], hi[1], hi[2], hi[3]};
+  *reinterpret_cast<u32x4*>(img + bimg_index(seq + 8, k0)) = u32x4{lo[0], lo[1], lo[2], lo[3]};
+}
+
+// Block-wide (256 threads) sum, uniform in every thread.
+__device__ __forceinline__ float block256_sum(float v, float* s_red) {
+  v = wave_sum(v);
+  if (lane_id() == 0) s_red[threadIdx.x / kWave] = v;
+  __syncthreads();
+  const float r = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+  __syncthreads();
+  return r;
+}
+
+// Image of u = x * gamma * s (s = rstd(x) when norm, else 1), with ss[seq] =
+// sum of x^2 and scale[seq] = s; one block per sequence column (zeros beyond
+// nseq).  Rows are fp32 x[seq] (TX float) or the fp16 embedding rows of
+// token[seq] (TX uint16_t, also copied to x_out as fp32).
+template <typename TX>
+__global__ __launch_bounds__(256) void bimage8_kernel(const TX* x, long ldx, const int64_t* token, long V,
+                                                      const uint16_t* gamma, bool norm, float eps, int K, int nseq,
+                                                      float* x_out, uint16_t* img, float* ss, float* scale) {
+  __shared__ float s_red[4];
+  const int seq = blockIdx.x;
+  const bool live = seq < nseq;
+  const TX* row = x;
+  if constexpr (sizeof(TX) == 2) {
+    long tk = live ? token[seq] : 0;
+    if (tk < 0 || tk >= V) tk = 0;
+    row = x + tk * (long)K;
   } else {
-    if (t < kRG * kB && seq < a.nseq) {
-      if (a.residual != nullptr) v += a.residual[(long)seq * a.ldr + row];
-      a.y[(long)seq * a.ldy + row] = v;
+    row = x + (long)seq * ldx;
+  }
+  float q = 0.f;
+  for (int k = threadIdx.x * 8; k < K; k += 256 * 8) {
+    float u[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (live) load_act8<TX>(row, k, u);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) q = __builtin_fmaf(u[i], u[i], q);
+  }
+  q = block256_sum(q, s_red);
+  const float s = norm ? rsqrtf(q / (float)K + eps) : 1.f;
+  for (int k = threadIdx.x * 8; k < K; k += 256 * 8) {
+    float u[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (live) load_act8<TX>(row, k, u);
+    if (x_out != nullptr && live) {
+      float4* o = reinterpret_cast<float4*>(x_out + (long)seq * K + k);
+      o[0] = float4{u[0], u[1], u[2], u[3]};
+      o[1] = float4{u[4], u[5], u[6], u[7]};
     }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) u[i] *= (gamma != nullptr ? h2f(gamma[k + i]) : 1.f) * s;
+    bimg_store8(img, seq, k, u);
+  }
+  if (threadIdx.x == 0) {
+    if (ss != nullptr) ss[seq] = q;
+    if (scale != nullptr) scale[seq] = s;
   }
 }
 
@@ -225,31 +387,8 @@ __global__ __launch_bounds__(256) void argmax8_reduce_kernel(const float* part_v
     }
     __syncthreads();
   }
-  if (threadIdx.x == 0) token[seq] = r_i[0] == 0x7fffffffffffL ? 0 : r_i[0];
-}
-
-// y[b] = rmsnorm(x[b]) * gamma (fp32), one block per sequence.
-__global__ __launch_bounds__(256) void rmsnorm8_kernel(const float* x, long ldx, const uint16_t* gamma, float eps,
-                                                       int K, float* y, long ldy) {
-  __shared__ float s_red[4];
-  const float* row = x + (long)blockIdx.x * ldx;
-  float ss = 0.f;
-  for (int k = threadIdx.x; k < K; k += blockDim.x) ss = __builtin_fmaf(row[k], row[k], ss);
-  ss = wave_sum(ss);
-  if (lane_id() == 0) s_red[threadIdx.x / kWave] = ss;
-  __syncthreads();
-  const float rstd = rsqrtf((s_red[0] + s_red[1] + s_red[2] + s_red[3]) / (float)K + eps);
-  for (int k = threadIdx.x; k < K; k += blockDim.x)
-    y[(long)blockIdx.x * ldy + k] = (row[k] * rstd) * h2f(gamma[k]);
-}
-
-// x[b] = embed[token[b]] (fp32), one block per sequence.
-__global__ __launch_bounds__(256) void embed8_kernel(const uint16_t* table, const int64_t* token, float* out,
-                                                     int H, long V) {
-  long t = token[blockIdx.x];
-  if (t < 0 || t >= V) t = 0;
-  const uint16_t* row = table + t * (long)H;
-  for (int i = threadIdx.x; i < H; i += blockDim.x) out[(long)blockIdx.x * H + i] = h2f(row[i]);
+  // no finite maximum anywhere (all partials -inf / NaN): token 0
+  if (threadIdx.x == 0) token[seq] = r_i[0] >= 0x7fffffffL ? 0 : r_i[0];
 }
 
 // Per sequence: out_tokens[counter][b] = token[b] (while counter < max_tokens),
@@ -269,49 +408,59 @@ __global__ void advance8_kernel(const int64_t* token, int64_t* out_tokens, int64
   if (b == 0) counter[0] = c + 1;
 }
 
-template <int K, bool NORM, int EPI>
-int launch8(const Gemv8Args& a, hipStream_t s) {
-  const long rows = (EPI == EPI_SILU) ? a.up_offset : a.N;
-  const unsigned grid = (unsigned)((rows + kRG - 1) / kRG);
-  hipLaunchKernelGGL((gemv8_kernel<K, NORM, EPI>), dim3(grid), dim3(kWaves * kWave), 0, s, a);
+template <int KW, int EPI>
+int launch8(const Gemv8Args& a, unsigned gx, hipStream_t s) {
+  hipLaunchKernelGGL((gemv8_kernel<KW, EPI>), dim3(gx, (unsigned)a.ksplit), dim3(kWaves * kWave), 0, s, a);
   return qd_host::launch_status("gemv8_kernel");
 }
 
 }  // namespace
 
-int gemv8_launch(const Gemv8Args& a, bool norm, int epi, hipStream_t s) {
-  if (a.nseq < 1 || a.nseq > kB) return QD_ERR_SHAPE;
+int gemv8_launch(const Gemv8Args& a, int epi, hipStream_t s) {
+  if (a.nseq < 1 || a.nseq > kB || a.ksplit < 1 || a.K % a.ksplit != 0 || a.xb == nullptr) return QD_ERR_SHAPE;
   const long rows = (epi == EPI_SILU) ? a.up_offset : a.N;
-  if (rows % kRG != 0 || a.ldx % 4 != 0) return QD_ERR_SHAPE;
-#define QD_G8(KK)                                                                   \
-  if (a.K == KK) {                                                                  \
-    if (epi == EPI_SILU) return norm ? launch8<KK, true, EPI_SILU>(a, s) : launch8<KK, false, EPI_SILU>(a, s); \
-    if (epi == EPI_ARGMAX) return norm ? launch8<KK, true, EPI_ARGMAX>(a, s) : launch8<KK, false, EPI_ARGMAX>(a, s); \
-    return norm ? launch8<KK, true, EPI_STORE>(a, s) : launch8<KK, false, EPI_STORE>(a, s); \
+  if (rows % kRG != 0 || rows <= 0) return QD_ERR_SHAPE;
+  const long KW = a.K / a.ksplit;
+  const unsigned nrg = (unsigned)(rows / kRG);
+  if (a.ksplit > 1 && (epi == EPI_ARGMAX || a.kpart == nullptr || a.kcount == nullptr)) return QD_ERR_SHAPE;
+  if (epi == EPI_ARGMAX) {
+    if (KW != 2048 || a.part_val == nullptr || a.part_idx == nullptr) return QD_ERR_SHAPE;
+    const unsigned gx = (a.grid > 0 && (unsigned)a.grid < nrg) ? (unsigned)a.grid : nrg;
+    return launch8<2048, EPI_ARGMAX>(a, gx, s);
   }
-  QD_G8(2048)
-  QD_G8(6144)
-#undef QD_G8
+  if (epi == EPI_SILU) {
+    if (KW == 2048) return launch8<2048, EPI_SILU>(a, nrg, s);
+    if (KW == 1024) return launch8<1024, EPI_SILU>(a, nrg, s);
+    return QD_ERR_SHAPE;
+  }
+  if (KW == 3072) return launch8<3072, EPI_STORE>(a, nrg, s);
+  if (KW == 2048) return launch8<2048, EPI_STORE>(a, nrg, s);
+  if (KW == 1024) return launch8<1024, EPI_STORE>(a, nrg, s);
   return QD_ERR_SHAPE;
 }
 
 int gemv8_row_groups(long N) { return (int)((N + kRG - 1) / kRG); }
 
+int bimage8_launch(const float* x, long ldx, const uint16_t* gamma, bool norm, float eps, int K, int nseq,
+                   uint16_t* img, float* ss, float* scale, hipStream_t s) {
+  if (K % 32 != 0 || nseq < 1 || nseq > kB) return QD_ERR_SHAPE;
+  hipLaunchKernelGGL((bimage8_kernel<float>), dim3(kB), dim3(256), 0, s, x, ldx, nullptr, 0L, gamma, norm, eps, K,
+                     nseq, nullptr, img, ss, scale);
+  return qd_host::launch_status("bimage8_kernel");
+}
+
+int embed8_launch(const uint16_t* table, const int64_t* token, float* out, int H, long V, int nseq,
+                  const uint16_t* gamma, float eps, uint16_t* img, float* ss, float* scale, hipStream_t s) {
+  if (H % 32 != 0 || nseq < 1 || nseq > kB) return QD_ERR_SHAPE;
+  hipLaunchKernelGGL((bimage8_kernel<uint16_t>), dim3(kB), dim3(256), 0, s, table, 0L, token, V, gamma, true, eps,
+                     H, nseq, out, img, ss, scale);
+  return qd_host::launch_status("embed8_kernel");
+}
+
 int argmax8_reduce_launch(const float* part_val, const long* part_idx, int nblk, int64_t* token, int nseq,
                           hipStream_t s) {
   hipLaunchKernelGGL(argmax8_reduce_kernel, dim3((unsigned)nseq), dim3(256), 0, s, part_val, part_idx, nblk, token);
   return qd_host::launch_status("argmax8_reduce_kernel");
-}
-
-int rmsnorm8_launch(const float* x, long ldx, const uint16_t* gamma, float eps, int K, float* y, long ldy, int nseq,
-                    hipStream_t s) {
-  hipLaunchKernelGGL(rmsnorm8_kernel, dim3((unsigned)nseq), dim3(256), 0, s, x, ldx, gamma, eps, K, y, ldy);
-  return qd_host::launch_status("rmsnorm8_kernel");
-}
-
-int embed8_launch(const uint16_t* table, const int64_t* token, float* out, int H, long V, int nseq, hipStream_t s) {
-  hipLaunchKernelGGL(embed8_kernel, dim3((unsigned)nseq), dim3(256), 0, s, table, token, out, H, V);
-  return qd_host::launch_status("embed8_kernel");
 }
 
 int advance8_launch(const int64_t* token, int64_t* out_tokens, int64_t* counter, int64_t* cache_position,

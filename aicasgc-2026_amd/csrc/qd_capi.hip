@@ -5,6 +5,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -371,10 +372,25 @@ struct StepBuffers {
   char* argmax_ws;
   unsigned* tagged;   // persistent step hand-off words
   unsigned* control;  // persistent step: status, epoch, done
-  float* xn;          // batch step: final-norm output [B][H]
-  float* part_val;    // batch step: lm_head argmax partials [V/16][8]
+  // batch step (B > 1): operand images of x (times the next RMSNorm weight),
+  // attention output, r (times post_norm) and hidden; per-row-group sums of
+  // squares and image scales of x and r; K-split partials; lm_head partials
+  u16* xb;
+  u16* ab;
+  u16* rb;
+  u16* hb;
+  float* ss_x;
+  float* ss_r;
+  float* sc_x;
+  float* sc_r;
+  float* kpart;
+  unsigned* kcount;
+  float* part_val;
   long* part_idx;
 };
+
+constexpr int kBatchMaxKsplit = 6;
+constexpr int kBatchCounters = 1024;
 
 int batch_of(const qd_model_desc* d) { return d->batch > 1 ? d->batch : 1; }
 
@@ -395,10 +411,22 @@ bool step_layout(const qd_model_desc* d, int splits, StepBuffers* b, size_t* tot
   size_t o_gw = off; off += align256(argmax_ws_bytes());
   size_t o_tg = off; off += align256(4 * qd::kPersistTaggedWords);
   size_t o_ct = off; off += 256;
-  size_t o_xn = off, o_pv = off, o_pi = off;
+  size_t o_xb = off, o_ab = off, o_rb = off, o_hb = off, o_ssx = off, o_ssr = off, o_sc = off, o_kp = off,
+         o_kc = off, o_pv = off, o_pi = off;
   if (B > 1) {
+    // an operand image holds 16 fp16 columns per K index
     const size_t groups = (size_t)qd::gemv8_row_groups(d->vocab);
-    o_xn = off; off += align256(4 * B * (size_t)d->hidden);
+    const size_t hgroups = (size_t)qd::gemv8_row_groups(d->hidden);
+    const size_t max_rows = qkv_rows > (size_t)d->intermediate ? qkv_rows : (size_t)d->intermediate;
+    o_xb = off; off += align256(32 * (size_t)d->hidden);
+    o_ab = off; off += align256(32 * (size_t)d->num_heads * d->head_dim);
+    o_rb = off; off += align256(32 * (size_t)d->hidden);
+    o_hb = off; off += align256(32 * (size_t)d->intermediate);
+    o_ssx = off; off += align256(4 * hgroups * qd::kBatchMax);
+    o_ssr = off; off += align256(4 * hgroups * qd::kBatchMax);
+    o_sc = off; off += 256;
+    o_kp = off; off += align256(4 * (size_t)qd::gemv8_row_groups((long)max_rows) * kBatchMaxKsplit * 2 * 128);
+    o_kc = off; off += align256(4 * (size_t)kBatchCounters);
     o_pv = off; off += align256(4 * groups * qd::kBatchMax);
     o_pi = off; off += align256(8 * groups * qd::kBatchMax);
   }
@@ -415,15 +443,29 @@ bool step_layout(const qd_model_desc* d, int splits, StepBuffers* b, size_t* tot
     b->argmax_ws = base + o_gw;
     b->tagged = reinterpret_cast<unsigned*>(base + o_tg);
     b->control = reinterpret_cast<unsigned*>(base + o_ct);
-    b->xn = reinterpret_cast<float*>(base + o_xn);
+    b->xb = reinterpret_cast<u16*>(base + o_xb);
+    b->ab = reinterpret_cast<u16*>(base + o_ab);
+    b->rb = reinterpret_cast<u16*>(base + o_rb);
+    b->hb = reinterpret_cast<u16*>(base + o_hb);
+    b->ss_x = reinterpret_cast<float*>(base + o_ssx);
+    b->ss_r = reinterpret_cast<float*>(base + o_ssr);
+    b->sc_x = reinterpret_cast<float*>(base + o_sc);
+    b->sc_r = b->sc_x + qd::kBatchMax;
+    b->kpart = reinterpret_cast<float*>(base + o_kp);
+    b->kcount = reinterpret_cast<unsigned*>(base + o_kc);
     b->part_val = reinterpret_cast<float*>(base + o_pv);
     b->part_idx = reinterpret_cast<long*>(base + o_pi);
   }
   return true;
 }
 
+// Splits per kv head: batch-1 default; a batch step already has B x Hkv
+// sequence-heads to spread over the CUs, so it takes 1/B as many (at least 4).
 int splits_of(const qd_model_desc* d) {
-  return d->attn_splits > 0 ? d->attn_splits : qd_attention_default_splits(d->capacity);
+  if (d->attn_splits > 0) return d->attn_splits;
+  const int s = qd_attention_default_splits(d->capacity);
+  const int B = batch_of(d);
+  return B > 1 ? std::max(4, s / B) : s;
 }
 
 }  // namespace
@@ -552,13 +594,36 @@ int qd_decode_step_mode(const qd_model_desc* d) {
 
 namespace {
 
+// Workgroups per row group along K for a batch GEMV (K ranges of 1024, 2048
+// or 3072): the smallest split whose workgroup count is a multiple of the 256
+// CUs, else the smallest that gives at least 256 workgroups.
+int batch_ksplit(long rows, long K) {
+  const long groups = rows / 16;
+  const int cand[] = {1, 2, 3, 6};
+  auto ok = [&](int ks) {
+    const long kw = K / ks;
+    return K % ks == 0 && (kw == 1024 || kw == 2048 || kw == 3072);
+  };
+  for (int ks : cand)
+    if (ok(ks) && (groups * ks) % 256 == 0) return ks;
+  for (int ks : cand)
+    if (ok(ks) && groups * ks >= 256) return ks;
+  for (int ks : cand)
+    if (ok(ks)) return ks;
+  return 1;
+}
+
 // Batch step (batch 2..8): the kernel chain with MFMA batch GEMVs and the
 // split-KV attention run per sequence (grid y), every sequence at its own cache
-// position.
+// position.  Activations move between the GEMVs as operand images: x (times
+// the next input_norm, or final_norm after the last layer, scaled by rstd of
+// the previous r), the attention output, r (times post_norm, scaled by rstd
+// of x) and the MLP hidden; each producer also writes per-row-group sums of
+// squares, from which the consumer applies its RMSNorm.
 int batch_step(const qd_model_desc* d, hipStream_t s) {
   const int B = batch_of(d);
   QD_REQUIRE(B <= qd::kBatchMax, QD_ERR_SHAPE, "batch %d > %d", B, qd::kBatchMax);
-  QD_REQUIRE(d->hidden == 2048 && d->num_heads * d->head_dim == 2048 &&
+  QD_REQUIRE(d->num_layers >= 1 && d->hidden == 2048 && d->num_heads * d->head_dim == 2048 &&
                  (d->intermediate == 2048 || d->intermediate == 6144) && d->vocab % 16 == 0,
              QD_ERR_SHAPE, "batch step supports H = Hq*D = 2048, I in {2048, 6144}, vocab %% 16 == 0");
   const int splits = splits_of(d);
@@ -567,15 +632,23 @@ int batch_step(const qd_model_desc* d, hipStream_t s) {
   step_layout(d, splits, &b, &total);
   const int H = d->hidden, D = d->head_dim, Hq = d->num_heads, Hkv = d->num_kv_heads, I = d->intermediate;
   const long qkv_rows = (long)Hq * D + 2L * Hkv * D;
+  const int hparts = qd::gemv8_row_groups(H);
   int st = QD_OK;
-  if ((st = qd::embed8_launch((const u16*)d->embed, d->token, b.x, H, d->vocab, B, s))) return st;
+  if ((st = qd::embed8_launch((const u16*)d->embed, d->token, b.x, H, d->vocab, B,
+                              (const u16*)d->layers[0].input_norm, d->eps, b.xb, b.ss_x, b.sc_x, s)))
+    return st;
+  auto base = [&](qd::Gemv8Args& g, long N, long K) {
+    g.nseq = B; g.eps = d->eps; g.N = N; g.K = K; g.ldw = K; g.ksplit = batch_ksplit(N, K);
+    g.kpart = b.kpart; g.kcount = b.kcount;
+  };
   for (int li = 0; li < d->num_layers; ++li) {
     const qd_layer_weights& w = d->layers[li];
+    const int xparts = li == 0 ? 1 : hparts;   // the embedding kernel writes one partial
     qd::Gemv8Args g;
-    g.nseq = B; g.eps = d->eps;
-    g.x = b.x; g.ldx = H; g.gamma = (const u16*)w.input_norm; g.W = (const u16*)w.qkv; g.ldw = H;
-    g.N = qkv_rows; g.K = H; g.y = b.qkv; g.ldy = qkv_rows;
-    if ((st = qd::gemv8_launch(g, true, qd::EPI_STORE, s))) return st;
+    base(g, qkv_rows, H);
+    g.xb = b.xb; g.in_ss = b.ss_x; g.in_parts = xparts; g.in_scale = b.sc_x; g.W = (const u16*)w.qkv;
+    g.y = b.qkv; g.ldy = qkv_rows;
+    if ((st = qd::gemv8_launch(g, qd::EPI_STORE, s))) return st;
     qd::AttnArgs aa;
     aa.k = (const u16*)w.k_cache; aa.v = (const u16*)w.v_cache; aa.k_w = (u16*)w.k_cache; aa.v_w = (u16*)w.v_cache;
     aa.stride_h = (long)d->capacity * D; aa.stride_s = D; aa.T = d->capacity; aa.cache_position = d->cache_position;
@@ -584,31 +657,44 @@ int batch_step(const qd_model_desc* d, hipStream_t s) {
     aa.rope_pos = d->rope_position; aa.inv_freq = d->inv_freq; aa.sec_h = d->sec_h; aa.sec_w = d->sec_w;
     aa.q_rot_out = b.q_rot;
     aa.batch = B; aa.bs_q = qkv_rows; aa.bs_cache = (long)Hkv * d->capacity * D;
+    aa.out_img = b.ab;
     attn_ws(b.attn_ws, aa);
     aa.lse = aa.o_part + (size_t)B * Hq * splits * 128;
     if ((st = qd::attention_partial_launch<float>(aa, s))) return st;
     if ((st = qd::attention_merge_launch<float>(aa, s))) return st;
+    // r = x + W_o attn; image of r * post_norm * rstd(x)
     qd::Gemv8Args go;
-    go.nseq = B; go.x = b.attn; go.ldx = (long)Hq * D; go.W = (const u16*)w.o_proj; go.ldw = (long)Hq * D;
-    go.N = H; go.K = (long)Hq * D; go.residual = b.x; go.ldr = H; go.y = b.r; go.ldy = H;
-    if ((st = qd::gemv8_launch(go, false, qd::EPI_STORE, s))) return st;
+    base(go, H, (long)Hq * D);
+    go.xb = b.ab; go.W = (const u16*)w.o_proj; go.residual = b.x; go.ldr = H; go.y = b.r; go.ldy = H;
+    go.yb = b.rb; go.yb_gamma = (const u16*)w.post_norm; go.pre_ss = b.ss_x; go.pre_parts = xparts;
+    go.out_scale = b.sc_r; go.yss = b.ss_r;
+    if ((st = qd::gemv8_launch(go, qd::EPI_STORE, s))) return st;
     qd::Gemv8Args gu;
-    gu.nseq = B; gu.eps = d->eps; gu.x = b.r; gu.ldx = H; gu.gamma = (const u16*)w.post_norm;
-    gu.W = (const u16*)w.gate_up; gu.ldw = H; gu.N = I; gu.up_offset = I; gu.K = H; gu.y = b.hidden; gu.ldy = I;
-    if ((st = qd::gemv8_launch(gu, true, qd::EPI_SILU, s))) return st;
+    base(gu, I, H);
+    gu.xb = b.rb; gu.in_ss = b.ss_r; gu.in_parts = hparts; gu.in_scale = b.sc_r; gu.W = (const u16*)w.gate_up;
+    gu.up_offset = I; gu.yb = b.hb;
+    if ((st = qd::gemv8_launch(gu, qd::EPI_SILU, s))) return st;
+    // x = r + W_down hidden; image of x * (next input_norm | final_norm) * rstd(r)
+    const u16* next_gamma =
+        (const u16*)(li + 1 < d->num_layers ? d->layers[li + 1].input_norm : d->final_norm);
     qd::Gemv8Args gd;
-    gd.nseq = B; gd.x = b.hidden; gd.ldx = I; gd.W = (const u16*)w.down; gd.ldw = I; gd.N = H; gd.K = I;
-    gd.residual = b.r; gd.ldr = H; gd.y = b.x; gd.ldy = H;
-    if ((st = qd::gemv8_launch(gd, false, qd::EPI_STORE, s))) return st;
+    base(gd, H, I);
+    gd.xb = b.hb; gd.W = (const u16*)w.down; gd.residual = b.r; gd.ldr = H; gd.y = b.x; gd.ldy = H;
+    gd.yb = b.xb; gd.yb_gamma = next_gamma; gd.pre_ss = b.ss_r; gd.pre_parts = hparts; gd.out_scale = b.sc_x;
+    gd.yss = b.ss_x;
+    if ((st = qd::gemv8_launch(gd, qd::EPI_STORE, s))) return st;
   }
-  // final RMSNorm, tied lm_head, per-sequence argmax
-  if ((st = qd::rmsnorm8_launch(b.x, H, (const u16*)d->final_norm, d->eps, H, b.xn, H, B, s))) return st;
+  // final RMSNorm (applied through the image of x), tied lm_head, per-sequence argmax
   qd::Gemv8Args gl;
-  gl.nseq = B; gl.x = b.xn; gl.ldx = H; gl.W = (const u16*)d->embed; gl.ldw = H; gl.N = d->vocab; gl.K = H;
+  base(gl, d->vocab, H);
+  gl.ksplit = 1;
+  gl.xb = b.xb; gl.in_ss = b.ss_x; gl.in_parts = hparts; gl.in_scale = b.sc_x; gl.W = (const u16*)d->embed;
   gl.y = reinterpret_cast<float*>(d->logits_out); gl.ldy = d->vocab; gl.part_val = b.part_val;
   gl.part_idx = b.part_idx;
-  if ((st = qd::gemv8_launch(gl, false, qd::EPI_ARGMAX, s))) return st;
-  return qd::argmax8_reduce_launch(b.part_val, b.part_idx, qd::gemv8_row_groups(d->vocab), d->token, B, s);
+  const int groups = qd::gemv8_row_groups(d->vocab);
+  gl.grid = std::min(groups, 2 * qd_host::cu_count());
+  if ((st = qd::gemv8_launch(gl, qd::EPI_ARGMAX, s))) return st;
+  return qd::argmax8_reduce_launch(b.part_val, b.part_idx, gl.grid, d->token, B, s);
 }
 
 }  // namespace
@@ -744,22 +830,46 @@ int qd_decode_advance_batch(const int64_t* token, int64_t* out_tokens, int64_t* 
                              S(stream));
 }
 
+size_t qd_batch_gemv_workspace_bytes(long N, long K) {
+  if (N <= 0 || K <= 0) return 0;
+  // image [K][16] fp16, ss + scale [2][8], K-split partials [N/16][<= 6][<= 2][128], counters [N/16]
+  return align256(32 * (size_t)K) + 256 + align256(4 * (size_t)qd::gemv8_row_groups(N) * kBatchMaxKsplit * 256) +
+         align256(4 * (size_t)qd::gemv8_row_groups(N));
+}
+
 int qd_batch_gemv(const float* x, long ldx, const void* gamma, float eps, const void* W, long ldw, long N, long K,
                   long up_offset, const float* residual, long ldr, float* y, long ldy, int nseq, int epilogue,
-                  void* stream) {
-  QD_REQUIRE(x && W && y, QD_ERR_ARG, "null pointer");
+                  void* workspace, size_t workspace_bytes, void* stream) {
+  QD_REQUIRE(x && W && y && workspace, QD_ERR_ARG, "null pointer");
   QD_REQUIRE(nseq >= 1 && nseq <= qd::kBatchMax, QD_ERR_SHAPE, "nseq %d outside 1..%d", nseq, qd::kBatchMax);
   QD_REQUIRE(epilogue == QD_BATCH_EPI_STORE || epilogue == QD_BATCH_EPI_SILU, QD_ERR_ARG, "bad epilogue %d",
              epilogue);
-  QD_REQUIRE((K == 2048 || K == 6144) && N % 16 == 0 && ldx % 4 == 0 && a16(x) && a16(W) && ldw % 8 == 0,
+  QD_REQUIRE((K == 2048 || K == 6144) && N % 16 == 0 && N > 0 && ldx % 4 == 0 && a16(x) && a16(W) && ldw % 8 == 0,
              QD_ERR_SHAPE, "need K in {2048, 6144}, N %% 16 == 0 and 16-byte aligned rows");
+  QD_REQUIRE(epilogue != QD_BATCH_EPI_SILU || (up_offset == N && K == 2048), QD_ERR_SHAPE,
+             "SiLU epilogue: up_offset must equal N and K must be 2048");
+  QD_REQUIRE(a16(workspace) && workspace_bytes >= qd_batch_gemv_workspace_bytes(N, K), QD_ERR_ARG,
+             "workspace needs %zu bytes (16-byte aligned)", qd_batch_gemv_workspace_bytes(N, K));
+  char* ws = reinterpret_cast<char*>(workspace);
+  u16* img = reinterpret_cast<u16*>(ws);
+  float* ss = reinterpret_cast<float*>(ws + align256(32 * (size_t)K));
+  float* scale = ss + qd::kBatchMax;
+  float* kpart = reinterpret_cast<float*>(ws + align256(32 * (size_t)K) + 256);
+  unsigned* kcount = reinterpret_cast<unsigned*>(
+      ws + align256(32 * (size_t)K) + 256 + align256(4 * (size_t)qd::gemv8_row_groups(N) * kBatchMaxKsplit * 256));
+  int st = qd::bimage8_launch(x, ldx, (const u16*)gamma, gamma != nullptr, eps, (int)K, nseq, img, ss, scale,
+                              S(stream));
+  if (st) return st;
   qd::Gemv8Args g;
-  g.x = x; g.ldx = ldx; g.gamma = (const u16*)gamma; g.eps = eps; g.W = (const u16*)W; g.ldw = ldw; g.N = N;
-  g.K = K; g.up_offset = epilogue == QD_BATCH_EPI_SILU ? up_offset : 0; g.residual = residual; g.ldr = ldr;
-  g.y = y; g.ldy = ldy; g.nseq = nseq;
-  if (epilogue == QD_BATCH_EPI_SILU) QD_REQUIRE(up_offset == N, QD_ERR_ARG, "SiLU epilogue: up_offset must equal N");
-  return qd::gemv8_launch(g, gamma != nullptr, epilogue == QD_BATCH_EPI_SILU ? qd::EPI_SILU : qd::EPI_STORE,
-                          S(stream));
+  g.xb = img; g.in_ss = gamma != nullptr ? ss : nullptr; g.in_parts = 1; g.in_scale = scale; g.eps = eps;
+  g.W = (const u16*)W; g.ldw = ldw; g.N = N; g.K = K; g.residual = residual; g.ldr = ldr; g.y = y; g.ldy = ldy;
+  g.nseq = nseq; g.kpart = kpart; g.kcount = kcount;
+  g.ksplit = batch_ksplit(N, K);
+  if (epilogue == QD_BATCH_EPI_SILU) {
+    g.up_offset = up_offset;
+    return qd::gemv8_launch(g, qd::EPI_SILU, S(stream));
+  }
+  return qd::gemv8_launch(g, qd::EPI_STORE, S(stream));
 }
 
 }  // extern "C"

@@ -180,6 +180,26 @@ __device__ __forceinline__ void fence_release() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
 }
 
+// ---------------------------------------------------------------- batch operand images
+//
+// The B operand of the batch GEMV (v_mfma_f32_16x16x32_f16, 16 columns) for an
+// activation u[8][K] of up to 8 sequences, stored in MFMA lane order so one
+// 16-byte load per lane and K tile of 32 fetches it:
+//   image[((k / 32) * 64 + col + 16 ((k % 32) / 8)) * 8 + k % 8]
+// column seq (< 8) holds fp16(u[seq][k]), column seq + 8 the fp16 rounding
+// residual u - fp16(u), so the two MFMA columns sum to u with ~22 bits.
+
+__device__ __forceinline__ long bimg_index(int col, long k) {
+  return (((k >> 5) * 64 + col + 16 * ((k & 31) >> 3)) << 3) + (k & 7);
+}
+
+__device__ __forceinline__ void bimg_store(uint16_t* img, int seq, long k, float u) {
+  const _Float16 hi = (_Float16)u;
+  const _Float16 lo = (_Float16)(u - (float)hi);
+  img[bimg_index(seq, k)] = __builtin_bit_cast(uint16_t, hi);
+  img[bimg_index(seq + 8, k)] = __builtin_bit_cast(uint16_t, lo);
+}
+
 }  // namespace qd
 
 // Host-side error reporting shared by the C-ABI translation units.

@@ -72,6 +72,7 @@ struct AttnArgs {
   // caches, of o_part / lse / out / q_rot_out; cache_position[b], rope_pos[3b..]
   int batch = 1;
   long bs_q = 0, bs_cache = 0;
+  uint16_t* out_img = nullptr;        // merge: batch operand image of the output (instead of out)
 };
 
 // Partials of every (kv head, split); fused prologue when a.qkv != nullptr.
@@ -180,12 +181,19 @@ int decode_persistent_launch(const PersistArgs& a, hipStream_t s);
 
 constexpr int kBatchMax = 8;
 
-// Batch GEMV y[b][r] = W[r] . x'[b] for b < nseq (x' = RMSNorm(x) * gamma when
-// gamma is given), K in {2048, 6144}, rows a multiple of 16.
+// Batch GEMV on MFMA: y[b][r] = f[b] * (W[r] . u[b]) for b < nseq, where u is
+// the input's operand image (u = x * gamma * s, written by the producer with
+// scale s = in_scale[b]) and f = rstd(in_ss) / s (1 / s without in_ss), so
+// y = W . (RMSNorm(x) * gamma).  K in {2048, 6144}; rows a multiple of 16.
+// The epilogue adds the residual (EPI_STORE) or forms silu(gate) * up
+// (EPI_SILU), stores y, and writes the output's own operand image (times
+// yb_gamma and out scale rstd(pre_ss), stored to out_scale) with per-row-group
+// partial sums of y^2 (yss).
 struct Gemv8Args {
-  const float* x = nullptr;        // fp32 [nseq][ldx]
-  long ldx = 0;
-  const uint16_t* gamma = nullptr; // fp16 [K]
+  const uint16_t* xb = nullptr;    // input operand image [K/32][64][8] fp16
+  const float* in_ss = nullptr;    // [in_parts][8] partial sums of squares of x, or null (no RMSNorm)
+  int in_parts = 0;
+  const float* in_scale = nullptr; // [8] scale of the input image, or null (1)
   float eps = 1e-6f;
   const uint16_t* W = nullptr;     // fp16 [rows][ldw]
   long ldw = 0;
@@ -194,20 +202,34 @@ struct Gemv8Args {
   long up_offset = 0;
   const float* residual = nullptr; // fp32 [nseq][ldr] added in EPI_STORE, or null
   long ldr = 0;
-  float* y = nullptr;              // fp32 [nseq][ldy] (EPI_ARGMAX: optional logits)
+  float* y = nullptr;              // fp32 [nseq][ldy] or null (EPI_ARGMAX: optional logits)
   long ldy = 0;
+  uint16_t* yb = nullptr;          // output operand image [N/32][64][8], or null
+  const uint16_t* yb_gamma = nullptr;
+  const float* pre_ss = nullptr;   // [pre_parts][8]: output image scale rstd over N, or null (1)
+  int pre_parts = 0;
+  float* out_scale = nullptr;      // [8] the output image's scale, or null
+  float* yss = nullptr;            // [N/16][8] partial sums of squares of y, or null
   int nseq = 0;
-  float* part_val = nullptr;       // EPI_ARGMAX: [row groups][8]
+  int ksplit = 1;                  // workgroups per row group along K (not EPI_ARGMAX)
+  float* kpart = nullptr;          // ksplit > 1: [N/16][ksplit][1 or 2 (EPI_SILU)][128] partial products
+  unsigned* kcount = nullptr;      // ksplit > 1: [N/16] arrival counters (zero, self-resetting)
+  int grid = 0;                    // EPI_ARGMAX: workgroups (each loops over row groups); 0: one per group
+  float* part_val = nullptr;       // EPI_ARGMAX: [grid][8]
   long* part_idx = nullptr;
 };
 
-int gemv8_launch(const Gemv8Args& a, bool norm, int epi, hipStream_t s);
+int gemv8_launch(const Gemv8Args& a, int epi, hipStream_t s);
 int gemv8_row_groups(long N);
+// Image of u = x * gamma * s (gamma null: 1), s = rstd(x) when norm else 1,
+// sum of squares of x as one partial ss[8], s to scale[8].
+int bimage8_launch(const float* x, long ldx, const uint16_t* gamma, bool norm, float eps, int K, int nseq,
+                   uint16_t* img, float* ss, float* scale, hipStream_t s);
 int argmax8_reduce_launch(const float* part_val, const long* part_idx, int nblk, int64_t* token, int nseq,
                           hipStream_t s);
-int rmsnorm8_launch(const float* x, long ldx, const uint16_t* gamma, float eps, int K, float* y, long ldy, int nseq,
-                    hipStream_t s);
-int embed8_launch(const uint16_t* table, const int64_t* token, float* out, int H, long V, int nseq, hipStream_t s);
+// x[b] = embed[token[b]] and its image (gamma, scale rstd(x)), ss, scale.
+int embed8_launch(const uint16_t* table, const int64_t* token, float* out, int H, long V, int nseq,
+                  const uint16_t* gamma, float eps, uint16_t* img, float* ss, float* scale, hipStream_t s);
 int advance8_launch(const int64_t* token, int64_t* out_tokens, int64_t* counter, int64_t* cache_position,
                     int64_t* rope_position, int max_tokens, int nseq, hipStream_t s);
 // 0 when the device can keep the whole persistent grid resident at once.

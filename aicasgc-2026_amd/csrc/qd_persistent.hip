@@ -9,8 +9,7 @@
 //                               32 position slots x 16 lanes; online softmax
 //   MERGE    partials -> attn   workgroup = 8 dims of one q head (wave 0)
 //   O_PROJ   attn -> r          1 row of W_o per wave, + residual x
-//   GATE_UP  r -> hidden        24 (gate, up) row pairs per workgroup (3 or 4 per wave, none
-//                               for wave 0), RMSNorm prologue, SiLU*up
+//   GATE_UP  r -> hidden        3 (gate, up) row pairs per wave, RMSNorm prologue, SiLU*up
 //   DOWN     hidden -> x        1 row of W_d per wave, + residual r
 //
 // Weights never depend on activations, so each wave issues the register loads
@@ -59,7 +58,7 @@ constexpr unsigned kSpinLimit = 1u << 16;  // polls per thread and launch (tens 
 
 static_assert(NQKV == 2 * NTH, "QKV: two rows per wave");
 static_assert(H == NTH, "o_proj / down: one row per wave");
-static_assert(I == 3 * NTH, "gate_up: 24 row pairs per workgroup");
+static_assert(I == 3 * NTH, "gate_up: three row pairs per wave");
 static_assert(MERGE_DIMS == 8, "merge: 8 dims per workgroup");
 
 // Parity of the words written at layer l of the launch with epoch ep.  It
@@ -302,25 +301,20 @@ struct Ctx {
   float rc, rs;               // M-RoPE cos / sin of rotary pair `lane`
 };
 
-// Wave roles.
-enum Role { ROLE_MERGER = 0, ROLE_POLLER = 1, ROLE_STREAMER = 2 };
-
-// The layer loop of one wave role: wave 0 (polls, merges the split partials,
-// gathers the merged output; no gate/up rows), waves 1..NA-1 (poll) and the
-// streamers.  Each role runs its own instance: their weight loads are issued
-// at different points, and in one shared loop the compiler would have to keep
-// each role's loop-carried weight registers live on the other roles' paths as
-// well.  All instances execute the same sequence of workgroup barriers.
-template <int ROLE>
+// The layer loop of one wave group.  Pollers (waves 0..NA-1) and streamers
+// run separate instances: their weight loads are issued at different points,
+// and in one shared loop the compiler would have to keep each group's
+// loop-carried weight registers live on the other group's path as well.
+// Both instances execute the same sequence of workgroup barriers.
+template <bool STREAM>
 __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& cx, Smem& sm, Spin& sp) {
-  constexpr bool STREAM = ROLE == ROLE_STREAMER;
   const int w = cx.w, gw = cx.gw, kvh = cx.kvh, split = cx.split, t0 = cx.t0, t1 = cx.t1, mh = cx.mh,
             md0 = cx.md0;
   const long pos = cx.pos;
   const unsigned ep = cx.ep;
   const float rc = cx.rc, rs = cx.rs;
   constexpr bool streamer = STREAM;
-  constexpr bool poller = ROLE == ROLE_MERGER;  // polls the split partials and the merged output
+  const bool poller = (w == 0);     // polls the split partials (MERGE) and the merged output
   int lane = lane_id();
   int tid = threadIdx.x;
   const Rsrc r_x = rsrc_of(a.x_t, H), r_qkv = rsrc_of(a.qkv_t, NQKV), r_op = rsrc_of(a.opart_t, HQ * NS * D),
@@ -383,18 +377,12 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
     nw0 = nw[lane];
     nw1 = nw[lane + 64];
   };
-  // W_gate/up row pairs: 24 per workgroup; streamers take 3 each (pairs
-  // 12..23), pollers 1-3 take 4 each (pairs 0..11) and wave 0, which issues its
-  // loads last (after the merge and the merged-output gather), takes none.
-  constexpr int GP = STREAM ? 3 : 4;
-  constexpr bool has_gu = ROLE != ROLE_MERGER;
-  const long gu0 = (long)blockIdx.x * (3 * NW) + (STREAM ? 12 + 3 * (w - NA) : 4 * (w - 1));
-  auto issue_gu = [&](const PersistLayer& Lx, u32x4 (&wgu)[2 * GP][4]) {
+  auto issue_gu = [&](const PersistLayer& Lx, u32x4 (&wgu)[6][4]) {
 #pragma unroll
-    for (int p = 0; p < GP; ++p) {
-      const long o = gu0 + p;
+    for (int p = 0; p < 3; ++p) {
+      const long o = (long)gw * 3 + p;
       load_row<4>(Lx.gate_up + o * H, lane, wgu[p]);
-      load_row<4>(Lx.gate_up + (o + I) * H, lane, wgu[GP + p]);
+      load_row<4>(Lx.gate_up + (o + I) * H, lane, wgu[3 + p]);
     }
   };
   auto issue_wd = [&](const PersistLayer& Lx, u32x4 (&wd)[1][12]) {
@@ -420,7 +408,7 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
     // re-issues its own, unused): a conditional issue would leave the previous
     // values live to the end of the iteration on the path that skips it.
     const PersistLayer& Ln = a.layers[l + 1 < a.num_layers ? l + 1 : l];
-    u32x4 wgu[2 * GP][4];         // W_gate/up rows gu0..gu0+GP-1 (+I)
+    u32x4 wgu[6][4];              // W_gate/up rows 3gw..3gw+2 (+I)
     u32x4 wd[1][12];              // W_down row gw
 
     // ================================================================ QKV
@@ -525,43 +513,23 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
             vv[u] = *reinterpret_cast<const u32x4*>(&s_kv[1][dl]);
           }
         }
-        // block online softmax: the KU scores first (independent row sums),
-        // then one rescale of the running state per head
-        float sc[2][KU];
 #pragma unroll
         for (int u = 0; u < KU; ++u) {
           const bool valid = t + u * SLOTS < t1;
+          float vf[8];
+          unpack8(vv[u], vf);
 #pragma unroll
           for (int g = 0; g < 2; ++g) {
-            const float d = row16_sum(dot8(kk[u], q[g], 0.f)) * a.scale;
-            sc[g][u] = valid ? d : -INFINITY;
-          }
-        }
+            const float s = row16_sum(dot8(kk[u], q[g], 0.f)) * a.scale;
+            const float dlt = s - m[g];
+            const float e = __expf(-fabsf(dlt));
+            const bool up = valid && dlt > 0.f;
+            const float c = up ? e : 1.f;
+            const float p = valid ? (up ? 1.f : e) : 0.f;
+            m[g] = up ? s : m[g];
+            lsum[g] = __builtin_fmaf(lsum[g], c, p);
 #pragma unroll
-        for (int g = 0; g < 2; ++g) {
-          float mb = sc[g][0];
-#pragma unroll
-          for (int u = 1; u < KU; ++u) mb = fmaxf(mb, sc[g][u]);
-          const float mn = fmaxf(m[g], mb);
-          const bool any = mn != -INFINITY;
-          const float corr = any ? __expf(m[g] - mn) : 1.f;
-          float p[KU];
-          float ps = 0.f;
-#pragma unroll
-          for (int u = 0; u < KU; ++u) {
-            p[u] = any ? __expf(sc[g][u] - mn) : 0.f;
-            ps += p[u];
-          }
-          lsum[g] = __builtin_fmaf(lsum[g], corr, ps);
-          m[g] = mn;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) acc[g][i] *= corr;
-#pragma unroll
-          for (int u = 0; u < KU; ++u) {
-            float vf[8];
-            unpack8(vv[u], vf);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) acc[g][i] = __builtin_fmaf(p[u], vf[i], acc[g][i]);
+            for (int i = 0; i < 8; ++i) acc[g][i] = __builtin_fmaf(acc[g][i], c, p * vf[i]);
           }
         }
       }
@@ -632,7 +600,7 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
     }
     // waves 1-3 right after the partials, wave 0 after its two polls
     QD_FRESH_LANE();
-    if (!streamer && has_gu) issue_gu(Lw, wgu);
+    if (!streamer) issue_gu(Lw, wgu);
     __syncthreads();
 
     // ================================================================ O_PROJ
@@ -655,18 +623,18 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
       gp_next = ld16(Ln.post_norm + tid * 8);
       issue_wd(Lw, wd);
     }
-    if (has_gu) {
-      float gu[2 * GP];
-      rows_dot_norm<4, 2 * GP>(wgu, s_r, s_gpost, lds_rstd<4>(s_r, lane, a.eps), lane, gu);
+    {
+      float gu[6];
+      rows_dot_norm<4, 6>(wgu, s_r, s_gpost, lds_rstd<4>(s_r, lane, a.eps), lane, gu);
       if (lane == 0) {
 #pragma unroll
-        for (int p = 0; p < GP; ++p) {
+        for (int p = 0; p < 3; ++p) {
           const float g = gu[p];
-          put(a.hid_t + gu0 + p, par, (g / (1.0f + __expf(-g))) * gu[GP + p]);
+          put(a.hid_t + (long)gw * 3 + p, par, (g / (1.0f + __expf(-g))) * gu[3 + p]);
         }
       }
+      if (!streamer) puts_done();
     }
-    if (!streamer) puts_done();
     QD_FRESH_LANE();
     if (streamer) {
       issue_qkv(Ln);
@@ -736,9 +704,8 @@ __global__ __launch_bounds__(512) void decode_persistent_kernel(const PersistArg
     sincosf((float)a.rope_position[stream] * a.inv_freq[lane], &cx.rs, &cx.rc);
   }
 
-  if (w >= NA) persist_layers<ROLE_STREAMER>(a, cx, sm, sp);
-  else if (w > 0) persist_layers<ROLE_POLLER>(a, cx, sm, sp);
-  else persist_layers<ROLE_MERGER>(a, cx, sm, sp);
+  if (w >= NA) persist_layers<true>(a, cx, sm, sp);
+  else persist_layers<false>(a, cx, sm, sp);
 
   // The last workgroup to finish advances the epoch for the next launch.  Every
   // workgroup read the epoch before it produced anything, so none can read the

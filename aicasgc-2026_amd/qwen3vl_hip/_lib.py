@@ -66,8 +66,9 @@ _SIGS = {
     "qd_decode_step_mode": (c_int, [P]),
     "qd_decode_layers_persistent": (c_int, [P, P]),
     "qd_decode_status": (c_int, [P, POINTER(ctypes.c_uint), c_int]),
+    "qd_batch_gemv_workspace_bytes": (ctypes.c_size_t, [c_long, c_long]),
     "qd_batch_gemv": (c_int, [P, c_long, P, c_float, P, c_long, c_long, c_long, c_long, P, c_long, P, c_long, c_int,
-                              c_int, P]),
+                              c_int, P, ctypes.c_size_t, P]),
     "qd_decode_advance_batch": (c_int, [P, P, P, P, P, c_int, c_int, P]),
 }
 

@@ -321,10 +321,14 @@ int qd_decode_status(const qd_model_desc* d, unsigned* status, int reset);
 /* Batch GEMV for up to 8 sequences: y[b][r] = W[r] . x'[b] for b < nseq, with
  * x' = RMSNorm(x[b]) * gamma when gamma != NULL (eps), else x.  x, residual, y
  * fp32 with row strides ldx / ldr / ldy; W fp16 [rows, ldw]; K in {2048, 6144};
- * N a multiple of 16; for QD_BATCH_EPI_SILU up_offset == N. */
+ * N a multiple of 16; for QD_BATCH_EPI_SILU up_offset == N and K == 2048.
+ * workspace: device memory of qd_batch_gemv_workspace_bytes(N, K) bytes,
+ * zeroed before its first use (it holds self-resetting counters) and not
+ * shared by two calls in flight. */
+size_t qd_batch_gemv_workspace_bytes(long N, long K);
 int qd_batch_gemv(const float* x, long ldx, const void* gamma, float eps, const void* W, long ldw, long N,
                   long K, long up_offset, const float* residual, long ldr, float* y, long ldy, int nseq,
-                  int epilogue, void* stream);
+                  int epilogue, void* workspace, size_t workspace_bytes, void* stream);
 
 /* qd_decode_advance for a batch: out_tokens [max_tokens][batch]. */
 int qd_decode_advance_batch(const int64_t* token, int64_t* out_tokens, int64_t* counter,

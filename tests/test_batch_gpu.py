@@ -34,9 +34,12 @@ def _gemv(x, W, gamma, residual, nseq, epi, up_offset, cuda):
     gd = gamma.to(cuda).contiguous() if gamma is not None else None
     rd = residual.to(cuda).contiguous() if residual is not None else None
     y = torch.full((8, N), float("nan"), dtype=torch.float32, device=cuda)
-    _lib.check(_lib.lib().qd_batch_gemv(
-        _lib.ptr(xd), K, _lib.ptr(gd), ctypes_float(1e-6), _lib.ptr(Wd), K, N, K, up_offset, _lib.ptr(rd),
-        N, _lib.ptr(y), N, nseq, epi, _lib.stream()), "qd_batch_gemv")
+    nws = _lib.lib().qd_batch_gemv_workspace_bytes(N, K)
+    ws = torch.zeros(nws, dtype=torch.uint8, device=cuda)
+    for _ in range(2):   # the second call runs on counters the first one reset
+        _lib.check(_lib.lib().qd_batch_gemv(
+            _lib.ptr(xd), K, _lib.ptr(gd), ctypes_float(1e-6), _lib.ptr(Wd), K, N, K, up_offset, _lib.ptr(rd),
+            N, _lib.ptr(y), N, nseq, epi, _lib.ptr(ws), nws, _lib.stream()), "qd_batch_gemv")
     torch.cuda.synchronize()
     return y.cpu()
 
@@ -85,12 +88,17 @@ def test_batch_gemv_rejects_bad_shapes(cuda):
     z = torch.zeros(8, 1024, device=cuda)
     W = torch.zeros(64, 1024, dtype=torch.float16, device=cuda)
     y = torch.zeros(8, 64, device=cuda)
+    nws = _lib.lib().qd_batch_gemv_workspace_bytes(64, 2048)
+    ws = torch.zeros(nws, dtype=torch.uint8, device=cuda)
     st = _lib.lib().qd_batch_gemv(_lib.ptr(z), 1024, None, ctypes_float(1e-6), _lib.ptr(W), 1024, 64, 1024, 0, None,
-                                  64, _lib.ptr(y), 64, 8, 0, _lib.stream())
+                                  64, _lib.ptr(y), 64, 8, 0, _lib.ptr(ws), nws, _lib.stream())
     assert st != 0 and "K in" in _lib.last_error()
     st = _lib.lib().qd_batch_gemv(_lib.ptr(z), 1024, None, ctypes_float(1e-6), _lib.ptr(W), 1024, 64, 2048, 0, None,
-                                  64, _lib.ptr(y), 64, 9, 0, _lib.stream())
+                                  64, _lib.ptr(y), 64, 9, 0, _lib.ptr(ws), nws, _lib.stream())
     assert st != 0 and "nseq" in _lib.last_error()
+    st = _lib.lib().qd_batch_gemv(_lib.ptr(z), 1024, None, ctypes_float(1e-6), _lib.ptr(W), 1024, 64, 2048, 0, None,
+                                  64, _lib.ptr(y), 64, 8, 0, _lib.ptr(ws), 256, _lib.stream())
+    assert st != 0 and "workspace" in _lib.last_error()
 
 
 VOCAB = 8192
