@@ -11,9 +11,11 @@
 //
 // Online softmax per slot in fp32 (one exp per position and head); the 16 slot
 // states are merged through LDS into one (normalised output, LSE) pair per
-// split.  A second, tiny kernel merges the splits.  No workgroup waits on
-// another inside a launch, so no device-scope fence is needed: the partials
-// become visible to the merge kernel at the launch boundary.
+// split.  A second, tiny kernel merges the splits: the partials become visible
+// to it at the launch boundary.  With arrival counters (a.done, the batch
+// step) the merge runs in the partial kernel instead: each split publishes its
+// partials with agent-coherent stores and counts its arrival, and the last
+// split of a kv head merges all of them; no workgroup ever waits on another.
 //
 // The fused variant (native decode step) also performs the decode step's q/k
 // head RMSNorm + M-RoPE and the static-cache write in its prologue: every
@@ -30,6 +32,7 @@
 namespace qd {
 
 namespace {
+constexpr int kFusedMergeMaxSplits = 64;
 constexpr int kD = 128;
 constexpr int kHalf = 64;
 constexpr int kSlots = 16;
@@ -128,7 +131,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
   if (Ll < 0) Ll = 0;
   const int L = (int)Ll;
   const int chunk = (L + a.n_split - 1) / a.n_split;
-  const int t0 = split * chunk;
+  const int t0 = min(split * chunk, L);
   const int t1 = min(t0 + chunk, L);
 
   // The cache rows do not depend on the prologue: the first batch of K/V loads
@@ -250,8 +253,50 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
       }
     }
     const int h = kvh * G + g;
-    o_part[((long)h * a.n_split + split) * kD + d] = den > 0.f ? num / den : 0.f;
-    if (d == 0) lse_out[(long)h * a.n_split + split] = den > 0.f ? M + __logf(den) : -INFINITY;
+    const float o = den > 0.f ? num / den : 0.f;
+    const float lse = den > 0.f ? M + __logf(den) : -INFINITY;
+    if (a.done == nullptr) {
+      o_part[((long)h * a.n_split + split) * kD + d] = o;
+      if (d == 0) lse_out[(long)h * a.n_split + split] = lse;
+    } else {
+      store_coherent(o_part + ((long)h * a.n_split + split) * kD + d, o);
+      if (d == 0) store_coherent(lse_out + (long)h * a.n_split + split, lse);
+    }
+  }
+  if (a.done == nullptr) return;
+
+  // ---- fused merge: the last split of this kv head to finish combines all of them
+  __shared__ int s_last;
+  __shared__ float s_w[G][kFusedMergeMaxSplits];
+  stores_done();
+  __syncthreads();
+  if (threadIdx.x == 0) s_last = arrive_last(a.done + (long)bq * a.Hkv + kvh, (unsigned)a.n_split);
+  __syncthreads();
+  if (!s_last) return;
+  const int S = a.n_split;
+  for (int i = threadIdx.x; i < G * S; i += blockDim.x)
+    s_w[i / S][i % S] = load_coherent(lse_out + (long)(kvh * G + i / S) * S + i % S);
+  __syncthreads();
+  for (int t = threadIdx.x; t < G * kD; t += blockDim.x) {
+    const int g = t / kD;
+    const int d = t % kD;
+    const int h = kvh * G + g;
+    float M = -INFINITY;
+    for (int s = 0; s < S; ++s) M = fmaxf(M, s_w[g][s]);
+    float num = 0.f, den = 0.f;
+    if (M != -INFINITY) {
+      const float* op = o_part + (long)h * S * kD + d;
+      for (int s = 0; s < S; ++s) {
+        const float w = __expf(s_w[g][s] - M);   // empty splits: exp(-inf) = 0
+        den += w;
+        num = __builtin_fmaf(w, load_coherent(const_cast<float*>(op) + (long)s * kD), num);
+      }
+    }
+    const float o = den > 0.f ? num / den : 0.f;
+    if (a.out_img != nullptr)
+      bimg_store(a.out_img, bq, (long)h * kD + d, o);
+    else
+      store_act(reinterpret_cast<TQ*>(a.out) + (long)bq * a.Hq * kD, (long)h * kD + d, o);
   }
 }
 
@@ -329,6 +374,7 @@ static int launch_partial_g(const AttnArgs& a, hipStream_t s) {
 
 template <typename TQ>
 int attention_partial_launch(const AttnArgs& a, hipStream_t s) {
+  if (a.done != nullptr && a.n_split > kFusedMergeMaxSplits) return QD_ERR_SHAPE;
   return a.qkv != nullptr ? launch_partial_g<TQ, true>(a, s) : launch_partial_g<TQ, false>(a, s);
 }
 

@@ -45,16 +45,6 @@ constexpr int kWaves = 8;         // K slices per workgroup
 constexpr int kKT = 32;           // K per MFMA
 constexpr int kOut = kRG * kB;    // outputs of one row group
 
-// Agent-coherent float store / load (written through to, and read past, the
-// XCD-private L2), and a wait for this thread's outstanding memory operations.
-__device__ __forceinline__ void store_coherent(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float load_coherent(float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void stores_done() { __builtin_amdgcn_s_waitcnt(0x0f70); }   // vmcnt(0)
-
 // Lane permutation of a 16-byte register quad: lane d receives lane addr/4's.
 __device__ __forceinline__ u32x4 bpermute4(int addr, const u32x4& v) {
   return u32x4{(unsigned)__builtin_amdgcn_ds_bpermute(addr, (int)v.x), (unsigned)__builtin_amdgcn_ds_bpermute(addr, (int)v.y),
@@ -210,12 +200,7 @@ __global__ __launch_bounds__(512) void gemv8_kernel(const Gemv8Args a) {
         }
         stores_done();
         __syncthreads();
-        if (t == 0) {
-          const unsigned old = __hip_atomic_fetch_add(a.kcount + rg, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          const int last = old == (unsigned)(a.ksplit - 1);
-          if (last) __hip_atomic_store(a.kcount + rg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          s_last = last;
-        }
+        if (t == 0) s_last = arrive_last(a.kcount + rg, (unsigned)a.ksplit);
         __syncthreads();
         if (!s_last) return;
         if (t < kOut) {

@@ -385,6 +385,7 @@ struct StepBuffers {
   float* sc_r;
   float* kpart;
   unsigned* kcount;
+  unsigned* attn_done;
   float* part_val;
   long* part_idx;
 };
@@ -412,7 +413,7 @@ bool step_layout(const qd_model_desc* d, int splits, StepBuffers* b, size_t* tot
   size_t o_tg = off; off += align256(4 * qd::kPersistTaggedWords);
   size_t o_ct = off; off += 256;
   size_t o_xb = off, o_ab = off, o_rb = off, o_hb = off, o_ssx = off, o_ssr = off, o_sc = off, o_kp = off,
-         o_kc = off, o_pv = off, o_pi = off;
+         o_kc = off, o_ad = off, o_pv = off, o_pi = off;
   if (B > 1) {
     // an operand image holds 16 fp16 columns per K index
     const size_t groups = (size_t)qd::gemv8_row_groups(d->vocab);
@@ -427,6 +428,7 @@ bool step_layout(const qd_model_desc* d, int splits, StepBuffers* b, size_t* tot
     o_sc = off; off += 256;
     o_kp = off; off += align256(4 * (size_t)qd::gemv8_row_groups((long)max_rows) * kBatchMaxKsplit * 2 * 128);
     o_kc = off; off += align256(4 * (size_t)kBatchCounters);
+    o_ad = off; off += align256(4 * B * (size_t)d->num_kv_heads);
     o_pv = off; off += align256(4 * groups * qd::kBatchMax);
     o_pi = off; off += align256(8 * groups * qd::kBatchMax);
   }
@@ -453,6 +455,7 @@ bool step_layout(const qd_model_desc* d, int splits, StepBuffers* b, size_t* tot
     b->sc_r = b->sc_x + qd::kBatchMax;
     b->kpart = reinterpret_cast<float*>(base + o_kp);
     b->kcount = reinterpret_cast<unsigned*>(base + o_kc);
+    b->attn_done = reinterpret_cast<unsigned*>(base + o_ad);
     b->part_val = reinterpret_cast<float*>(base + o_pv);
     b->part_idx = reinterpret_cast<long*>(base + o_pi);
   }
@@ -627,6 +630,7 @@ int batch_step(const qd_model_desc* d, hipStream_t s) {
                  (d->intermediate == 2048 || d->intermediate == 6144) && d->vocab % 16 == 0,
              QD_ERR_SHAPE, "batch step supports H = Hq*D = 2048, I in {2048, 6144}, vocab %% 16 == 0");
   const int splits = splits_of(d);
+  QD_REQUIRE(splits <= 64, QD_ERR_SHAPE, "batch step: at most 64 attention splits (got %d)", splits);
   StepBuffers b;
   size_t total = 0;
   step_layout(d, splits, &b, &total);
@@ -657,11 +661,10 @@ int batch_step(const qd_model_desc* d, hipStream_t s) {
     aa.rope_pos = d->rope_position; aa.inv_freq = d->inv_freq; aa.sec_h = d->sec_h; aa.sec_w = d->sec_w;
     aa.q_rot_out = b.q_rot;
     aa.batch = B; aa.bs_q = qkv_rows; aa.bs_cache = (long)Hkv * d->capacity * D;
-    aa.out_img = b.ab;
+    aa.out_img = b.ab; aa.done = b.attn_done;
     attn_ws(b.attn_ws, aa);
     aa.lse = aa.o_part + (size_t)B * Hq * splits * 128;
     if ((st = qd::attention_partial_launch<float>(aa, s))) return st;
-    if ((st = qd::attention_merge_launch<float>(aa, s))) return st;
     // r = x + W_o attn; image of r * post_norm * rstd(x)
     qd::Gemv8Args go;
     base(go, H, (long)Hq * D);

@@ -180,6 +180,27 @@ __device__ __forceinline__ void fence_release() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
 }
 
+// Fence-free hand-off of a few values: agent-coherent stores (written through
+// the XCD-private L2), a wait until this thread's stores have completed, then
+// an arrival count; the consumer reads with agent-coherent loads.
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void stores_done() { __builtin_amdgcn_s_waitcnt(0x0f70); }   // vmcnt(0)
+
+// Arrival of one workgroup (call from one thread after stores_done() and a
+// workgroup barrier): true for the last of `expected` arrivals, which also
+// re-arms the counter for the next launch.
+__device__ __forceinline__ bool arrive_last(unsigned* counter, unsigned expected) {
+  const unsigned old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const bool last = old == expected - 1;
+  if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return last;
+}
+
 // ---------------------------------------------------------------- batch operand images
 //
 // The B operand of the batch GEMV (v_mfma_f32_16x16x32_f16, 16 columns) for an

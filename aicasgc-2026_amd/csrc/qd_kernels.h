@@ -73,6 +73,8 @@ struct AttnArgs {
   int batch = 1;
   long bs_q = 0, bs_cache = 0;
   uint16_t* out_img = nullptr;        // merge: batch operand image of the output (instead of out)
+  unsigned* done = nullptr;           // [batch][Hkv] arrival counters: the last split of a kv head
+                                      // merges in the partial kernel (no merge launch), or null
 };
 
 // Partials of every (kv head, split); fused prologue when a.qkv != nullptr.
