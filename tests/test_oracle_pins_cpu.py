@@ -303,6 +303,44 @@ def test_greedy_generate_matches_step_by_step_decoding():
     assert toks2 == toks
 
 
+def test_oracle_batch_step_matches_transformers_per_sequence():
+    """Batch decode step (config 4 semantics): three sequences with different
+    cache lengths and rope positions share one call; each sequence's logits equal
+    transformers' Qwen3VLTextModel decoding that sequence alone after its own
+    prefill, so a mixed-up sequence index, position or cache row fails."""
+    from transformers.cache_utils import DynamicCache
+
+    from qwen3vl_hip import synthetic as syn
+
+    shape, oshape = _tiny()
+    w = syn.model_weights(15, shape)
+    hf = _hf_tiny_model(w, shape)
+    F32 = torch.float32
+    lengths, T = [5, 9, 2], 12
+    g = torch.Generator().manual_seed(15)
+    caches = [(torch.zeros(3, 2, T, 32, dtype=F32), torch.zeros(3, 2, T, 32, dtype=F32)) for _ in range(2)]
+    tokens, rope, ref = [], [], []
+    for b, L in enumerate(lengths):
+        ids = torch.randint(0, shape.vocab, (L,), generator=g)
+        pos = torch.arange(L).view(1, L).expand(3, L)
+        tok = int(torch.randint(0, shape.vocab, (1,), generator=g))
+        rp = L + 3 * b                                   # rope position differs from the cache position
+        with torch.no_grad():
+            cache = DynamicCache(config=hf.config)
+            hf(inputs_embeds=w.embed_tokens[ids].float()[None], position_ids=pos[:, None, :], past_key_values=cache,
+               use_cache=True)
+            out = hf(inputs_embeds=w.embed_tokens[tok].float().view(1, 1, -1), position_ids=torch.full((3, 1, 1), rp),
+                     past_key_values=cache, use_cache=True)
+            ref.append(out.last_hidden_state[0, -1] @ w.embed_tokens.float().T)
+        O.prefill(w, w.embed_tokens[ids].float(), pos, [(k[b:b + 1], v[b:b + 1]) for k, v in caches], oshape, F32)
+        tokens.append(tok)
+        rope.append(rp)
+    logits, toks = O.decode_step_batch(w, tokens, caches, lengths, rope, oshape, F32)
+    for b in range(3):
+        assert (logits[b] - ref[b]).abs().max() < 2e-5 * ref[b].abs().max(), f"sequence {b}"
+        assert toks[b] == int(torch.argmax(ref[b]))
+
+
 @pytest.mark.parametrize("L", [0, 4096])
 def test_step_roofline_bytes(L):
     assert O.roofline_bytes_step(L) == 3_441_154_048 + 114_688 * L
