@@ -3,8 +3,9 @@
 The hot path is one call of the native ``qd_decode_step`` (embedding row,
 28 layers of HIP kernels, final norm, lm_head + argmax) followed by
 ``qd_decode_advance`` (append the token, advance cache/rope positions on the
-device).  Both are captured once into a HIP graph (``torch.cuda.CUDAGraph``);
-generation is a loop of graph replays with no host writes in between.
+device).  Both are captured once into a HIP graph (``torch.cuda.CUDAGraph``),
+and 8 consecutive steps into a second graph; generation is a loop of graph
+replays with no host writes in between.
 
 Mirrors the reference's decode engine: GreedyDecodeEngine.generate
 (evaluation_wrapper.py:149-315) and DecodeCudaGraphRunner
@@ -32,15 +33,69 @@ def rope_inv_freq(shape: Qwen3VLTextShape = QWEN3VL_2B) -> torch.Tensor:
     return 1.0 / (shape.rope_theta ** (torch.arange(0, d, 2, dtype=torch.float32) / d))
 
 
-class DecodeEngine:
+class _CapturedSteps:
+    """HIP-graph capture shared by the engines: one step (``step_eager``:
+    decode + advance) in one graph, and ``steps_per_graph`` consecutive steps
+    in a second.  Each step reads the token and positions the previous step's
+    advance wrote on the device, so k steps replay as one graph launch and the
+    launch gap between graph replays is paid once per k tokens."""
+
+    def _state_tensors(self):
+        return (self.token, self.cache_position, self.rope_position, self.step_counter)
+
+    def capture(self) -> None:
+        # Warm up once on a side stream so lazy initialisation is not captured,
+        # restoring the device state (positions, counter, the cache rows the
+        # warm-up step wrote) afterwards.
+        saved = [t.clone() for t in self._state_tensors()]
+        snap = self._snapshot()
+        side = torch.cuda.Stream(self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(side):
+            self.step_eager()
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        torch.cuda.synchronize(self.device)
+        for t, v in zip(self._state_tensors(), saved):
+            t.copy_(v)
+        self._restore(snap)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.step_eager()
+        torch.cuda.synchronize(self.device)
+        self.graph = g
+        self.graph_multi = None
+        if self.steps_per_graph > 1:
+            gm = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gm):
+                for _ in range(self.steps_per_graph):
+                    self.step_eager()
+            torch.cuda.synchronize(self.device)
+            self.graph_multi = gm
+
+    def replay_steps(self, n: int) -> None:
+        """Enqueue n captured steps: n // k replays of the k-step graph, then
+        single-step replays."""
+        if self.graph is None:
+            self.capture()
+        k = self.steps_per_graph if self.graph_multi is not None else 1
+        for _ in range(n // k):
+            (self.graph_multi if k > 1 else self.graph).replay()
+        for _ in range(n % k):
+            self.graph.replay()
+
+
+class DecodeEngine(_CapturedSteps):
     """Owns device weights, the static KV cache and the captured decode step."""
 
     STEP_MODES = {"auto": _lib.STEP_AUTO, "chain": _lib.STEP_CHAIN, "persistent": _lib.STEP_PERSISTENT}
 
     def __init__(self, weights: ModelWeights, capacity: int, device="cuda", attn_splits: int = 0,
-                 keep_logits: bool = False, step_mode: str = "auto"):
+                 keep_logits: bool = False, step_mode: str = "auto", steps_per_graph: int = 8):
         if not torch.cuda.is_available():
             raise RuntimeError("DecodeEngine needs a ROCm GPU")
+        if steps_per_graph < 1:
+            raise ValueError("steps_per_graph must be >= 1")
+        self.steps_per_graph = int(steps_per_graph)
         self.device = torch.device(device)
         if self.device.index is None:
             self.device = torch.device("cuda", torch.cuda.current_device())
@@ -96,6 +151,7 @@ class DecodeEngine:
         d.workspace = self.workspace.data_ptr()
         self.desc = d
         self.graph = None
+        self.graph_multi = None
         self._graph_max_tokens = 0
 
     @property
@@ -129,6 +185,7 @@ class DecodeEngine:
         if self.out_tokens.numel() < n:
             self.out_tokens = torch.zeros(n, dtype=torch.int64, device=self.device)
             self.graph = None  # the captured advance kernel points at the old buffer
+            self.graph_multi = None
 
     # ------------------------------------------------------------ step
     def step_eager(self) -> None:
@@ -161,34 +218,13 @@ class DecodeEngine:
         return {name: self.workspace[o: o + 4 * n].view(torch.float32)
                 for (name, n), o in zip(sizes.items(), offs)}
 
-    def capture(self) -> None:
-        """Capture one step into a HIP graph (decode + advance)."""
-        # Warm up once on a side stream so lazy initialisation is not captured,
-        # restoring the device state afterwards.
-        saved = [t.clone() for t in (self.token, self.cache_position, self.rope_position, self.step_counter)]
-        snap = self._snapshot_row()
-        side = torch.cuda.Stream(self.device)
-        side.wait_stream(torch.cuda.current_stream(self.device))
-        with torch.cuda.stream(side):
-            self.step_eager()
-        torch.cuda.current_stream(self.device).wait_stream(side)
-        torch.cuda.synchronize(self.device)
-        for t, v in zip((self.token, self.cache_position, self.rope_position, self.step_counter), saved):
-            t.copy_(v)
-        self._restore_row(snap)
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            self.step_eager()
-        torch.cuda.synchronize(self.device)
-        self.graph = g
-
-    def _snapshot_row(self):
+    def _snapshot(self):
         pos = int(self.cache_position.item())
         if not (0 <= pos < self.capacity):
             return None
         return pos, [(k[:, :, pos].clone(), v[:, :, pos].clone()) for k, v in zip(self.k_caches, self.v_caches)]
 
-    def _restore_row(self, snap) -> None:
+    def _restore(self, snap) -> None:
         if snap is None:
             return
         pos, rows = snap
@@ -210,12 +246,10 @@ class DecodeEngine:
         self.reserve_tokens(n_steps)
         self.set_state(first_token, start_position, start_position + rope_delta)
         self.step_counter.zero_()
-        if use_graph and self.graph is None:
-            self.capture()
-        for _ in range(n_steps):
-            if use_graph:
-                self.graph.replay()
-            else:
+        if use_graph:
+            self.replay_steps(n_steps)
+        else:
+            for _ in range(n_steps):
                 self.step_eager()
         torch.cuda.synchronize(self.device)
         return self.out_tokens[:n_steps].tolist()
@@ -283,7 +317,7 @@ class DecodeEngine:
         return [first] + rest
 
 
-class BatchDecodeEngine:
+class BatchDecodeEngine(_CapturedSteps):
     """Greedy decoding of B (2..8) independent sequences per step (config 4).
 
     Every sequence has its own static cache rows ``[B, Hkv, T, D]`` per layer
@@ -295,9 +329,12 @@ class BatchDecodeEngine:
     """
 
     def __init__(self, weights: ModelWeights, batch: int, capacity: int, device="cuda", attn_splits: int = 0,
-                 keep_logits: bool = False):
+                 keep_logits: bool = False, steps_per_graph: int = 4):
         if not torch.cuda.is_available():
             raise RuntimeError("BatchDecodeEngine needs a ROCm GPU")
+        if steps_per_graph < 1:
+            raise ValueError("steps_per_graph must be >= 1")
+        self.steps_per_graph = int(steps_per_graph)
         if not 2 <= batch <= 8:
             raise ValueError("batch must be 2..8")
         self.device = torch.device(device)
@@ -350,6 +387,7 @@ class BatchDecodeEngine:
         d.workspace = self.workspace.data_ptr()
         self.desc = d
         self.graph = None
+        self.graph_multi = None
 
     def set_state(self, tokens, cache_positions, rope_positions) -> None:
         self.token.copy_(torch.as_tensor(tokens, dtype=torch.int64))
@@ -361,6 +399,7 @@ class BatchDecodeEngine:
         if self.out_tokens.shape[0] < n:
             self.out_tokens = torch.zeros(n, self.batch, dtype=torch.int64, device=self.device)
             self.graph = None
+            self.graph_multi = None
 
     def step_eager(self) -> None:
         st = ctypes.c_void_p(torch.cuda.current_stream(self.device).cuda_stream)
@@ -371,26 +410,7 @@ class BatchDecodeEngine:
             ctypes.c_void_p(self.rope_position.data_ptr()), int(self.out_tokens.shape[0]), self.batch, st),
             "qd_decode_advance_batch")
 
-    def capture(self) -> None:
-        """Capture step + advance into a HIP graph (warm-up on a side stream, state restored)."""
-        saved = [t.clone() for t in (self.token, self.cache_position, self.rope_position, self.step_counter)]
-        rows = self._snapshot_rows()
-        side = torch.cuda.Stream(self.device)
-        side.wait_stream(torch.cuda.current_stream(self.device))
-        with torch.cuda.stream(side):
-            self.step_eager()
-        torch.cuda.current_stream(self.device).wait_stream(side)
-        torch.cuda.synchronize(self.device)
-        for t, v in zip((self.token, self.cache_position, self.rope_position, self.step_counter), saved):
-            t.copy_(v)
-        self._restore_rows(rows)
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            self.step_eager()
-        torch.cuda.synchronize(self.device)
-        self.graph = g
-
-    def _snapshot_rows(self):
+    def _snapshot(self):
         pos = self.cache_position.tolist()
         snap = []
         for k, v in zip(self.k_caches, self.v_caches):
@@ -398,7 +418,7 @@ class BatchDecodeEngine:
                          for b, p in enumerate(pos)])
         return pos, snap
 
-    def _restore_rows(self, rows) -> None:
+    def _restore(self, rows) -> None:
         pos, snap = rows
         for (k, v), per in zip(zip(self.k_caches, self.v_caches), snap):
             for b, (p, kv) in enumerate(zip(pos, per)):
@@ -415,12 +435,10 @@ class BatchDecodeEngine:
         self.reserve_tokens(n_steps)
         self.set_state(first_tokens, start_positions, rope_positions)
         self.step_counter.zero_()
-        if use_graph and self.graph is None:
-            self.capture()
-        for _ in range(n_steps):
-            if use_graph:
-                self.graph.replay()
-            else:
+        if use_graph:
+            self.replay_steps(n_steps)
+        else:
+            for _ in range(n_steps):
                 self.step_eager()
         torch.cuda.synchronize(self.device)
         return self.out_tokens[:n_steps].tolist()
