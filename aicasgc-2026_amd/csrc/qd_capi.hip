@@ -60,14 +60,16 @@ using u16 = uint16_t;
 inline hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
 inline bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Workspace layout of the lm_head argmax: [counter (256 B)] [vals] [idx].
+// Workspace layout of the lm_head argmax: [counter (256 B)] [vals] [idx].  The
+// counter (fused reduction by the last block) is used only where the
+// workspace is known to be zeroed: the decode step's.
 constexpr size_t kArgmaxHeader = 256;
 size_t argmax_ws_bytes() {
   return kArgmaxHeader + (size_t)qd::kMaxArgmaxBlocks * (sizeof(float) + sizeof(long));
 }
-void argmax_ws(void* ws, GemvArgs& a) {
+void argmax_ws(void* ws, GemvArgs& a, bool fused_reduce = false) {
   char* b = reinterpret_cast<char*>(ws);
-  a.counter = reinterpret_cast<unsigned*>(b);
+  a.counter = fused_reduce ? reinterpret_cast<unsigned*>(b) : nullptr;
   a.part_idx = reinterpret_cast<long*>(b + kArgmaxHeader);
   a.part_val = reinterpret_cast<float*>(b + kArgmaxHeader + (size_t)qd::kMaxArgmaxBlocks * sizeof(long));
 }
@@ -702,6 +704,9 @@ int batch_step(const qd_model_desc* d, hipStream_t s) {
 
 }  // namespace
 
+static int step_phases(const qd_model_desc* d, int first_layer, int n_layers, unsigned phase_mask, bool advance,
+                       void* stream);
+
 int qd_decode_step(const qd_model_desc* d, void* stream) {
   QD_REQUIRE(d, QD_ERR_ARG, "null descriptor");
   const int mode = qd_decode_step_mode(d);
@@ -711,14 +716,14 @@ int qd_decode_step(const qd_model_desc* d, void* stream) {
     if (st) return st;
     return batch_step(d, S(stream));
   }
-  if (mode == QD_STEP_CHAIN) return qd_decode_step_phases(d, 0, d->num_layers, QD_PHASE_ALL, stream);
+  if (mode == QD_STEP_CHAIN) return step_phases(d, 0, d->num_layers, QD_PHASE_ALL, true, stream);
   int st = qd_decode_step_phases(d, 0, 0, 0, stream);  // descriptor checks only
   if (st) return st;
   StepBuffers b;
   size_t total = 0;
   step_layout(d, splits_of(d), &b, &total);
   if ((st = launch_persistent(d, b, S(stream)))) return st;
-  return qd_decode_step_phases(d, 0, 0, QD_PHASE_LM_HEAD, stream);
+  return step_phases(d, 0, 0, QD_PHASE_LM_HEAD, true, stream);
 }
 
 int qd_decode_layers_persistent(const qd_model_desc* d, void* stream) {
@@ -750,8 +755,11 @@ int qd_decode_status(const qd_model_desc* d, unsigned* status, int reset) {
   return QD_OK;
 }
 
-int qd_decode_step_phases(const qd_model_desc* d, int first_layer, int n_layers, unsigned phase_mask,
-                          void* stream) {
+// The kernel chain of a batch-1 step (the phases in phase_mask); `advance`:
+// the lm_head's last workgroup also performs the descriptor's end-of-step
+// advance (qd_decode_step only, never for phase-wise runs).
+static int step_phases(const qd_model_desc* d, int first_layer, int n_layers, unsigned phase_mask, bool advance,
+                       void* stream) {
   QD_REQUIRE(d && d->layers && d->embed && d->final_norm && d->token && d->cache_position && d->rope_position &&
                  d->inv_freq && d->workspace,
              QD_ERR_ARG, "incomplete model descriptor");
@@ -813,9 +821,19 @@ int qd_decode_step_phases(const qd_model_desc* d, int first_layer, int n_layers,
   GemvArgs gl;
   gl.x = b.x; gl.gamma = (const u16*)d->final_norm; gl.eps = d->eps; gl.W = (const u16*)d->embed;
   gl.N = d->vocab; gl.K = H; gl.ldw = H; gl.y = d->logits_out; gl.token = d->token;
-  argmax_ws(b.argmax_ws, gl);
+  argmax_ws(b.argmax_ws, gl, true);
+  if (advance && d->advance_counter != nullptr) {
+    gl.adv_out = d->advance_out_tokens; gl.adv_counter = d->advance_counter;
+    gl.adv_cache_position = const_cast<int64_t*>(d->cache_position);
+    gl.adv_rope_position = const_cast<int64_t*>(d->rope_position); gl.adv_max_tokens = d->advance_max_tokens;
+  }
   if (phase_mask & QD_PHASE_LM_HEAD) return qd::gemv_argmax<qd::PRO_RMSNORM, float, u16>(gl, s);
   return QD_OK;
+}
+
+int qd_decode_step_phases(const qd_model_desc* d, int first_layer, int n_layers, unsigned phase_mask,
+                          void* stream) {
+  return step_phases(d, first_layer, n_layers, phase_mask, false, stream);
 }
 
 int qd_decode_advance(const int64_t* token, int64_t* out_tokens, int64_t* counter, int64_t* cache_position,

@@ -42,6 +42,52 @@ __device__ __forceinline__ void load_rows(const GemvArgs& a, long o0, long kofs,
   }
 }
 
+// First maximal index over n per-block partials (whole block, 256 threads),
+// read with agent-coherent loads: the last block of a fused lm_head + argmax.
+// Writes a.token[0] and, when a.adv_counter is set, advances the decode state
+// as decode_advance_kernel does.
+__device__ __forceinline__ void argmax_finish(const GemvArgs& a, int n) {
+  __shared__ float r_v[256];
+  __shared__ long r_i[256];
+  float bv = -INFINITY;
+  long bi = 0x7fffffffffffL;
+  for (int b = threadIdx.x; b < n; b += blockDim.x) {
+    const float v = load_coherent(a.part_val + b);
+    const long i = load_coherent(a.part_idx + b);
+    if (v > bv || (v == bv && i < bi)) {
+      bv = v;
+      bi = i;
+    }
+  }
+  r_v[threadIdx.x] = bv;
+  r_i[threadIdx.x] = bi;
+  __syncthreads();
+  for (int s = blockDim.x / 2; s > 0; s >>= 1) {
+    if ((int)threadIdx.x < s) {
+      const float v = r_v[threadIdx.x + s];
+      const long i = r_i[threadIdx.x + s];
+      if (v > r_v[threadIdx.x] || (v == r_v[threadIdx.x] && i < r_i[threadIdx.x])) {
+        r_v[threadIdx.x] = v;
+        r_i[threadIdx.x] = i;
+      }
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const int64_t tok = r_i[0] == 0x7fffffffffffL ? 0 : (int64_t)r_i[0];
+    a.token[0] = tok;
+    if (a.adv_counter != nullptr) {
+      const int64_t c = a.adv_counter[0];
+      if (a.adv_out != nullptr && c < a.adv_max_tokens) a.adv_out[c] = tok;
+      a.adv_counter[0] = c + 1;
+      a.adv_cache_position[0] += 1;
+      a.adv_rope_position[0] += 1;
+      a.adv_rope_position[1] += 1;
+      a.adv_rope_position[2] += 1;
+    }
+  }
+}
+
 // PIPE: issue the next row group's loads right after the dot products (only
 // worth its registers when a wave walks many row groups, i.e. the lm_head).
 template <int KCH, int R, int PRO, int EPI, typename TX, typename TY, bool PIPE = (EPI == EPI_ARGMAX)>
@@ -188,9 +234,11 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
   }
 
   if constexpr (EPI == EPI_ARGMAX) {
-    // per-block (max, first index); reduced by argmax_reduce_kernel in the next launch
+    // per-block (max, first index); reduced by argmax_reduce_kernel in the next
+    // launch, or (a.counter set) by the last block to finish
     __shared__ float s_v[16];
     __shared__ long s_i[16];
+    __shared__ int s_last;
     if (lane == 0) {
       s_v[wib] = best_v;
       s_i[wib] = best_i;
@@ -205,8 +253,19 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
           bi = s_i[w];
         }
       }
-      a.part_val[blockIdx.x] = bv;
-      a.part_idx[blockIdx.x] = bi;
+      if (a.counter == nullptr) {
+        a.part_val[blockIdx.x] = bv;
+        a.part_idx[blockIdx.x] = bi;
+      } else {
+        store_coherent(a.part_val + blockIdx.x, bv);
+        store_coherent(a.part_idx + blockIdx.x, bi);
+        stores_done();
+        s_last = arrive_last(a.counter, gridDim.x);
+      }
+    }
+    if (a.counter != nullptr) {
+      __syncthreads();
+      if (s_last) argmax_finish(a, (int)gridDim.x);
     }
   }
 }
@@ -371,7 +430,7 @@ int gemv_argmax(const GemvArgs& a, hipStream_t s) {
   if (max_blocks > kMaxArgmaxBlocks) max_blocks = kMaxArgmaxBlocks;
   long blocks = 0;
   int st = launch_k<4, PRO, EPI_ARGMAX, TX, TY>(a, a.K, 1, max_blocks, s, &blocks);
-  if (st != QD_OK) return st;
+  if (st != QD_OK || a.counter != nullptr) return st;
   hipLaunchKernelGGL(argmax_reduce_kernel, dim3(1), dim3(kThreads), 0, s, a.part_val, a.part_idx, (int)blocks,
                      a.token);
   return qd_host::launch_status("argmax_reduce_kernel");

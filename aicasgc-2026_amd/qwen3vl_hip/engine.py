@@ -90,7 +90,8 @@ class DecodeEngine(_CapturedSteps):
     STEP_MODES = {"auto": _lib.STEP_AUTO, "chain": _lib.STEP_CHAIN, "persistent": _lib.STEP_PERSISTENT}
 
     def __init__(self, weights: ModelWeights, capacity: int, device="cuda", attn_splits: int = 0,
-                 keep_logits: bool = False, step_mode: str = "auto", steps_per_graph: int = 8):
+                 keep_logits: bool = False, step_mode: str = "auto", steps_per_graph: int = 8,
+                 fuse_advance: bool = True):
         if not torch.cuda.is_available():
             raise RuntimeError("DecodeEngine needs a ROCm GPU")
         if steps_per_graph < 1:
@@ -153,6 +154,8 @@ class DecodeEngine(_CapturedSteps):
         self.graph = None
         self.graph_multi = None
         self._graph_max_tokens = 0
+        if fuse_advance:
+            self._bind_advance()
 
     @property
     def step_mode(self) -> str:
@@ -184,14 +187,24 @@ class DecodeEngine(_CapturedSteps):
     def reserve_tokens(self, n: int) -> None:
         if self.out_tokens.numel() < n:
             self.out_tokens = torch.zeros(n, dtype=torch.int64, device=self.device)
-            self.graph = None  # the captured advance kernel points at the old buffer
+            self.graph = None  # the captured advance points at the old buffer
             self.graph_multi = None
+            self._bind_advance()
+
+    def _bind_advance(self) -> None:
+        """The step ends with the position advance, fused into its last kernel."""
+        d = self.desc
+        d.advance_out_tokens = self.out_tokens.data_ptr()
+        d.advance_counter = self.step_counter.data_ptr()
+        d.advance_max_tokens = int(self.out_tokens.numel())
 
     # ------------------------------------------------------------ step
     def step_eager(self) -> None:
         """Enqueue one decode step + advance on the current stream."""
         st = torch.cuda.current_stream(self.device).cuda_stream
         _lib.check(_lib.lib().qd_decode_step(ctypes.byref(self.desc), ctypes.c_void_p(st)), "qd_decode_step")
+        if self.desc.advance_counter:
+            return
         _lib.check(_lib.lib().qd_decode_advance(
             ctypes.c_void_p(self.token.data_ptr()), ctypes.c_void_p(self.out_tokens.data_ptr()),
             ctypes.c_void_p(self.step_counter.data_ptr()), ctypes.c_void_p(self.cache_position.data_ptr()),

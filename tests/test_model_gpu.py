@@ -44,10 +44,17 @@ def test_two_layer_model_greedy_matches_oracle(cuda, step_mode):
     ref, margins, _ = O.greedy_generate(w, prompt, n, cap)
     print(f"gpu {toks}\noracle {ref}\nmin margin {min(margins):.4g}", flush=True)
     assert toks == ref
-    # eager decode from the same state gives the same tokens as graph replay
-    eng2 = DecodeEngine(w.to(cuda), capacity=cap, step_mode=step_mode)
+    # eager decode from the same state gives the same tokens as graph replay,
+    # with the position advance as its own launch instead of fused into the lm_head
+    eng2 = DecodeEngine(w.to(cuda), capacity=cap, step_mode=step_mode, fuse_advance=False)
     first = eng2.prefill(prompt)
     assert eng2.decode(first, prompt.length, prompt.rope_delta, n - 1, use_graph=False) == toks[1:]
+    # one graph per step instead of several (steps_per_graph=1), fused advance
+    eng3 = DecodeEngine(w.to(cuda), capacity=cap, step_mode=step_mode, steps_per_graph=1)
+    first = eng3.prefill(prompt)
+    assert eng3.decode(first, prompt.length, prompt.rope_delta, n - 1, use_graph=True) == toks[1:]
+    assert int(eng3.step_counter.item()) == n - 1
+    assert int(eng3.cache_position.item()) == prompt.length + n - 1
 
 
 @pytest.fixture(scope="module")
