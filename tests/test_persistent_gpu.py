@@ -4,8 +4,9 @@ kernel-chain step on the same inputs.
 
 Cases cover the attention split edge cases of the persistent kernel (32
 splits per kv head): a context of one row (cache_position 0), fewer rows than
-splits, a context that is not a multiple of the split size, and a full
-4096-row cache.
+splits, a context that is not a multiple of the split size, a full 4096-row
+cache and an 8000-row context (several K/V batches per split).  The lm_head's
+fused argmax (last workgroup reduces the partials) is checked on ties.
 """
 
 from __future__ import annotations
@@ -38,7 +39,7 @@ def _oracle_step(w, token, kc, vc, pos, rope_pos):
     return h, logits, tok
 
 
-@pytest.mark.parametrize("pos,cap", [(0, 64), (5, 64), (45, 64), (1000, 1030), (4095, 4096)])
+@pytest.mark.parametrize("pos,cap", [(0, 64), (5, 64), (45, 64), (1000, 1030), (4095, 4096), (8000, 8192)])
 def test_persistent_step_matches_oracle_and_chain(cuda, two_layer_weights, pos, cap):
     from qwen3vl_hip import synthetic as syn
     from qwen3vl_hip.engine import DecodeEngine
@@ -124,3 +125,21 @@ def test_persistent_mode_rejected_for_other_shapes(cuda):
     with pytest.raises(RuntimeError, match="specialised"):
         eng_p.decode(1, 0, 0, 1, use_graph=False)
     assert _lib.lib().qd_decode_layers_persistent(None, None) != 0
+
+
+def test_fused_argmax_ties_take_the_first_index(cuda):
+    """Every embedding row identical: all logits tie, so each step's token is 0
+    (torch.argmax takes the first maximum) through the lm_head's last-workgroup
+    reduction over all its blocks, in both step modes; the fused advance moves
+    the positions and the counter once per step."""
+    from qwen3vl_hip import synthetic as syn
+    from qwen3vl_hip.config import Qwen3VLTextShape
+    from qwen3vl_hip.engine import DecodeEngine
+
+    w = syn.model_weights(9, shape=Qwen3VLTextShape(num_layers=2, vocab=VOCAB))
+    w.embed_tokens[:] = w.embed_tokens[3].clone()
+    for mode in ("persistent", "chain"):
+        eng = DecodeEngine(w, capacity=64, step_mode=mode)
+        assert eng.decode(5, 10, 0, 6, use_graph=True) == [0] * 6
+        assert int(eng.cache_position.item()) == 16 and int(eng.step_counter.item()) == 6
+        assert eng.rope_position.tolist() == [16, 16, 16]
