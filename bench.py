@@ -29,6 +29,7 @@ import os
 import platform
 import sys
 import time
+import types
 from pathlib import Path
 
 REPO = Path(__file__).resolve().parent
@@ -37,6 +38,7 @@ for _p in (str(REPO), str(REPO / "aicasgc-2026_amd")):
         sys.path.insert(0, _p)
 
 PEAK_HBM_GBPS = 8000.0
+PEAK_FP16_TFLOPS = 2500.0   # dense fp16 MFMA
 WEIGHT_SEED = 3
 PROMPT_SEED = 3
 
@@ -95,11 +97,60 @@ def bench_batch8(w, steps: int, warmup: int = 4) -> dict:
     nbytes = sum(per_step) / steps
     gbps = nbytes / (ms * 1e-3) / 1e9
     del eng
+    # GEMV flops on MFMA (2 per weight and sequence; attention runs on the VALU)
+    s = w.shape
+    gemv_params = s.num_layers * (s.qkv_rows * s.hidden + s.hidden * s.q_size + 3 * s.intermediate * s.hidden) \
+        + s.vocab * s.hidden
+    mfma_tflops = 2 * 8 * gemv_params / (ms * 1e-3) / 1e12
     return {"workload": "config4: 8 sequences, valid KV lengths U[2048,4096] (seeded), greedy, 4 steps per HIP graph",
             "kv_lengths": lens, "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 4),
             "tokens_per_s": round(8 * 1000.0 / ms, 1), "step_bytes": int(nbytes), "achieved_GBps": round(gbps, 1),
             "roofline_frac": round(gbps / PEAK_HBM_GBPS, 4),
-            "roofline_ms": round(nbytes / (PEAK_HBM_GBPS * 1e9) * 1e3, 4)}
+            "roofline_ms": round(nbytes / (PEAK_HBM_GBPS * 1e9) * 1e3, 4),
+            "mfma": {"gflop_per_step": round(2 * 8 * gemv_params / 1e9, 2), "achieved_TFLOPs": round(mfma_tflops, 2),
+                     "peak_TFLOPs": PEAK_FP16_TFLOPS, "frac": round(mfma_tflops / PEAK_FP16_TFLOPS, 5)}}
+
+
+def cpu_baseline_batch8(weights_gpu, n_steps: int = 2) -> dict:
+    """Config 4 on the host: the oracle's batch step (each sequence its own
+    fp32 step on its own cache rows) at the batch-8 KV lengths, random K/V."""
+    import torch
+
+    from oracle import qwen3vl_oracle as O
+    from qwen3vl_hip import synthetic as syn
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    s = weights_gpu.shape
+    f32 = types.SimpleNamespace(
+        embed_tokens=weights_gpu.embed_tokens.detach().to("cpu", torch.float32),
+        final_norm_weight=weights_gpu.final_norm_weight.detach().to("cpu", torch.float32),
+        layers=[{k: v.detach().to("cpu", torch.float32) for k, v in lw.tensors().items()}
+                for lw in weights_gpu.layers])
+    lens = [int(v) for v in syn.batch8_kv_lengths()]
+    cap = max(lens) + n_steps + 1
+    g = torch.Generator().manual_seed(98)
+    caches = [(torch.randn(8, s.num_kv_heads, cap, s.head_dim, generator=g).half(),
+               torch.randn(8, s.num_kv_heads, cap, s.head_dim, generator=g).half()) for _ in range(s.num_layers)]
+    toks, pos, times = [11, 22, 33, 44, 55, 66, 77, 88], list(lens), []
+    for _ in range(n_steps):
+        t0 = time.perf_counter()
+        _, toks = O.decode_step_batch(f32, toks, caches, pos, pos)
+        times.append(time.perf_counter() - t0)
+        pos = [p + 1 for p in pos]
+    return {"value": round(1000.0 * sorted(times)[len(times) // 2], 1), "unit": "ms/step", "cores": cores,
+            "kind": "port",
+            "sample": f"median of {n_steps} batch-8 steps of the oracle's fp32 restatement at the KV lengths above"}
+
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
 
 def cpu_baseline(weights_gpu, prompt_len: int, n_steps: int, warmup: int = 2) -> dict:
@@ -145,7 +196,7 @@ def cpu_baseline(weights_gpu, prompt_len: int, n_steps: int, warmup: int = 2) ->
         "kind": "port",
         "sample": (f"median of {n_steps} decode steps (after {warmup} warm-up) of the oracle's fp32 PyTorch "
                    f"restatement of the 28-layer step + lm_head at context ~{prompt_len}, random K/V prefix, "
-                   f"torch threads={cores}, cpu={platform.processor() or platform.machine()}"),
+                   f"torch threads={cores}, cpu={_cpu_model()}"),
     }
 
 
@@ -156,7 +207,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--ctx-steps", type=int, default=64, help="decode steps timed around a 4096 context")
     ap.add_argument("--kernel-reps", type=int, default=10, help="repetitions of the gate_up timing (x28 launches)")
-    ap.add_argument("--cpu-steps", type=int, default=12)
+    ap.add_argument("--cpu-steps", type=int, default=40)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--attn-splits", type=int, default=0)
     ap.add_argument("--step-mode", choices=["auto", "chain", "persistent"], default="auto")
@@ -323,6 +374,9 @@ def main() -> int:
         log("cpu baseline ...")
         cpu = cpu_baseline(w, prompt.length, args.cpu_steps)
         log(f"cpu baseline {cpu['value']} ms/token on {cpu['cores']} cores")
+        if b8 is not None:
+            b8["cpu_baseline"] = cpu_baseline_batch8(w)
+            log(f"cpu baseline batch8 {b8['cpu_baseline']['value']} ms/step")
 
     out = {
         "metric": "bs1 decode ms/token, Qwen3-VL-2B fp16; achieved HBM GB/s vs 8 TB/s peak",
