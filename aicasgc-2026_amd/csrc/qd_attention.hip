@@ -36,28 +36,30 @@ constexpr int kFusedMergeMaxSplits = 64;
 constexpr int kD = 128;
 constexpr int kHalf = 64;
 constexpr int kSlots = 16;
-constexpr int kUnroll = 8;
+constexpr int kUnroll = 4;
 }  // namespace
 
-// RMSNorm(head) * w then rotate-half RoPE on the pair (j, j + 64) held by lane j.
-__device__ __forceinline__ void head_norm_rope(float x0, float x1, const uint16_t* w, float eps, float c, float s,
-                                               int j, float& o0, float& o1) {
+// RMSNorm(head) * w then rotate-half RoPE on the pair (j, j + 64) held by lane
+// j; w0 / w1 are the norm weights of dims j and j + 64 (fp16 bits).
+__device__ __forceinline__ void head_norm_rope(float x0, float x1, unsigned w0, unsigned w1, float eps, float c,
+                                               float s, float& o0, float& o1) {
   const float ss = wave_sum(x0 * x0 + x1 * x1);
   const float rstd = rsqrtf(ss / (float)kD + eps);
-  const float n0 = (x0 * rstd) * h2f(w[j]);
-  const float n1 = (x1 * rstd) * h2f(w[j + kHalf]);
+  const float n0 = (x0 * rstd) * h2f((uint16_t)w0);
+  const float n1 = (x1 * rstd) * h2f((uint16_t)w1);
   o0 = n0 * c - n1 * s;
   o1 = n1 * c + n0 * s;
 }
 
-// cos/sin of frequency slot j from the (T, H, W) rope positions (interleaved
-// M-RoPE: j % 3 == 1 (j < 3*sec_h) -> H, j % 3 == 2 (j < 3*sec_w) -> W, else T).
-__device__ __forceinline__ void mrope_cs(const int64_t* pos3, const float* inv_freq, int sec_h, int sec_w, int j,
+// cos/sin of frequency slot j (inverse frequency inv_freq_j) from the (T, H, W)
+// rope positions (interleaved M-RoPE: j % 3 == 1 (j < 3*sec_h) -> H,
+// j % 3 == 2 (j < 3*sec_w) -> W, else T).
+__device__ __forceinline__ void mrope_cs(long pt, long ph, long pw, float inv_freq_j, int sec_h, int sec_w, int j,
                                          float& c, float& s) {
-  int stream = 0;
-  if (j % 3 == 1 && j < 3 * sec_h) stream = 1;
-  else if (j % 3 == 2 && j < 3 * sec_w) stream = 2;
-  const float f = (float)pos3[stream] * inv_freq[j];
+  long p = pt;
+  if (j % 3 == 1 && j < 3 * sec_h) p = ph;
+  else if (j % 3 == 2 && j < 3 * sec_w) p = pw;
+  const float f = (float)p * inv_freq_j;
   sincosf(f, &s, &c);
 }
 
@@ -90,19 +92,31 @@ __device__ __forceinline__ void online_softmax_batch(const u32x4 (&kk)[kUnroll],
   }
 }
 
-// K/V rows of positions t, t+16, ... into registers; rows >= t1 (and the new
-// position in the fused variant, patched from LDS by the caller) read as zero.
+// K/V rows of positions t, t+16, ... into registers.  The loads are
+// unconditional (rows past t1 re-read row t1 - 1, an L1/L2 hit) so the number
+// of loads in flight is the same on every path and a wave waits only for the
+// batch it consumes; kv_select() zeroes the rows >= t1 and the skipped row.
 __device__ __forceinline__ void load_kv_batch(const uint16_t* kb, const uint16_t* vb, long stride_s, int t, int t1,
-                                              long skip, u32x4 (&kk)[kUnroll], u32x4 (&vv)[kUnroll]) {
+                                              u32x4 (&kk)[kUnroll], u32x4 (&vv)[kUnroll]) {
+  const int last = t1 > 0 ? t1 - 1 : 0;
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int tt = min(t + u * kSlots, last);
+    kk[u] = ld_stream(kb + (long)tt * stride_s);
+    vv[u] = ld_stream(vb + (long)tt * stride_s);
+  }
+}
+
+// Rows >= t1 and row `skip` of a loaded batch read as zero (stale cache rows may
+// hold any bit pattern; a zero V keeps them out of the accumulators).
+__device__ __forceinline__ void kv_select(int t, int t1, long skip, u32x4 (&kk)[kUnroll], u32x4 (&vv)[kUnroll]) {
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
     const int tt = t + u * kSlots;
-    kk[u] = u32x4{0u, 0u, 0u, 0u};
-    vv[u] = u32x4{0u, 0u, 0u, 0u};
-    if (tt < t1 && tt != skip) {
-      kk[u] = ld_stream(kb + (long)tt * stride_s);
-      vv[u] = ld_stream(vb + (long)tt * stride_s);
-    }
+    const bool keep = tt < t1 && tt != skip;
+    const u32x4 z = {0u, 0u, 0u, 0u};
+    kk[u] = keep ? kk[u] : z;
+    vv[u] = keep ? vv[u] : z;
   }
 }
 
@@ -143,33 +157,67 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
   const int wave_t0 = t0 + (threadIdx.x / kWave) * 4;
   const int row_off = slot - (threadIdx.x / kWave) * 4;
   const long skip = FUSED_ROPE ? pos : -1;
-  u32x4 kk[kUnroll], vv[kUnroll];
-  load_kv_batch(kb, vb, a.stride_s, wave_t0 + row_off, t1, skip, kk, vv);
+
+  // The prologue's own inputs are loaded first, then two batches of K/V rows
+  // (A: kk/vv, B: kn/vn), which do not depend on the prologue.  Loads complete
+  // in issue order, so the prologue waits only for its inputs while the K/V rows
+  // are in flight.  A and B alternate roles in the loop below (no register
+  // copies, which would wait for the loads).
+  constexpr int kPre = (G + 2 + 3) / 4;   // prologue items (q heads, k, v) per wave
+  const int w = threadIdx.x / kWave;
+  const int j = lane_id();
+  float pre[kPre][2] = {};
+  unsigned pw[kPre][2] = {};   // fp16 bits, one per register (packing would wait for the loads)
+  float ifq = 0.f;
+  float q[G][8];
+  if constexpr (FUSED_ROPE) {
+    ifq = a.inv_freq[j];
+#pragma unroll
+    for (int i = 0; i < kPre; ++i) {
+      const int item = w + 4 * i;
+      if (item < G + 2) {
+        const TQ* src = item < G    ? qkv + (long)(kvh * G + item) * kD
+                        : item == G ? qkv + (long)a.Hq * kD + (long)kvh * kD
+                                    : qkv + (long)(a.Hq + a.Hkv) * kD + (long)kvh * kD;
+        pre[i][0] = load_act(src, j);
+        pre[i][1] = load_act(src, j + kHalf);
+        if (item <= G) {
+          const uint16_t* nw = item < G ? a.q_weight : a.k_weight;
+          pw[i][0] = nw[j];
+          pw[i][1] = nw[j + kHalf];
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int g = 0; g < G; ++g) load_act8(q_in, (long)(kvh * G + g) * a.q_stride + dl, q[g]);
+  }
+  constexpr int kStep = kSlots * kUnroll;
+  u32x4 kk[kUnroll], vv[kUnroll], kn[kUnroll], vn[kUnroll];
+  load_kv_batch(kb, vb, a.stride_s, wave_t0 + row_off, t1, kk, vv);
+  load_kv_batch(kb, vb, a.stride_s, wave_t0 + kStep + row_off, t1, kn, vn);
 
   __shared__ float s_q[G][kD];
   __shared__ __align__(16) uint16_t s_kv[2][kD];   // new token's K_rot and V, fp16 as cached
   if constexpr (FUSED_ROPE) {
-    const int w = threadIdx.x / kWave;
-    const int j = lane_id();
     float c, s;
-    mrope_cs(rope_pos, a.inv_freq, a.sec_h, a.sec_w, j, c, s);
-    for (int item = w; item < G + 2; item += 4) {
+    mrope_cs(rope_pos[0], rope_pos[1], rope_pos[2], ifq, a.sec_h, a.sec_w, j, c, s);
+#pragma unroll
+    for (int i = 0; i < kPre; ++i) {
+      const int item = w + 4 * i;
       if (item < G) {
-        const TQ* src = qkv + (long)(kvh * G + item) * kD;
         float o0, o1;
-        head_norm_rope(load_act(src, j), load_act(src, j + kHalf), a.q_weight, a.eps, c, s, j, o0, o1);
+        head_norm_rope(pre[i][0], pre[i][1], pw[i][0], pw[i][1], a.eps, c, s, o0, o1);
         s_q[item][j] = o0;
         s_q[item][j + kHalf] = o1;
       } else if (item == G) {
-        const TQ* src = qkv + (long)a.Hq * kD + (long)kvh * kD;
         float o0, o1;
-        head_norm_rope(load_act(src, j), load_act(src, j + kHalf), a.k_weight, a.eps, c, s, j, o0, o1);
+        head_norm_rope(pre[i][0], pre[i][1], pw[i][0], pw[i][1], a.eps, c, s, o0, o1);
         s_kv[0][j] = f2h(o0);
         s_kv[0][j + kHalf] = f2h(o1);
-      } else {
-        const TQ* src = qkv + (long)(a.Hq + a.Hkv) * kD + (long)kvh * kD;
-        s_kv[1][j] = f2h(load_act(src, j));
-        s_kv[1][j + kHalf] = f2h(load_act(src, j + kHalf));
+      } else if (item == G + 1) {
+        s_kv[1][j] = f2h(pre[i][0]);
+        s_kv[1][j + kHalf] = f2h(pre[i][1]);
       }
     }
     __syncthreads();
@@ -186,15 +234,11 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
     }
   }
 
-  float q[G][8];
+  if constexpr (FUSED_ROPE) {
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    if constexpr (FUSED_ROPE) {
+    for (int g = 0; g < G; ++g)
 #pragma unroll
       for (int i = 0; i < 8; ++i) q[g][i] = s_q[g][dl + i];
-    } else {
-      load_act8(q_in, (long)(kvh * G + g) * a.q_stride + dl, q[g]);
-    }
   }
 
   float m[G], l[G], acc[G][8];
@@ -206,21 +250,26 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
     for (int i = 0; i < 8; ++i) acc[g][i] = 0.f;
   }
 
-#pragma unroll 1
-  for (int tw = wave_t0; tw < t1; tw += kSlots * kUnroll) {
-    const int t = tw + row_off;
-    if (tw != wave_t0) load_kv_batch(kb, vb, a.stride_s, t, t1, skip, kk, vv);
+  // the new position comes from LDS (fp16, as written to the cache)
+  auto consume = [&](u32x4 (&bk)[kUnroll], u32x4 (&bv)[kUnroll], int t) {
+    kv_select(t, t1, skip, bk, bv);
     if constexpr (FUSED_ROPE) {
-      // the new position comes from LDS (fp16, as written to the cache)
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
         if (t + u * kSlots == pos && pos < t1) {
-          kk[u] = *reinterpret_cast<const u32x4*>(&s_kv[0][dl]);
-          vv[u] = *reinterpret_cast<const u32x4*>(&s_kv[1][dl]);
+          bk[u] = *reinterpret_cast<const u32x4*>(&s_kv[0][dl]);
+          bv[u] = *reinterpret_cast<const u32x4*>(&s_kv[1][dl]);
         }
       }
     }
-    online_softmax_batch<G>(kk, vv, t, t1, q, a.scale, m, l, acc);
+    online_softmax_batch<G>(bk, bv, t, t1, q, a.scale, m, l, acc);
+  };
+#pragma unroll 1
+  for (int tw = wave_t0; tw < t1; tw += 2 * kStep) {
+    consume(kk, vv, tw + row_off);
+    load_kv_batch(kb, vb, a.stride_s, tw + 2 * kStep + row_off, t1, kk, vv);
+    if (tw + kStep < t1) consume(kn, vn, tw + kStep + row_off);
+    load_kv_batch(kb, vb, a.stride_s, tw + 3 * kStep + row_off, t1, kn, vn);
   }
 
   // ---- merge the 16 slots of this workgroup into one (output, LSE) per q head
