@@ -13,7 +13,7 @@
 // per-row-group partial sums of squares written by the same producer.
 //
 // A workgroup (8 waves) owns 16 rows (the MFMA M dimension; 16 gate + 16 up
-// rows for the SiLU epilogue) and a K range of KW (1024, 2048 or 3072); wave w owns
+// rows for the SiLU epilogue) and a K range of KW (1024, 2048, 3072 or 6144); wave w owns
 // the slice [w KW/8, (w+1) KW/8) and keeps its image tiles in registers.  W is
 // loaded in coalesced 128-byte row pieces and moved into the MFMA A layout
 // (row lane % 16, k 8 (lane / 16) .. +8) with ds_bpermute: loading the A layout
@@ -53,10 +53,20 @@ __device__ __forceinline__ u32x4 bpermute4(int addr, const u32x4& v) {
 
 // rstd of sequence seq from `parts` partial sums of squares ([parts][8]) over
 // n elements; every lane of the calling wave gets the same value.
-__device__ __forceinline__ float seq_rstd(const float* ss, int parts, int seq, float n, float eps) {
-  float q = 0.f;
-  for (int p = lane_id(); p < parts; p += kWave) q += ss[(long)p * kB + seq];
-  return rsqrtf(wave_sum(q) / n + eps);
+// Partial sums of squares of sequence seq ([parts][8], parts <= 128): two per
+// lane, loaded ahead of their use; ss_rstd() finishes the reduction.
+struct SsPart {
+  float a = 0.f, b = 0.f;
+};
+__device__ __forceinline__ SsPart ss_load(const float* ss, int parts, int seq) {
+  SsPart r;
+  const int p = lane_id();
+  if (ss != nullptr && p < parts) r.a = ss[(long)p * kB + seq];
+  if (ss != nullptr && p + kWave < parts) r.b = ss[(long)(p + kWave) * kB + seq];
+  return r;
+}
+__device__ __forceinline__ float ss_rstd(SsPart q, float n, float eps) {
+  return rsqrtf(wave_sum(q.a + q.b) / n + eps);
 }
 
 template <int KW, int EPI>
@@ -86,18 +96,16 @@ __global__ __launch_bounds__(512) void gemv8_kernel(const Gemv8Args a) {
   // into the MFMA A layout with ds_bpermute (lane d = row r + 16 c of tile 2j+q
   // takes row r, k 32q + 8c: load r / 8, source lane 8 (r % 8) + 4q + c).
   static_assert(NT % 2 == 0, "tile pairs");
+  // (issued in the order the MFMA loop consumes them: gate pair, up pair, ...)
   auto load_w = [&](int rg, u32x4 (&wt)[NT], u32x4 (&wt2)[NW2]) {
     const uint16_t* p = a.W + ((long)rg * kRG + (lane >> 3)) * a.ldw + kb + (lane & 7) * 8;
+    const uint16_t* p2 = p + a.up_offset * a.ldw;
     const long h8row = 8 * a.ldw;
 #pragma unroll
     for (int i = 0; i < NT; i += 2) {
       wt[i] = ld_stream(p + i * kKT);
       wt[i + 1] = ld_stream(p + h8row + i * kKT);
-    }
-    if constexpr (DUAL) {
-      const uint16_t* p2 = p + a.up_offset * a.ldw;
-#pragma unroll
-      for (int i = 0; i < NT; i += 2) {
+      if constexpr (DUAL) {
         wt2[i] = ld_stream(p2 + i * kKT);
         wt2[i + 1] = ld_stream(p2 + h8row + i * kKT);
       }
@@ -114,30 +122,46 @@ __global__ __launch_bounds__(512) void gemv8_kernel(const Gemv8Args a) {
   };
 
   int rg = blockIdx.x;
-  u32x4 wt[NT], wt2[NW2];
-  load_w(rg, wt, wt2);
-  // the wave's image tiles: read once (L2-resident), used for every row group
+  const int rl = t & 15;    // epilogue thread: row rl of the group, sequence seq
+  const int seq = (t >> 4) & (kB - 1);
+  const bool live = seq < a.nseq;
+  // the epilogue's residual and norm weight, loaded before the weights so the
+  // epilogue does not wait for another round trip (one row group per
+  // workgroup outside EPI_ARGMAX)
+  float res = 0.f, gam = 1.f;
+  if constexpr (!ARGMAX) {
+    if (t < kOut) {
+      const long row = (long)rg * kRG + rl;
+      if (a.residual != nullptr && live) res = a.residual[(long)seq * a.ldr + row];
+      if (a.yb_gamma != nullptr) gam = h2f(a.yb_gamma[row]);
+    }
+  }
+  // Then the wave's image tiles (read once, used for every row group) and the
+  // norm partial sums, and only then the weights: loads complete in issue
+  // order, so the MFMAs and the norm factors wait only for what they use while
+  // the weight stream is still arriving.
   u32x4 bt[NT];
   {
     const u32x4* src = reinterpret_cast<const u32x4*>(a.xb) + (kb / kKT) * kWave + lane;
 #pragma unroll
     for (int i = 0; i < NT; ++i) bt[i] = src[i * kWave];
   }
+  const SsPart in_q = ss_load(a.in_ss, a.in_parts, w);
+  const SsPart pre_q = ss_load(a.pre_ss, a.pre_parts, w);
+  u32x4 wt[NT], wt2[NW2];
+  load_w(rg, wt, wt2);
   // wave w: factors of sequence w
   {
     float f = 1.f, o = 1.f;
-    if (a.in_ss != nullptr) f = seq_rstd(a.in_ss, a.in_parts, w, (float)a.K, a.eps);
+    if (a.in_ss != nullptr) f = ss_rstd(in_q, (float)a.K, a.eps);
     if (a.in_scale != nullptr) f /= a.in_scale[w];
     if (w >= a.nseq) f = 0.f;
-    if (a.pre_ss != nullptr) o = seq_rstd(a.pre_ss, a.pre_parts, w, (float)a.N, a.eps);
+    if (a.pre_ss != nullptr) o = ss_rstd(pre_q, (float)a.N, a.eps);
     if (lane == 0) {
       s_fac[w] = f;
       s_osc[w] = o;
     }
   }
-  const int rl = t & 15;    // epilogue thread: row rl of the group, sequence seq
-  const int seq = (t >> 4) & (kB - 1);
-  const bool live = seq < a.nseq;
   float best = -INFINITY;
   int best_i = 0x7fffffff;
 
@@ -239,12 +263,12 @@ __global__ __launch_bounds__(512) void gemv8_kernel(const Gemv8Args a) {
           v2 *= s_fac[seq];
           v = (v / (1.0f + __expf(-v))) * v2;
         } else {
-          if (a.residual != nullptr && live) v += a.residual[(long)seq * a.ldr + row];
+          v += res;
         }
         if (!live) v = 0.f;
         if (a.y != nullptr && live) a.y[(long)seq * a.ldy + row] = v;
         if (a.yb != nullptr)
-          bimg_store(a.yb, seq, row, v * (a.yb_gamma != nullptr ? h2f(a.yb_gamma[row]) : 1.f) * s_osc[seq]);
+          bimg_store(a.yb, seq, row, v * gam * s_osc[seq]);
         if (a.yss != nullptr) {
           const float q = row16_sum(v * v);
           if (rl == 0) a.yss[(long)rg * kB + seq] = q;
@@ -403,6 +427,9 @@ int launch8(const Gemv8Args& a, unsigned gx, hipStream_t s) {
 
 int gemv8_launch(const Gemv8Args& a, int epi, hipStream_t s) {
   if (a.nseq < 1 || a.nseq > kB || a.ksplit < 1 || a.K % a.ksplit != 0 || a.xb == nullptr) return QD_ERR_SHAPE;
+  if ((a.in_ss != nullptr && (a.in_parts < 1 || a.in_parts > 2 * kWave)) ||
+      (a.pre_ss != nullptr && (a.pre_parts < 1 || a.pre_parts > 2 * kWave)))
+    return QD_ERR_SHAPE;
   const long rows = (epi == EPI_SILU) ? a.up_offset : a.N;
   if (rows % kRG != 0 || rows <= 0) return QD_ERR_SHAPE;
   const long KW = a.K / a.ksplit;
@@ -418,6 +445,7 @@ int gemv8_launch(const Gemv8Args& a, int epi, hipStream_t s) {
     if (KW == 1024) return launch8<1024, EPI_SILU>(a, nrg, s);
     return QD_ERR_SHAPE;
   }
+  if (KW == 6144) return launch8<6144, EPI_STORE>(a, nrg, s);
   if (KW == 3072) return launch8<3072, EPI_STORE>(a, nrg, s);
   if (KW == 2048) return launch8<2048, EPI_STORE>(a, nrg, s);
   if (KW == 1024) return launch8<1024, EPI_STORE>(a, nrg, s);
