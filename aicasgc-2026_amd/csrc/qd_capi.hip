@@ -60,16 +60,13 @@ using u16 = uint16_t;
 inline hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
 inline bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Workspace layout of the lm_head argmax: [counter (256 B)] [vals] [idx].  The
-// counter (fused reduction by the last block) is used only where the
-// workspace is known to be zeroed: the decode step's.
+// Workspace layout of the lm_head argmax: [reserved (256 B)] [vals] [idx].
 constexpr size_t kArgmaxHeader = 256;
 size_t argmax_ws_bytes() {
   return kArgmaxHeader + (size_t)qd::kMaxArgmaxBlocks * (sizeof(float) + sizeof(long));
 }
-void argmax_ws(void* ws, GemvArgs& a, bool fused_reduce = false) {
+void argmax_ws(void* ws, GemvArgs& a) {
   char* b = reinterpret_cast<char*>(ws);
-  a.counter = fused_reduce ? reinterpret_cast<unsigned*>(b) : nullptr;
   a.part_idx = reinterpret_cast<long*>(b + kArgmaxHeader);
   a.part_val = reinterpret_cast<float*>(b + kArgmaxHeader + (size_t)qd::kMaxArgmaxBlocks * sizeof(long));
 }
@@ -821,7 +818,7 @@ static int step_phases(const qd_model_desc* d, int first_layer, int n_layers, un
   GemvArgs gl;
   gl.x = b.x; gl.gamma = (const u16*)d->final_norm; gl.eps = d->eps; gl.W = (const u16*)d->embed;
   gl.N = d->vocab; gl.K = H; gl.ldw = H; gl.y = d->logits_out; gl.token = d->token;
-  argmax_ws(b.argmax_ws, gl, true);
+  argmax_ws(b.argmax_ws, gl);
   if (advance && d->advance_counter != nullptr) {
     gl.adv_out = d->advance_out_tokens; gl.adv_counter = d->advance_counter;
     gl.adv_cache_position = const_cast<int64_t*>(d->cache_position);

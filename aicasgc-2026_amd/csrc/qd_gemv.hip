@@ -42,8 +42,7 @@ __device__ __forceinline__ void load_rows(const GemvArgs& a, long o0, long kofs,
   }
 }
 
-// First maximal index over n per-block partials (whole block, 256 threads),
-// read with agent-coherent loads: the last block of a fused lm_head + argmax.
+// First maximal index over n per-block partials (whole block, 256 threads).
 // Writes a.token[0] and, when a.adv_counter is set, advances the decode state
 // as decode_advance_kernel does.
 __device__ __forceinline__ void argmax_finish(const GemvArgs& a, int n) {
@@ -52,8 +51,8 @@ __device__ __forceinline__ void argmax_finish(const GemvArgs& a, int n) {
   float bv = -INFINITY;
   long bi = 0x7fffffffffffL;
   for (int b = threadIdx.x; b < n; b += blockDim.x) {
-    const float v = load_coherent(a.part_val + b);
-    const long i = load_coherent(a.part_idx + b);
+    const float v = a.part_val[b];
+    const long i = a.part_idx[b];
     if (v > bv || (v == bv && i < bi)) {
       bv = v;
       bi = i;
@@ -234,11 +233,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
   }
 
   if constexpr (EPI == EPI_ARGMAX) {
-    // per-block (max, first index); reduced by argmax_reduce_kernel in the next
-    // launch, or (a.counter set) by the last block to finish
+    // per-block (max, first index); reduced by argmax_reduce_kernel in the next launch
     __shared__ float s_v[16];
     __shared__ long s_i[16];
-    __shared__ int s_last;
     if (lane == 0) {
       s_v[wib] = best_v;
       s_i[wib] = best_i;
@@ -253,53 +250,17 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
           bi = s_i[w];
         }
       }
-      if (a.counter == nullptr) {
-        a.part_val[blockIdx.x] = bv;
-        a.part_idx[blockIdx.x] = bi;
-      } else {
-        store_coherent(a.part_val + blockIdx.x, bv);
-        store_coherent(a.part_idx + blockIdx.x, bi);
-        stores_done();
-        s_last = arrive_last(a.counter, gridDim.x);
-      }
-    }
-    if (a.counter != nullptr) {
-      __syncthreads();
-      if (s_last) argmax_finish(a, (int)gridDim.x);
+      a.part_val[blockIdx.x] = bv;
+      a.part_idx[blockIdx.x] = bi;
     }
   }
 }
 
-// One block: the first index of the maximum over n per-block partials.
-__global__ __launch_bounds__(256) void argmax_reduce_kernel(const float* part_val, const long* part_idx, int n,
-                                                            int64_t* token) {
-  __shared__ float r_v[256];
-  __shared__ long r_i[256];
-  float bv = -INFINITY;
-  long bi = 0x7fffffffffffL;
-  for (int b = threadIdx.x; b < n; b += blockDim.x) {
-    const float v = part_val[b];
-    const long i = part_idx[b];
-    if (v > bv || (v == bv && i < bi)) {
-      bv = v;
-      bi = i;
-    }
-  }
-  r_v[threadIdx.x] = bv;
-  r_i[threadIdx.x] = bi;
-  __syncthreads();
-  for (int s = blockDim.x / 2; s > 0; s >>= 1) {
-    if ((int)threadIdx.x < s) {
-      const float v = r_v[threadIdx.x + s];
-      const long i = r_i[threadIdx.x + s];
-      if (v > r_v[threadIdx.x] || (v == r_v[threadIdx.x] && i < r_i[threadIdx.x])) {
-        r_v[threadIdx.x] = v;
-        r_i[threadIdx.x] = i;
-      }
-    }
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) token[0] = (int64_t)r_i[0];
+// One block: the first index of the maximum over n per-block partials -> a.token[0];
+// when a.adv_counter is set it also advances the decode state as
+// decode_advance_kernel does (one launch less per decode step).
+__global__ __launch_bounds__(256) void argmax_reduce_kernel(const GemvArgs a, int n) {
+  argmax_finish(a, n);
 }
 
 // Generic fallback: any K % 8 == 0; one wave per output row, x streamed from
@@ -430,9 +391,8 @@ int gemv_argmax(const GemvArgs& a, hipStream_t s) {
   if (max_blocks > kMaxArgmaxBlocks) max_blocks = kMaxArgmaxBlocks;
   long blocks = 0;
   int st = launch_k<4, PRO, EPI_ARGMAX, TX, TY>(a, a.K, 1, max_blocks, s, &blocks);
-  if (st != QD_OK || a.counter != nullptr) return st;
-  hipLaunchKernelGGL(argmax_reduce_kernel, dim3(1), dim3(kThreads), 0, s, a.part_val, a.part_idx, (int)blocks,
-                     a.token);
+  if (st != QD_OK) return st;
+  hipLaunchKernelGGL(argmax_reduce_kernel, dim3(1), dim3(kThreads), 0, s, a, (int)blocks);
   return qd_host::launch_status("argmax_reduce_kernel");
 }
 

@@ -29,10 +29,8 @@ struct GemvArgs {
   float eps = 1e-6f;
   float* part_val = nullptr;       // EPI_ARGMAX per-block max / EPI_PARTIAL [splits, N]
   long* part_idx = nullptr;        // EPI_ARGMAX per-block argmax
-  unsigned* counter = nullptr;     // EPI_ARGMAX: arrival counter (zeroed, self-resetting); when set the
-                                   // last block reduces the partials (no reduce launch)
   int64_t* token = nullptr;        // EPI_ARGMAX result
-  // EPI_ARGMAX with counter: the last block also advances the decode state
+  // EPI_ARGMAX: the argmax reduction also advances the decode state
   // (qd_decode_advance semantics) when adv_counter is set
   int64_t* adv_out = nullptr;
   int64_t* adv_counter = nullptr;

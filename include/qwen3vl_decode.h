@@ -240,7 +240,7 @@ typedef struct qd_model_desc {
   /* Optional end-of-step advance (batch 1).  When advance_counter != NULL the
    * step finishes with qd_decode_advance(token, advance_out_tokens,
    * advance_counter, cache_position, rope_position, advance_max_tokens) done
-   * by the lm_head's last workgroup instead of a separate launch; the
+   * by the argmax reduction instead of a separate launch; the
    * cache_position / rope_position buffers are then written by the step. */
   int64_t* advance_out_tokens;
   int64_t* advance_counter;

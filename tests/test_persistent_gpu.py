@@ -6,7 +6,7 @@ Cases cover the attention split edge cases of the persistent kernel (32
 splits per kv head): a context of one row (cache_position 0), fewer rows than
 splits, a context that is not a multiple of the split size, a full 4096-row
 cache and an 8000-row context (several K/V batches per split).  The lm_head's
-fused argmax (last workgroup reduces the partials) is checked on ties.
+argmax reduction (with the fused position advance) is checked on ties.
 """
 
 from __future__ import annotations
@@ -129,8 +129,8 @@ def test_persistent_mode_rejected_for_other_shapes(cuda):
 
 def test_fused_argmax_ties_take_the_first_index(cuda):
     """Every embedding row identical: all logits tie, so each step's token is 0
-    (torch.argmax takes the first maximum) through the lm_head's last-workgroup
-    reduction over all its blocks, in both step modes; the fused advance moves
+    (torch.argmax takes the first maximum) through the lm_head's per-block
+    partials and their reduction, in both step modes; the fused advance moves
     the positions and the counter once per step."""
     from qwen3vl_hip import synthetic as syn
     from qwen3vl_hip.config import Qwen3VLTextShape
