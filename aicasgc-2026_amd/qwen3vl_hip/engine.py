@@ -265,6 +265,10 @@ class DecodeEngine(_CapturedSteps):
             for _ in range(n_steps):
                 self.step_eager()
         torch.cuda.synchronize(self.device)
+        if self.step_mode == "persistent" and self.status(reset=True) != 0:
+            # a hand-off wait ran out of its polling budget (e.g. the grid was not
+            # co-resident because another process held CUs): the tokens are invalid
+            raise RuntimeError("persistent decode step: a workgroup hand-off timed out; results are invalid")
         return self.out_tokens[:n_steps].tolist()
 
     # ------------------------------------------------------------ prefill
