@@ -252,24 +252,81 @@ class DecodeEngine(_CapturedSteps):
 
     # ------------------------------------------------------------ generation
     def decode(self, first_token: int, start_position: int, rope_delta: int, n_steps: int,
-               use_graph: bool = True) -> list:
-        """Greedy decode n_steps tokens after ``first_token`` at cache row start_position."""
+               use_graph: bool = True, eos_token_ids=None, eos_window: int = 2) -> list:
+        """Greedy decode n_steps tokens after ``first_token`` at cache row start_position.
+
+        With ``eos_token_ids`` generation stops at the first of them (included in
+        the result), detected without stalling the device: after every graph
+        replay the new tokens are copied to pinned host memory behind an event,
+        the host checks copies whose event has completed and blocks only when
+        ``eos_window`` copies are outstanding (the reference's async EOS poll,
+        evaluation_wrapper.py:317-463, :906-939).  Steps already enqueued when
+        the EOS is seen still run; their tokens are dropped.
+        """
         if start_position + n_steps > self.capacity:
             raise ValueError("static cache too small for the requested generation")
         self.reserve_tokens(n_steps)
         self.set_state(first_token, start_position, start_position + rope_delta)
         self.step_counter.zero_()
+        if eos_token_ids is not None and n_steps > 0:
+            n_out = self._decode_until_eos(n_steps, use_graph, set(int(t) for t in eos_token_ids),
+                                           max(1, int(eos_window)))
+            self._check_status()
+            return self._host_tokens[:n_out].tolist()
         if use_graph:
             self.replay_steps(n_steps)
         else:
             for _ in range(n_steps):
                 self.step_eager()
         torch.cuda.synchronize(self.device)
+        self._check_status()
+        return self.out_tokens[:n_steps].tolist()
+
+    def _decode_until_eos(self, n_steps: int, use_graph: bool, eos: set, window: int) -> int:
+        """Enqueue steps in chunks (one graph replay each), staging each chunk's
+        tokens to pinned host memory; returns how many tokens to keep."""
+        from collections import deque
+
+        if getattr(self, "_host_tokens", None) is None or self._host_tokens.numel() < n_steps:
+            self._host_tokens = torch.zeros(max(n_steps, 64), dtype=torch.int64, pin_memory=True)
+        host = self._host_tokens
+        if use_graph and self.graph is None:
+            self.capture()
+        k = self.steps_per_graph if (use_graph and self.graph_multi is not None) else 1
+        stream = torch.cuda.current_stream(self.device)
+        pending, done, found = deque(), 0, None
+        while done < n_steps and found is None:
+            chunk = min(k, n_steps - done)
+            if use_graph:
+                self.replay_steps(chunk)
+            else:
+                for _ in range(chunk):
+                    self.step_eager()
+            host[done:done + chunk].copy_(self.out_tokens[done:done + chunk], non_blocking=True)
+            ev = torch.cuda.Event()
+            ev.record(stream)
+            pending.append((ev, done, chunk))
+            done += chunk
+            while pending and found is None and (len(pending) >= window or pending[0][0].query()):
+                ev0, s0, c0 = pending.popleft()
+                ev0.synchronize()
+                for i in range(s0, s0 + c0):
+                    if int(host[i]) in eos:
+                        found = i
+                        break
+        torch.cuda.synchronize(self.device)
+        if found is None:
+            for i in range(done):
+                if int(host[i]) in eos:
+                    found = i
+                    break
+        return found + 1 if found is not None else done
+
+    def _check_status(self) -> None:
         if self.step_mode == "persistent" and self.status(reset=True) != 0:
             # a hand-off wait ran out of its polling budget (e.g. the grid was not
             # co-resident because another process held CUs): the tokens are invalid
             raise RuntimeError("persistent decode step: a workgroup hand-off timed out; results are invalid")
-        return self.out_tokens[:n_steps].tolist()
 
     # ------------------------------------------------------------ prefill
     @torch.no_grad()
@@ -327,10 +384,16 @@ class DecodeEngine(_CapturedSteps):
         logits = hn @ self.w.embed_tokens.float().T
         return int(torch.argmax(logits))
 
-    def generate(self, prompt: MultimodalPrompt, n_tokens: int, use_graph: bool = True) -> list:
-        """Prefill + greedy decode; returns n_tokens ids (the first from the prefill)."""
+    def generate(self, prompt: MultimodalPrompt, n_tokens: int, use_graph: bool = True, eos_token_ids=None,
+                 eos_window: int = 2) -> list:
+        """Prefill + greedy decode; returns n_tokens ids (the first from the
+        prefill), or fewer when ``eos_token_ids`` is given and one of them is
+        generated (the EOS token is the last one returned)."""
         first = self.prefill(prompt)
-        rest = self.decode(first, prompt.length, prompt.rope_delta, n_tokens - 1, use_graph) if n_tokens > 1 else []
+        if eos_token_ids is not None and first in set(int(t) for t in eos_token_ids):
+            return [first]
+        rest = self.decode(first, prompt.length, prompt.rope_delta, n_tokens - 1, use_graph, eos_token_ids,
+                           eos_window) if n_tokens > 1 else []
         return [first] + rest
 
 

@@ -143,3 +143,26 @@ def test_fused_argmax_ties_take_the_first_index(cuda):
         assert eng.decode(5, 10, 0, 6, use_graph=True) == [0] * 6
         assert int(eng.cache_position.item()) == 16 and int(eng.step_counter.item()) == 6
         assert eng.rope_position.tolist() == [16, 16, 16]
+
+
+def test_generate_stops_at_eos(cuda, two_layer_weights):
+    """Async EOS polling: generation stops at the first EOS token (returned last)
+    with the tokens before it identical to a fixed-length run, for several poll
+    windows and step modes; the prefill's token being EOS returns it alone."""
+    from qwen3vl_hip import synthetic as syn
+    from qwen3vl_hip.engine import DecodeEngine
+
+    w = two_layer_weights
+    prompt = syn.multimodal_prompt(23, grid_h=4, grid_w=8, n_text=16, shape=w.shape)
+    n = 40
+    cap = prompt.length + n + 8
+    for mode in ("persistent", "chain"):
+        eng = DecodeEngine(w, capacity=cap, step_mode=mode)
+        full = eng.generate(prompt, n, use_graph=True)
+        j = next(i for i in range(13, n) if full[i] not in full[:i])
+        for window in (1, 2, 3):
+            got = eng.generate(prompt, n, use_graph=True, eos_token_ids=[full[j], -5], eos_window=window)
+            assert got == full[:j + 1], (mode, window)
+        assert eng.generate(prompt, n, use_graph=False, eos_token_ids=[full[j]]) == full[:j + 1]
+        assert eng.generate(prompt, n, eos_token_ids=[full[0]]) == full[:1]
+        assert eng.generate(prompt, n, eos_token_ids=[-1]) == full
