@@ -63,39 +63,63 @@ __device__ __forceinline__ void mrope_cs(long pt, long ph, long pw, float inv_fr
   sincosf(f, &s, &c);
 }
 
-// Online-softmax update of one slot with kUnroll positions t, t+16, ...; a
-// position >= t1 contributes nothing.  Control flow is uniform across the wave
-// (invalid positions are masked with selects, their K/V registers are zero),
-// so the DPP row sums never run under divergent execution masks.
+// Online-softmax update of one slot with the kUnroll positions t, t+16, ...
+// as one block: the block's scores, one running-max update and one rescale of
+// the accumulators per block, then one FMA per dimension and position.  A
+// position >= t1 gets weight 0 (its K/V registers hold the finite row t1 - 1,
+// see load_kv_batch).  Control flow is uniform across the wave, so the DPP row
+// sums never run under divergent execution masks.
 template <int G>
 __device__ __forceinline__ void online_softmax_batch(const u32x4 (&kk)[kUnroll], const u32x4 (&vv)[kUnroll], int t,
                                                      int t1, const float (&q)[G][8], float scale, float (&m)[G],
                                                      float (&l)[G], float (&acc)[G][8]) {
+  float sc[kUnroll][G];
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
     const bool valid = t + u * kSlots < t1;
-    float vf[8];
-    unpack8(vv[u], vf);
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       const float s = row16_sum(dot8(kk[u], q[g], 0.f)) * scale;
-      const float dlt = s - m[g];
-      const float e = __expf(-fabsf(dlt));
-      const bool up = valid && dlt > 0.f;
-      const float c = up ? e : 1.f;                      // rescale of the running sums
-      const float p = valid ? (up ? 1.f : e) : 0.f;      // weight of this position
-      m[g] = up ? s : m[g];
-      l[g] = __builtin_fmaf(l[g], c, p);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) acc[g][i] = __builtin_fmaf(acc[g][i], c, p * vf[i]);
+      sc[u][g] = valid ? s : -INFINITY;
     }
+  }
+  float p[kUnroll][G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float mb = sc[0][g];
+#pragma unroll
+    for (int u = 1; u < kUnroll; ++u) mb = fmaxf(mb, sc[u][g]);
+    const float mn = fmaxf(m[g], mb);
+    // mn == -inf: nothing valid yet; keep the (zero) sums as they are
+    const float c = mn == -INFINITY ? 1.f : __expf(m[g] - mn);
+    float ps = 0.f;
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      p[u][g] = sc[u][g] == -INFINITY ? 0.f : __expf(sc[u][g] - mn);
+      ps += p[u][g];
+    }
+    l[g] = __builtin_fmaf(l[g], c, ps);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[g][i] *= c;
+    m[g] = mn;
+  }
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    float vf[8];
+    unpack8(vv[u], vf);
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[g][i] = __builtin_fmaf(p[u][g], vf[i], acc[g][i]);
   }
 }
 
 // K/V rows of positions t, t+16, ... into registers.  The loads are
-// unconditional (rows past t1 re-read row t1 - 1, an L1/L2 hit) so the number
-// of loads in flight is the same on every path and a wave waits only for the
-// batch it consumes; kv_select() zeroes the rows >= t1 and the skipped row.
+// unconditional (rows past t1 re-read row t1 - 1, an L1/L2 hit, so every
+// register holds finite cache data) and the number of loads in flight is the
+// same on every path, so a wave waits only for the batch it consumes.  The
+// softmax gives positions >= t1 weight 0; the fused variant replaces the new
+// position's row (not yet in the cache) from LDS.
 __device__ __forceinline__ void load_kv_batch(const uint16_t* kb, const uint16_t* vb, long stride_s, int t, int t1,
                                               u32x4 (&kk)[kUnroll], u32x4 (&vv)[kUnroll]) {
   const int last = t1 > 0 ? t1 - 1 : 0;
@@ -104,19 +128,6 @@ __device__ __forceinline__ void load_kv_batch(const uint16_t* kb, const uint16_t
     const int tt = min(t + u * kSlots, last);
     kk[u] = ld_stream(kb + (long)tt * stride_s);
     vv[u] = ld_stream(vb + (long)tt * stride_s);
-  }
-}
-
-// Rows >= t1 and row `skip` of a loaded batch read as zero (stale cache rows may
-// hold any bit pattern; a zero V keeps them out of the accumulators).
-__device__ __forceinline__ void kv_select(int t, int t1, long skip, u32x4 (&kk)[kUnroll], u32x4 (&vv)[kUnroll]) {
-#pragma unroll
-  for (int u = 0; u < kUnroll; ++u) {
-    const int tt = t + u * kSlots;
-    const bool keep = tt < t1 && tt != skip;
-    const u32x4 z = {0u, 0u, 0u, 0u};
-    kk[u] = keep ? kk[u] : z;
-    vv[u] = keep ? vv[u] : z;
   }
 }
 
@@ -156,7 +167,6 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
   // The wave's four slots advance together (trip count uniform per wave).
   const int wave_t0 = t0 + (threadIdx.x / kWave) * 4;
   const int row_off = slot - (threadIdx.x / kWave) * 4;
-  const long skip = FUSED_ROPE ? pos : -1;
 
   // The prologue's own inputs are loaded first, then two batches of K/V rows
   // (A: kk/vv, B: kn/vn), which do not depend on the prologue.  Loads complete
@@ -252,7 +262,6 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
 
   // the new position comes from LDS (fp16, as written to the cache)
   auto consume = [&](u32x4 (&bk)[kUnroll], u32x4 (&bv)[kUnroll], int t) {
-    kv_select(t, t1, skip, bk, bv);
     if constexpr (FUSED_ROPE) {
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
