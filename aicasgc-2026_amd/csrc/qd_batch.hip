@@ -40,10 +40,9 @@ namespace {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 
 constexpr int kB = kBatchMax;     // sequences per batch step (8)
-constexpr int kRG = 16;           // rows per row group (MFMA M)
+constexpr int kRG = 16;           // rows per row group (MFMA M; 8 with zero rows)
 constexpr int kWaves = 8;         // K slices per workgroup
 constexpr int kKT = 32;           // K per MFMA
-constexpr int kOut = kRG * kB;    // outputs of one row group
 
 // Lane permutation of a 16-byte register quad: lane d receives lane addr/4's.
 __device__ __forceinline__ u32x4 bpermute4(int addr, const u32x4& v) {
@@ -53,32 +52,56 @@ __device__ __forceinline__ u32x4 bpermute4(int addr, const u32x4& v) {
 
 // rstd of sequence seq from `parts` partial sums of squares ([parts][8]) over
 // n elements; every lane of the calling wave gets the same value.
-// Partial sums of squares of sequence seq ([parts][8], parts <= 128): two per
+// Partial sums of squares of sequence seq ([parts][8], parts <= 256): four per
 // lane, loaded ahead of their use; ss_rstd() finishes the reduction.
+constexpr int kMaxSsParts = 4 * kWave;
 struct SsPart {
-  float a = 0.f, b = 0.f;
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
 };
 __device__ __forceinline__ SsPart ss_load(const float* ss, int parts, int seq) {
   SsPart r;
   const int p = lane_id();
-  if (ss != nullptr && p < parts) r.a = ss[(long)p * kB + seq];
-  if (ss != nullptr && p + kWave < parts) r.b = ss[(long)(p + kWave) * kB + seq];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (ss != nullptr && p + i * kWave < parts) r.v[i] = ss[(long)(p + i * kWave) * kB + seq];
   return r;
 }
 __device__ __forceinline__ float ss_rstd(SsPart q, float n, float eps) {
-  return rsqrtf(wave_sum(q.a + q.b) / n + eps);
+  return rsqrtf(wave_sum((q.v[0] + q.v[1]) + (q.v[2] + q.v[3])) / n + eps);
 }
 
-template <int KW, int EPI>
+// Sum over groups of R consecutive lanes (R = 8 or 16); every lane of a group
+// receives its group's sum.
+template <int R>
+__device__ __forceinline__ float group_sum(float v) {
+  if constexpr (R == 16) {
+    return row16_sum(v);
+  } else {
+    v += __shfl_xor(v, 1);
+    v += __shfl_xor(v, 2);
+    v += __shfl_xor(v, 4);
+    return v;
+  }
+}
+
+// RG: rows per workgroup, 16 (the MFMA M dimension) or 8 (rows 8..15 of the
+// A operand are zero: twice the workgroups for the same rows, so a shape with
+// few row groups fills the CUs without splitting K).
+template <int KW, int EPI, int RG>
 __global__ __launch_bounds__(512) void gemv8_kernel(const Gemv8Args a) {
   constexpr int KS = KW / kWaves;
   constexpr int NT = KS / kKT;
   constexpr bool DUAL = EPI == EPI_SILU;
   constexpr bool ARGMAX = EPI == EPI_ARGMAX;
   constexpr int NA = DUAL ? 2 : 1;
-  constexpr int NW2 = DUAL ? NT : 1;
+  constexpr int NL = RG / 8;                 // weight loads per tile pair (8 rows each)
+  constexpr int NWT = NT / 2 * NL;
+  constexpr int NW2 = DUAL ? NWT : 1;
+  constexpr int OUT = RG * kB;               // outputs of one row group
+  static_assert(RG == 8 || RG == 16, "8 or 16 rows per workgroup");
+  static_assert(!ARGMAX || RG == 16, "argmax epilogue: 16 rows per group");
   __shared__ float s_fac[kB], s_osc[kB];
-  __shared__ float s_part[NA][kWaves][kB][kRG];
+  __shared__ float s_part[NA][kWaves][kB][RG];
   __shared__ int s_last;
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -88,50 +111,58 @@ __global__ __launch_bounds__(512) void gemv8_kernel(const Gemv8Args a) {
   const int t = threadIdx.x;
   const long kb = (long)blockIdx.y * KW + (long)w * KS;
   const long rows = DUAL ? a.up_offset : a.N;
-  const int nrg = (int)(rows / kRG);
+  const int nrg = (int)(rows / RG);
 
   // Weight loads are coalesced 128-byte row pieces: for the tile pair (2j, 2j+1)
   // (64 K values) load h covers rows 8h..8h+7 with 8 lanes x 16 bytes per row
   // (lane: row 8h + lane / 8, k 8 (lane % 8)).  pair_to_mfma() moves the pair
   // into the MFMA A layout with ds_bpermute (lane d = row r + 16 c of tile 2j+q
-  // takes row r, k 32q + 8c: load r / 8, source lane 8 (r % 8) + 4q + c).
+  // takes row r, k 32q + 8c: load r / 8, source lane 8 (r % 8) + 4q + c); with
+  // RG = 8 the rows 8..15 are zero.
   static_assert(NT % 2 == 0, "tile pairs");
   // (issued in the order the MFMA loop consumes them: gate pair, up pair, ...)
-  auto load_w = [&](int rg, u32x4 (&wt)[NT], u32x4 (&wt2)[NW2]) {
-    const uint16_t* p = a.W + ((long)rg * kRG + (lane >> 3)) * a.ldw + kb + (lane & 7) * 8;
+  auto load_w = [&](int rg, u32x4 (&wt)[NWT], u32x4 (&wt2)[NW2]) {
+    const uint16_t* p = a.W + ((long)rg * RG + (lane >> 3)) * a.ldw + kb + (lane & 7) * 8;
     const uint16_t* p2 = p + a.up_offset * a.ldw;
     const long h8row = 8 * a.ldw;
 #pragma unroll
-    for (int i = 0; i < NT; i += 2) {
-      wt[i] = ld_stream(p + i * kKT);
-      wt[i + 1] = ld_stream(p + h8row + i * kKT);
+    for (int j = 0; j < NT / 2; ++j) {
+#pragma unroll
+      for (int h = 0; h < NL; ++h) wt[j * NL + h] = ld_stream(p + h * h8row + 2 * j * kKT);
       if constexpr (DUAL) {
-        wt2[i] = ld_stream(p2 + i * kKT);
-        wt2[i + 1] = ld_stream(p2 + h8row + i * kKT);
+#pragma unroll
+        for (int h = 0; h < NL; ++h) wt2[j * NL + h] = ld_stream(p2 + h * h8row + 2 * j * kKT);
       }
     }
   };
   const int src0 = (8 * (m & 7) + (lane >> 4)) * 4;   // byte lane addresses for ds_bpermute
   const int src1 = src0 + 16;
   const bool upper = m >= 8;
-  auto pair_to_mfma = [&](const u32x4& l0, const u32x4& l1, u32x4& t0, u32x4& t1) {
-    const u32x4 a0 = bpermute4(src0, l0), b0 = bpermute4(src0, l1);
-    const u32x4 a1 = bpermute4(src1, l0), b1 = bpermute4(src1, l1);
-    t0 = upper ? b0 : a0;
-    t1 = upper ? b1 : a1;
+  auto pair_to_mfma = [&](const auto& w, int j, u32x4& t0, u32x4& t1) {
+    const u32x4 a0 = bpermute4(src0, w[j * NL]);
+    const u32x4 a1 = bpermute4(src1, w[j * NL]);
+    if constexpr (NL == 2) {
+      const u32x4 b0 = bpermute4(src0, w[j * NL + 1]), b1 = bpermute4(src1, w[j * NL + 1]);
+      t0 = upper ? b0 : a0;
+      t1 = upper ? b1 : a1;
+    } else {
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      t0 = upper ? z : a0;
+      t1 = upper ? z : a1;
+    }
   };
 
   int rg = blockIdx.x;
-  const int rl = t & 15;    // epilogue thread: row rl of the group, sequence seq
-  const int seq = (t >> 4) & (kB - 1);
+  const int rl = t % RG;    // epilogue thread: row rl of the group, sequence seq
+  const int seq = (t / RG) & (kB - 1);
   const bool live = seq < a.nseq;
   // the epilogue's residual and norm weight, loaded before the weights so the
   // epilogue does not wait for another round trip (one row group per
   // workgroup outside EPI_ARGMAX)
   float res = 0.f, gam = 1.f;
   if constexpr (!ARGMAX) {
-    if (t < kOut) {
-      const long row = (long)rg * kRG + rl;
+    if (t < OUT) {
+      const long row = (long)rg * RG + rl;
       if (a.residual != nullptr && live) res = a.residual[(long)seq * a.ldr + row];
       if (a.yb_gamma != nullptr) gam = h2f(a.yb_gamma[row]);
     }
@@ -148,7 +179,7 @@ __global__ __launch_bounds__(512) void gemv8_kernel(const Gemv8Args a) {
   }
   const SsPart in_q = ss_load(a.in_ss, a.in_parts, w);
   const SsPart pre_q = ss_load(a.pre_ss, a.pre_parts, w);
-  u32x4 wt[NT], wt2[NW2];
+  u32x4 wt[NWT], wt2[NW2];
   load_w(rg, wt, wt2);
   // wave w: factors of sequence w
   {
@@ -167,7 +198,7 @@ __global__ __launch_bounds__(512) void gemv8_kernel(const Gemv8Args a) {
 
   for (;;) {
     const int nxt = rg + (int)gridDim.x;
-    u32x4 wn[ARGMAX ? NT : 1], wn2[1];
+    u32x4 wn[ARGMAX ? NWT : 1], wn2[1];
     if constexpr (ARGMAX) {
       if (nxt < nrg) load_w(nxt, wn, wn2);
     }
@@ -175,13 +206,13 @@ __global__ __launch_bounds__(512) void gemv8_kernel(const Gemv8Args a) {
 #pragma unroll
     for (int i = 0; i < NT; i += 2) {
       u32x4 t0, t1;
-      pair_to_mfma(wt[i], wt[i + 1], t0, t1);
+      pair_to_mfma(wt, i / 2, t0, t1);
       acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, t0), __builtin_bit_cast(h8, bt[i]), acc, 0, 0,
                                                    0);
       acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, t1), __builtin_bit_cast(h8, bt[i + 1]), acc,
                                                    0, 0, 0);
       if constexpr (DUAL) {
-        pair_to_mfma(wt2[i], wt2[i + 1], t0, t1);
+        pair_to_mfma(wt2, i / 2, t0, t1);
         acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, t0), __builtin_bit_cast(h8, bt[i]), acc2,
                                                       0, 0, 0);
         acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, t1), __builtin_bit_cast(h8, bt[i + 1]),
@@ -196,16 +227,16 @@ __global__ __launch_bounds__(512) void gemv8_kernel(const Gemv8Args a) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const float v = c[j] + dpp<kDppRowRor8>(c[j]);
-        if (m < kB) s_part[0][w][m][4 * g + j] = v;
+        if (m < kB && 4 * g + j < RG) s_part[0][w][m][4 * g + j] = v;
         if constexpr (DUAL) {
           const float v2 = c2[j] + dpp<kDppRowRor8>(c2[j]);
-          if (m < kB) s_part[NA - 1][w][m][4 * g + j] = v2;
+          if (m < kB && 4 * g + j < RG) s_part[NA - 1][w][m][4 * g + j] = v2;
         }
       }
     }
     __syncthreads();
     float v = 0.f, v2 = 0.f;
-    if (t < kOut) {
+    if (t < OUT) {
 #pragma unroll
       for (int q = 0; q < kWaves; ++q) v += s_part[0][q][seq][rl];
       if constexpr (DUAL) {
@@ -217,28 +248,28 @@ __global__ __launch_bounds__(512) void gemv8_kernel(const Gemv8Args a) {
       if (a.ksplit > 1) {
         // publish this K range's partials (coherent stores, completed before the
         // arrival count); the last workgroup of the row group sums them in K order
-        float* kp = a.kpart + (long)rg * a.ksplit * (NA * kOut);
-        if (t < kOut) {
-          store_coherent(kp + (long)blockIdx.y * (NA * kOut) + t, v);
-          if constexpr (DUAL) store_coherent(kp + (long)blockIdx.y * (NA * kOut) + kOut + t, v2);
+        float* kp = a.kpart + (long)rg * a.ksplit * (NA * OUT);
+        if (t < OUT) {
+          store_coherent(kp + (long)blockIdx.y * (NA * OUT) + t, v);
+          if constexpr (DUAL) store_coherent(kp + (long)blockIdx.y * (NA * OUT) + OUT + t, v2);
         }
         stores_done();
         __syncthreads();
         if (t == 0) s_last = arrive_last(a.kcount + rg, (unsigned)a.ksplit);
         __syncthreads();
         if (!s_last) return;
-        if (t < kOut) {
+        if (t < OUT) {
           v = 0.f;
           v2 = 0.f;
           for (int q = 0; q < a.ksplit; ++q) {
-            v += load_coherent(kp + (long)q * (NA * kOut) + t);
-            if constexpr (DUAL) v2 += load_coherent(kp + (long)q * (NA * kOut) + kOut + t);
+            v += load_coherent(kp + (long)q * (NA * OUT) + t);
+            if constexpr (DUAL) v2 += load_coherent(kp + (long)q * (NA * OUT) + OUT + t);
           }
         }
       }
     }
-    if (t < kOut) {
-      const long row = (long)rg * kRG + rl;
+    if (t < OUT) {
+      const long row = (long)rg * RG + rl;
       v *= s_fac[seq];
       if constexpr (ARGMAX) {
         if (a.y != nullptr && live) a.y[(long)seq * a.ldy + row] = v;
@@ -270,7 +301,7 @@ __global__ __launch_bounds__(512) void gemv8_kernel(const Gemv8Args a) {
         if (a.yb != nullptr)
           bimg_store(a.yb, seq, row, v * gam * s_osc[seq]);
         if (a.yss != nullptr) {
-          const float q = row16_sum(v * v);
+          const float q = group_sum<RG>(v * v);
           if (rl == 0) a.yss[(long)rg * kB + seq] = q;
         }
         if (a.out_scale != nullptr && rg == 0 && rl == 0) a.out_scale[seq] = s_osc[seq];
@@ -282,12 +313,12 @@ __global__ __launch_bounds__(512) void gemv8_kernel(const Gemv8Args a) {
       if (nxt >= nrg) break;
       __syncthreads();   // s_part is rewritten by the next group
 #pragma unroll
-      for (int i = 0; i < NT; ++i) wt[i] = wn[i];
+      for (int i = 0; i < NWT; ++i) wt[i] = wn[i];
       rg = nxt;
     }
   }
   if constexpr (ARGMAX) {
-    if (t < kOut && rl == 0) {
+    if (t < OUT && rl == 0) {
       a.part_val[(long)blockIdx.x * kB + seq] = best;
       a.part_idx[(long)blockIdx.x * kB + seq] = best_i;
     }
@@ -417,9 +448,9 @@ __global__ void advance8_kernel(const int64_t* token, int64_t* out_tokens, int64
   if (b == 0) counter[0] = c + 1;
 }
 
-template <int KW, int EPI>
+template <int KW, int EPI, int RG>
 int launch8(const Gemv8Args& a, unsigned gx, hipStream_t s) {
-  hipLaunchKernelGGL((gemv8_kernel<KW, EPI>), dim3(gx, (unsigned)a.ksplit), dim3(kWaves * kWave), 0, s, a);
+  hipLaunchKernelGGL((gemv8_kernel<KW, EPI, RG>), dim3(gx, (unsigned)a.ksplit), dim3(kWaves * kWave), 0, s, a);
   return qd_host::launch_status("gemv8_kernel");
 }
 
@@ -427,32 +458,42 @@ int launch8(const Gemv8Args& a, unsigned gx, hipStream_t s) {
 
 int gemv8_launch(const Gemv8Args& a, int epi, hipStream_t s) {
   if (a.nseq < 1 || a.nseq > kB || a.ksplit < 1 || a.K % a.ksplit != 0 || a.xb == nullptr) return QD_ERR_SHAPE;
-  if ((a.in_ss != nullptr && (a.in_parts < 1 || a.in_parts > 2 * kWave)) ||
-      (a.pre_ss != nullptr && (a.pre_parts < 1 || a.pre_parts > 2 * kWave)))
+  if ((a.in_ss != nullptr && (a.in_parts < 1 || a.in_parts > kMaxSsParts)) ||
+      (a.pre_ss != nullptr && (a.pre_parts < 1 || a.pre_parts > kMaxSsParts)))
     return QD_ERR_SHAPE;
+  const int rg = a.rows_per_group;
+  if (rg != 8 && rg != 16) return QD_ERR_SHAPE;
   const long rows = (epi == EPI_SILU) ? a.up_offset : a.N;
-  if (rows % kRG != 0 || rows <= 0) return QD_ERR_SHAPE;
+  if (rows % rg != 0 || rows <= 0) return QD_ERR_SHAPE;
   const long KW = a.K / a.ksplit;
-  const unsigned nrg = (unsigned)(rows / kRG);
+  const unsigned nrg = (unsigned)(rows / rg);
   if (a.ksplit > 1 && (epi == EPI_ARGMAX || a.kpart == nullptr || a.kcount == nullptr)) return QD_ERR_SHAPE;
   if (epi == EPI_ARGMAX) {
-    if (KW != 2048 || a.part_val == nullptr || a.part_idx == nullptr) return QD_ERR_SHAPE;
+    if (KW != 2048 || rg != 16 || a.part_val == nullptr || a.part_idx == nullptr) return QD_ERR_SHAPE;
     const unsigned gx = (a.grid > 0 && (unsigned)a.grid < nrg) ? (unsigned)a.grid : nrg;
-    return launch8<2048, EPI_ARGMAX>(a, gx, s);
+    return launch8<2048, EPI_ARGMAX, 16>(a, gx, s);
   }
-  if (epi == EPI_SILU) {
-    if (KW == 2048) return launch8<2048, EPI_SILU>(a, nrg, s);
-    if (KW == 1024) return launch8<1024, EPI_SILU>(a, nrg, s);
+  if (rg == 8) {
+    if (epi == EPI_SILU) return KW == 2048 ? launch8<2048, EPI_SILU, 8>(a, nrg, s) : QD_ERR_SHAPE;
+    if (KW == 6144) return launch8<6144, EPI_STORE, 8>(a, nrg, s);
+    if (KW == 2048) return launch8<2048, EPI_STORE, 8>(a, nrg, s);
     return QD_ERR_SHAPE;
   }
-  if (KW == 6144) return launch8<6144, EPI_STORE>(a, nrg, s);
-  if (KW == 3072) return launch8<3072, EPI_STORE>(a, nrg, s);
-  if (KW == 2048) return launch8<2048, EPI_STORE>(a, nrg, s);
-  if (KW == 1024) return launch8<1024, EPI_STORE>(a, nrg, s);
+  if (epi == EPI_SILU) {
+    if (KW == 2048) return launch8<2048, EPI_SILU, 16>(a, nrg, s);
+    if (KW == 1024) return launch8<1024, EPI_SILU, 16>(a, nrg, s);
+    return QD_ERR_SHAPE;
+  }
+  if (KW == 6144) return launch8<6144, EPI_STORE, 16>(a, nrg, s);
+  if (KW == 3072) return launch8<3072, EPI_STORE, 16>(a, nrg, s);
+  if (KW == 2048) return launch8<2048, EPI_STORE, 16>(a, nrg, s);
+  if (KW == 1024) return launch8<1024, EPI_STORE, 16>(a, nrg, s);
   return QD_ERR_SHAPE;
 }
 
-int gemv8_row_groups(long N) { return (int)((N + kRG - 1) / kRG); }
+int gemv8_row_groups(long N, int rows_per_group) {
+  return (int)((N + rows_per_group - 1) / rows_per_group);
+}
 
 int bimage8_launch(const float* x, long ldx, const uint16_t* gamma, bool norm, float eps, int K, int nseq,
                    uint16_t* img, float* ss, float* scale, hipStream_t s) {

@@ -416,7 +416,7 @@ bool step_layout(const qd_model_desc* d, int splits, StepBuffers* b, size_t* tot
   if (B > 1) {
     // an operand image holds 16 fp16 columns per K index
     const size_t groups = (size_t)qd::gemv8_row_groups(d->vocab);
-    const size_t hgroups = (size_t)qd::gemv8_row_groups(d->hidden);
+    const size_t hgroups = (size_t)qd::gemv8_row_groups(d->hidden, 8);   // row groups of o_proj / down
     const size_t max_rows = qkv_rows > (size_t)d->intermediate ? qkv_rows : (size_t)d->intermediate;
     o_xb = off; off += align256(32 * (size_t)d->hidden);
     o_ab = off; off += align256(32 * (size_t)d->num_heads * d->head_dim);
@@ -596,23 +596,32 @@ int qd_decode_step_mode(const qd_model_desc* d) {
 
 namespace {
 
-// Workgroups per row group along K for a batch GEMV (K ranges of 1024, 2048
-// or 3072): the smallest split whose workgroup count is a multiple of the 256
+// Work split of a batch GEMV with `rows` output rows (gate rows for SiLU):
+// rows per workgroup (8 for K = 2048 when 16 would leave fewer row groups than
+// CUs (o_proj) and for gate_up: more workgroups and no K split; else 16) and
+// workgroups per row group along K (K ranges of 1024, 2048, 3072 or
+// 6144): the smallest split whose workgroup count is a multiple of the 256
 // CUs, else the smallest that gives at least 256 workgroups.
-int batch_ksplit(long rows, long K) {
-  const long groups = rows / 16;
+struct BatchSplit {
+  int rows_per_group, ksplit;
+};
+BatchSplit batch_split(long rows, long K, bool silu) {
+  const int rg = ((silu && K == 2048) || (!silu && rows / 16 < 256 && rows % 8 == 0 && K <= 2048)) ? 8 : 16;
+  const long groups = rows / rg;
   const int cand[] = {1, 2, 3, 6};
   auto ok = [&](int ks) {
     const long kw = K / ks;
-    return K % ks == 0 && (kw == 1024 || kw == 2048 || kw == 3072);
+    if (K % ks != 0) return false;
+    if (rg == 8) return ks == 1 && (kw == 2048 || kw == 6144);
+    return silu ? (kw == 1024 || kw == 2048) : (kw == 1024 || kw == 2048 || kw == 3072 || kw == 6144);
   };
   for (int ks : cand)
-    if (ok(ks) && (groups * ks) % 256 == 0) return ks;
+    if (ok(ks) && (groups * ks) % 256 == 0) return {rg, ks};
   for (int ks : cand)
-    if (ok(ks) && groups * ks >= 256) return ks;
+    if (ok(ks) && groups * ks >= 256) return {rg, ks};
   for (int ks : cand)
-    if (ok(ks)) return ks;
-  return 1;
+    if (ok(ks)) return {rg, ks};
+  return {16, 1};
 }
 
 // Batch step (batch 2..8): the kernel chain with MFMA batch GEMVs and the
@@ -635,18 +644,22 @@ int batch_step(const qd_model_desc* d, hipStream_t s) {
   step_layout(d, splits, &b, &total);
   const int H = d->hidden, D = d->head_dim, Hq = d->num_heads, Hkv = d->num_kv_heads, I = d->intermediate;
   const long qkv_rows = (long)Hq * D + 2L * Hkv * D;
-  const int hparts = qd::gemv8_row_groups(H);
+  // partial sums of squares of x and r: one per row group of their producers
+  // (down and o_proj)
+  const int x_parts = qd::gemv8_row_groups(H, batch_split(H, I, false).rows_per_group);
+  const int r_parts = qd::gemv8_row_groups(H, batch_split(H, (long)Hq * D, false).rows_per_group);
   int st = QD_OK;
   if ((st = qd::embed8_launch((const u16*)d->embed, d->token, b.x, H, d->vocab, B,
                               (const u16*)d->layers[0].input_norm, d->eps, b.xb, b.ss_x, b.sc_x, s)))
     return st;
-  auto base = [&](qd::Gemv8Args& g, long N, long K) {
-    g.nseq = B; g.eps = d->eps; g.N = N; g.K = K; g.ldw = K; g.ksplit = batch_ksplit(N, K);
+  auto base = [&](qd::Gemv8Args& g, long N, long K, bool silu = false) {
+    const BatchSplit sp = batch_split(N, K, silu);
+    g.nseq = B; g.eps = d->eps; g.N = N; g.K = K; g.ldw = K; g.ksplit = sp.ksplit; g.rows_per_group = sp.rows_per_group;
     g.kpart = b.kpart; g.kcount = b.kcount;
   };
   for (int li = 0; li < d->num_layers; ++li) {
     const qd_layer_weights& w = d->layers[li];
-    const int xparts = li == 0 ? 1 : hparts;   // the embedding kernel writes one partial
+    const int xparts = li == 0 ? 1 : x_parts;   // the embedding kernel writes one partial
     qd::Gemv8Args g;
     base(g, qkv_rows, H);
     g.xb = b.xb; g.in_ss = b.ss_x; g.in_parts = xparts; g.in_scale = b.sc_x; g.W = (const u16*)w.qkv;
@@ -672,8 +685,8 @@ int batch_step(const qd_model_desc* d, hipStream_t s) {
     go.out_scale = b.sc_r; go.yss = b.ss_r;
     if ((st = qd::gemv8_launch(go, qd::EPI_STORE, s))) return st;
     qd::Gemv8Args gu;
-    base(gu, I, H);
-    gu.xb = b.rb; gu.in_ss = b.ss_r; gu.in_parts = hparts; gu.in_scale = b.sc_r; gu.W = (const u16*)w.gate_up;
+    base(gu, I, H, true);
+    gu.xb = b.rb; gu.in_ss = b.ss_r; gu.in_parts = r_parts; gu.in_scale = b.sc_r; gu.W = (const u16*)w.gate_up;
     gu.up_offset = I; gu.yb = b.hb;
     if ((st = qd::gemv8_launch(gu, qd::EPI_SILU, s))) return st;
     // x = r + W_down hidden; image of x * (next input_norm | final_norm) * rstd(r)
@@ -682,7 +695,7 @@ int batch_step(const qd_model_desc* d, hipStream_t s) {
     qd::Gemv8Args gd;
     base(gd, H, I);
     gd.xb = b.hb; gd.W = (const u16*)w.down; gd.residual = b.r; gd.ldr = H; gd.y = b.x; gd.ldy = H;
-    gd.yb = b.xb; gd.yb_gamma = next_gamma; gd.pre_ss = b.ss_r; gd.pre_parts = hparts; gd.out_scale = b.sc_x;
+    gd.yb = b.xb; gd.yb_gamma = next_gamma; gd.pre_ss = b.ss_r; gd.pre_parts = r_parts; gd.out_scale = b.sc_x;
     gd.yss = b.ss_x;
     if ((st = qd::gemv8_launch(gd, qd::EPI_STORE, s))) return st;
   }
@@ -690,7 +703,8 @@ int batch_step(const qd_model_desc* d, hipStream_t s) {
   qd::Gemv8Args gl;
   base(gl, d->vocab, H);
   gl.ksplit = 1;
-  gl.xb = b.xb; gl.in_ss = b.ss_x; gl.in_parts = hparts; gl.in_scale = b.sc_x; gl.W = (const u16*)d->embed;
+  gl.rows_per_group = 16;
+  gl.xb = b.xb; gl.in_ss = b.ss_x; gl.in_parts = x_parts; gl.in_scale = b.sc_x; gl.W = (const u16*)d->embed;
   gl.y = reinterpret_cast<float*>(d->logits_out); gl.ldy = d->vocab; gl.part_val = b.part_val;
   gl.part_idx = b.part_idx;
   const int groups = qd::gemv8_row_groups(d->vocab);
@@ -882,7 +896,9 @@ int qd_batch_gemv(const float* x, long ldx, const void* gamma, float eps, const 
   g.xb = img; g.in_ss = gamma != nullptr ? ss : nullptr; g.in_parts = 1; g.in_scale = scale; g.eps = eps;
   g.W = (const u16*)W; g.ldw = ldw; g.N = N; g.K = K; g.residual = residual; g.ldr = ldr; g.y = y; g.ldy = ldy;
   g.nseq = nseq; g.kpart = kpart; g.kcount = kcount;
-  g.ksplit = batch_ksplit(N, K);
+  const BatchSplit sp = batch_split(N, K, epilogue == QD_BATCH_EPI_SILU);
+  g.ksplit = sp.ksplit;
+  g.rows_per_group = sp.rows_per_group;
   if (epilogue == QD_BATCH_EPI_SILU) {
     g.up_offset = up_offset;
     return qd::gemv8_launch(g, qd::EPI_SILU, S(stream));

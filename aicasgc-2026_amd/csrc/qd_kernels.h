@@ -192,7 +192,7 @@ constexpr int kBatchMax = 8;
 // Batch GEMV on MFMA: y[b][r] = f[b] * (W[r] . u[b]) for b < nseq, where u is
 // the input's operand image (u = x * gamma * s, written by the producer with
 // scale s = in_scale[b]) and f = rstd(in_ss) / s (1 / s without in_ss), so
-// y = W . (RMSNorm(x) * gamma).  K in {2048, 6144}; rows a multiple of 16.
+// y = W . (RMSNorm(x) * gamma).  K in {2048, 6144}; rows a multiple of rows_per_group.
 // The epilogue adds the residual (EPI_STORE) or forms silu(gate) * up
 // (EPI_SILU), stores y, and writes the output's own operand image (times
 // yb_gamma and out scale rstd(pre_ss), stored to out_scale) with per-row-group
@@ -217,18 +217,19 @@ struct Gemv8Args {
   const float* pre_ss = nullptr;   // [pre_parts][8]: output image scale rstd over N, or null (1)
   int pre_parts = 0;
   float* out_scale = nullptr;      // [8] the output image's scale, or null
-  float* yss = nullptr;            // [N/16][8] partial sums of squares of y, or null
+  float* yss = nullptr;            // [N/rows][8] partial sums of squares of y, or null
   int nseq = 0;
+  int rows_per_group = 16;         // 16 or 8 (not EPI_ARGMAX): rows of W per workgroup
   int ksplit = 1;                  // workgroups per row group along K (not EPI_ARGMAX)
-  float* kpart = nullptr;          // ksplit > 1: [N/16][ksplit][1 or 2 (EPI_SILU)][128] partial products
-  unsigned* kcount = nullptr;      // ksplit > 1: [N/16] arrival counters (zero, self-resetting)
+  float* kpart = nullptr;          // ksplit > 1: [N/rows][ksplit][1 or 2 (EPI_SILU)][rows * 8] partials
+  unsigned* kcount = nullptr;      // ksplit > 1: [N/rows] arrival counters (zero, self-resetting)
   int grid = 0;                    // EPI_ARGMAX: workgroups (each loops over row groups); 0: one per group
   float* part_val = nullptr;       // EPI_ARGMAX: [grid][8]
   long* part_idx = nullptr;
 };
 
 int gemv8_launch(const Gemv8Args& a, int epi, hipStream_t s);
-int gemv8_row_groups(long N);
+int gemv8_row_groups(long N, int rows_per_group = 16);
 // Image of u = x * gamma * s (gamma null: 1), s = rstd(x) when norm else 1,
 // sum of squares of x as one partial ss[8], s to scale[8].
 int bimage8_launch(const float* x, long ldx, const uint16_t* gamma, bool norm, float eps, int K, int nseq,
