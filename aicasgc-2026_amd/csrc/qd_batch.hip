@@ -196,23 +196,21 @@ __global__ __launch_bounds__(512) void gemv8_kernel(const Gemv8Args a) {
   float best = -INFINITY;
   int best_i = 0x7fffffff;
 
-  for (;;) {
-    const int nxt = rg + (int)gridDim.x;
-    u32x4 wn[ARGMAX ? NWT : 1], wn2[1];
-    if constexpr (ARGMAX) {
-      if (nxt < nrg) load_w(nxt, wn, wn2);
-    }
+  // One row group: MFMAs over the weights in wa (wa2: the up rows), the K-slice
+  // reduction through LDS, the K-split hand-off and the epilogue.  Returns
+  // false when this workgroup's part is done (K split, not the last to arrive).
+  auto process = [&](const auto& wa, const auto& wa2, int rg) -> bool {
     f32x4 acc = {0.f, 0.f, 0.f, 0.f}, acc2 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < NT; i += 2) {
       u32x4 t0, t1;
-      pair_to_mfma(wt, i / 2, t0, t1);
+      pair_to_mfma(wa, i / 2, t0, t1);
       acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, t0), __builtin_bit_cast(h8, bt[i]), acc, 0, 0,
                                                    0);
       acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, t1), __builtin_bit_cast(h8, bt[i + 1]), acc,
                                                    0, 0, 0);
       if constexpr (DUAL) {
-        pair_to_mfma(wt2, i / 2, t0, t1);
+        pair_to_mfma(wa2, i / 2, t0, t1);
         acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, t0), __builtin_bit_cast(h8, bt[i]), acc2,
                                                       0, 0, 0);
         acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, t1), __builtin_bit_cast(h8, bt[i + 1]),
@@ -257,7 +255,7 @@ __global__ __launch_bounds__(512) void gemv8_kernel(const Gemv8Args a) {
         __syncthreads();
         if (t == 0) s_last = arrive_last(a.kcount + rg, (unsigned)a.ksplit);
         __syncthreads();
-        if (!s_last) return;
+        if (!s_last) return false;
         if (t < OUT) {
           v = 0.f;
           v2 = 0.f;
@@ -307,13 +305,31 @@ __global__ __launch_bounds__(512) void gemv8_kernel(const Gemv8Args a) {
         if (a.out_scale != nullptr && rg == 0 && rl == 0) a.out_scale[seq] = s_osc[seq];
       }
     }
-    if constexpr (!ARGMAX) {
-      break;
-    } else {
+    return true;
+  };
+  if constexpr (!ARGMAX) {
+    if (!process(wt, wt2, rg)) return;
+  } else {
+    // The lm_head loops over row groups with the next group's weights in
+    // flight; the two buffers alternate roles (a register copy would wait for
+    // the prefetched loads).  The prefetch is unconditional (past the last
+    // group it re-reads the last group) so every path has the same loads in
+    // flight and each group waits only for its own.
+    u32x4 wn[NWT];
+    for (;;) {
+      int nxt = rg + (int)gridDim.x;
+      load_w(min(nxt, nrg - 1), wn, wt2);
+      __builtin_amdgcn_sched_barrier(0);   // keep the prefetch ahead of this group's work
+      process(wt, wt2, rg);
       if (nxt >= nrg) break;
       __syncthreads();   // s_part is rewritten by the next group
-#pragma unroll
-      for (int i = 0; i < NWT; ++i) wt[i] = wn[i];
+      rg = nxt;
+      nxt = rg + (int)gridDim.x;
+      load_w(min(nxt, nrg - 1), wt, wt2);
+      __builtin_amdgcn_sched_barrier(0);
+      process(wn, wt2, rg);
+      if (nxt >= nrg) break;
+      __syncthreads();
       rg = nxt;
     }
   }

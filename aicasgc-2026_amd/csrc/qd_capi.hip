@@ -708,7 +708,7 @@ int batch_step(const qd_model_desc* d, hipStream_t s) {
   gl.y = reinterpret_cast<float*>(d->logits_out); gl.ldy = d->vocab; gl.part_val = b.part_val;
   gl.part_idx = b.part_idx;
   const int groups = qd::gemv8_row_groups(d->vocab);
-  gl.grid = std::min(groups, 2 * qd_host::cu_count());
+  gl.grid = std::min(groups, qd_host::cu_count());   // one looping workgroup per CU (two buffers of weights in flight)
   if ((st = qd::gemv8_launch(gl, qd::EPI_ARGMAX, s))) return st;
   return qd::argmax8_reduce_launch(b.part_val, b.part_idx, gl.grid, d->token, B, s);
 }
