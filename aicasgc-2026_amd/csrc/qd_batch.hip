@@ -412,39 +412,52 @@ __global__ __launch_bounds__(256) void bimage8_kernel(const TX* x, long ldx, con
   }
 }
 
-// First maximal index per sequence over the workgroup partials (one block per
-// sequence); the result is the sequence's next token.
-__global__ __launch_bounds__(256) void argmax8_reduce_kernel(const float* part_val, const long* part_idx, int nblk,
-                                                             int64_t* token) {
-  __shared__ float r_v[256];
-  __shared__ long r_i[256];
-  const int seq = blockIdx.x;
-  float bv = -INFINITY;
-  long bi = 0x7fffffffffffL;
-  for (int b = threadIdx.x; b < nblk; b += blockDim.x) {
-    const float v = part_val[(long)b * kB + seq];
-    const long i = part_idx[(long)b * kB + seq];
-    if (v > bv || (v == bv && i < bi)) {
-      bv = v;
-      bi = i;
-    }
-  }
-  r_v[threadIdx.x] = bv;
-  r_i[threadIdx.x] = bi;
-  __syncthreads();
-  for (int s = blockDim.x / 2; s > 0; s >>= 1) {
-    if ((int)threadIdx.x < s) {
-      const float v = r_v[threadIdx.x + s];
-      const long i = r_i[threadIdx.x + s];
-      if (v > r_v[threadIdx.x] || (v == r_v[threadIdx.x] && i < r_i[threadIdx.x])) {
-        r_v[threadIdx.x] = v;
-        r_i[threadIdx.x] = i;
+// First maximal index per sequence over the workgroup partials: one block,
+// wave b reduces sequence b; the result is the sequence's next token.  With
+// adv_counter set the block then advances the decode state as advance8_kernel
+// does (one launch less per step).
+__global__ __launch_bounds__(512) void argmax8_reduce_kernel(const float* part_val, const long* part_idx, int nblk,
+                                                             int64_t* token, int nseq, int64_t* adv_out,
+                                                             int64_t* adv_counter, int64_t* adv_cache_position,
+                                                             int64_t* adv_rope_position, int adv_max_tokens) {
+  const int seq = threadIdx.x / kWave;
+  const int lane = lane_id();
+  const int64_t c = adv_counter != nullptr ? adv_counter[0] : 0;
+  if (seq < nseq) {
+    float bv = -INFINITY;
+    long bi = 0x7fffffffffffL;
+    for (int b = lane; b < nblk; b += kWave) {
+      const float v = part_val[(long)b * kB + seq];
+      const long i = part_idx[(long)b * kB + seq];
+      if (v > bv || (v == bv && i < bi)) {
+        bv = v;
+        bi = i;
       }
     }
-    __syncthreads();
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const float ov = __shfl_xor(bv, off);
+      const long oi = __shfl_xor(bi, off);
+      if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    if (lane == 0) {
+      // no finite maximum anywhere (all partials -inf / NaN): token 0
+      const int64_t tok = bi >= 0x7fffffffL ? 0 : bi;
+      token[seq] = tok;
+      if (adv_counter != nullptr) {
+        if (adv_out != nullptr && c < adv_max_tokens) adv_out[c * nseq + seq] = tok;
+        adv_cache_position[seq] += 1;
+        adv_rope_position[3 * seq + 0] += 1;
+        adv_rope_position[3 * seq + 1] += 1;
+        adv_rope_position[3 * seq + 2] += 1;
+      }
+    }
   }
-  // no finite maximum anywhere (all partials -inf / NaN): token 0
-  if (threadIdx.x == 0) token[seq] = r_i[0] >= 0x7fffffffL ? 0 : r_i[0];
+  __syncthreads();   // every wave read the counter before it moves
+  if (threadIdx.x == 0 && adv_counter != nullptr) adv_counter[0] = c + 1;
 }
 
 // Per sequence: out_tokens[counter][b] = token[b] (while counter < max_tokens),
@@ -528,8 +541,11 @@ int embed8_launch(const uint16_t* table, const int64_t* token, float* out, int H
 }
 
 int argmax8_reduce_launch(const float* part_val, const long* part_idx, int nblk, int64_t* token, int nseq,
-                          hipStream_t s) {
-  hipLaunchKernelGGL(argmax8_reduce_kernel, dim3((unsigned)nseq), dim3(256), 0, s, part_val, part_idx, nblk, token);
+                          hipStream_t s, int64_t* adv_out, int64_t* adv_counter, int64_t* adv_cache_position,
+                          int64_t* adv_rope_position, int adv_max_tokens) {
+  if (nseq < 1 || nseq > kB) return QD_ERR_SHAPE;
+  hipLaunchKernelGGL(argmax8_reduce_kernel, dim3(1), dim3(kB * kWave), 0, s, part_val, part_idx, nblk, token, nseq,
+                     adv_out, adv_counter, adv_cache_position, adv_rope_position, adv_max_tokens);
   return qd_host::launch_status("argmax8_reduce_kernel");
 }
 

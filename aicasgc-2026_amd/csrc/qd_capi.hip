@@ -710,6 +710,10 @@ int batch_step(const qd_model_desc* d, hipStream_t s) {
   const int groups = qd::gemv8_row_groups(d->vocab);
   gl.grid = std::min(groups, qd_host::cu_count());   // one looping workgroup per CU (two buffers of weights in flight)
   if ((st = qd::gemv8_launch(gl, qd::EPI_ARGMAX, s))) return st;
+  if (d->advance_counter != nullptr)
+    return qd::argmax8_reduce_launch(b.part_val, b.part_idx, gl.grid, d->token, B, s, d->advance_out_tokens,
+                                     d->advance_counter, const_cast<int64_t*>(d->cache_position),
+                                     const_cast<int64_t*>(d->rope_position), d->advance_max_tokens);
   return qd::argmax8_reduce_launch(b.part_val, b.part_idx, gl.grid, d->token, B, s);
 }
 

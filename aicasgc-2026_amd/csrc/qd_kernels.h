@@ -234,8 +234,11 @@ int gemv8_row_groups(long N, int rows_per_group = 16);
 // sum of squares of x as one partial ss[8], s to scale[8].
 int bimage8_launch(const float* x, long ldx, const uint16_t* gamma, bool norm, float eps, int K, int nseq,
                    uint16_t* img, float* ss, float* scale, hipStream_t s);
+// (with adv_counter: also the advance of advance8_launch)
 int argmax8_reduce_launch(const float* part_val, const long* part_idx, int nblk, int64_t* token, int nseq,
-                          hipStream_t s);
+                          hipStream_t s, int64_t* adv_out = nullptr, int64_t* adv_counter = nullptr,
+                          int64_t* adv_cache_position = nullptr, int64_t* adv_rope_position = nullptr,
+                          int adv_max_tokens = 0);
 // x[b] = embed[token[b]] and its image (gamma, scale rstd(x)), ss, scale.
 int embed8_launch(const uint16_t* table, const int64_t* token, float* out, int H, long V, int nseq,
                   const uint16_t* gamma, float eps, uint16_t* img, float* ss, float* scale, hipStream_t s);

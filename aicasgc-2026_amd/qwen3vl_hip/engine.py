@@ -403,13 +403,14 @@ class BatchDecodeEngine(_CapturedSteps):
     Every sequence has its own static cache rows ``[B, Hkv, T, D]`` per layer
     and its own cache / rope position, so ragged lengths need no padding.  The
     step is ``qd_decode_step`` with ``batch = B`` (MFMA batch GEMVs, per-sequence
-    split-KV attention, per-sequence argmax) followed by
-    ``qd_decode_advance_batch``, captured once into a HIP graph.  The reference
+    split-KV attention, per-sequence argmax) followed by the advance of
+    ``qd_decode_advance_batch`` (done by the argmax reduction itself unless
+    ``fuse_advance`` is False), captured once into a HIP graph.  The reference
     has no batch decode path (it rejects batch != 1, evaluation_wrapper.py:110-111).
     """
 
     def __init__(self, weights: ModelWeights, batch: int, capacity: int, device="cuda", attn_splits: int = 0,
-                 keep_logits: bool = False, steps_per_graph: int = 4):
+                 keep_logits: bool = False, steps_per_graph: int = 4, fuse_advance: bool = True):
         if not torch.cuda.is_available():
             raise RuntimeError("BatchDecodeEngine needs a ROCm GPU")
         if steps_per_graph < 1:
@@ -468,6 +469,15 @@ class BatchDecodeEngine(_CapturedSteps):
         self.desc = d
         self.graph = None
         self.graph_multi = None
+        if fuse_advance:
+            self._bind_advance()
+
+    def _bind_advance(self) -> None:
+        """The step ends with the per-sequence advance, fused into its argmax reduction."""
+        d = self.desc
+        d.advance_out_tokens = self.out_tokens.data_ptr()
+        d.advance_counter = self.step_counter.data_ptr()
+        d.advance_max_tokens = int(self.out_tokens.shape[0])
 
     def set_state(self, tokens, cache_positions, rope_positions) -> None:
         self.token.copy_(torch.as_tensor(tokens, dtype=torch.int64))
@@ -480,10 +490,14 @@ class BatchDecodeEngine(_CapturedSteps):
             self.out_tokens = torch.zeros(n, self.batch, dtype=torch.int64, device=self.device)
             self.graph = None
             self.graph_multi = None
+            if self.desc.advance_counter:
+                self._bind_advance()
 
     def step_eager(self) -> None:
         st = ctypes.c_void_p(torch.cuda.current_stream(self.device).cuda_stream)
         _lib.check(_lib.lib().qd_decode_step(ctypes.byref(self.desc), st), "qd_decode_step (batch)")
+        if self.desc.advance_counter:
+            return
         _lib.check(_lib.lib().qd_decode_advance_batch(
             ctypes.c_void_p(self.token.data_ptr()), ctypes.c_void_p(self.out_tokens.data_ptr()),
             ctypes.c_void_p(self.step_counter.data_ptr()), ctypes.c_void_p(self.cache_position.data_ptr()),

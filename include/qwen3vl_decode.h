@@ -237,10 +237,11 @@ typedef struct qd_model_desc {
   int batch;                   /* sequences per step: 0 or 1 = batch 1; 2..8 = batch step, then
                                   token [B], cache_position [B], rope_position [B][3], each layer's
                                   k_cache / v_cache [B, Hkv, T, D] and logits_out fp32 [B][V] */
-  /* Optional end-of-step advance (batch 1).  When advance_counter != NULL the
-   * step finishes with qd_decode_advance(token, advance_out_tokens,
-   * advance_counter, cache_position, rope_position, advance_max_tokens) done
-   * by the argmax reduction instead of a separate launch; the
+  /* Optional end-of-step advance.  When advance_counter != NULL the step
+   * finishes with qd_decode_advance (batch step: qd_decode_advance_batch,
+   * out_tokens [max][B]) on (token, advance_out_tokens, advance_counter,
+   * cache_position, rope_position, advance_max_tokens), done by the argmax
+   * reduction instead of a separate launch; the
    * cache_position / rope_position buffers are then written by the step. */
   int64_t* advance_out_tokens;
   int64_t* advance_counter;

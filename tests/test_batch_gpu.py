@@ -155,16 +155,22 @@ def test_batch_step_two_layers_matches_oracle(cuda, two_layer_weights):
     assert out[0] == toks
 
 
-def test_batch_graph_generation_matches_oracle(cuda, two_layer_weights):
+@pytest.mark.parametrize("fuse_advance", [True, False])
+def test_batch_graph_generation_matches_oracle(cuda, two_layer_weights, fuse_advance):
+    """Graph replays of 12 steps; the advance fused into the argmax reduction
+    or run as qd_decode_advance_batch after it."""
     from qwen3vl_hip.engine import BatchDecodeEngine
 
     w = two_layer_weights
     positions = [40, 3, 90, 12, 64, 27, 100, 8]
     tokens = [11, 22, 33, 44, 55, 66, 77, 88]
     n = 12
-    eng = BatchDecodeEngine(w, batch=8, capacity=128)
+    eng = BatchDecodeEngine(w, batch=8, capacity=128, fuse_advance=fuse_advance)
     caches = _fill_caches(eng, positions, 23)
     got = eng.decode(tokens, positions, positions, n, use_graph=True)
+    assert eng.cache_position.tolist() == [p + n for p in positions]
+    assert eng.rope_position.tolist() == [[p + n] * 3 for p in positions]
+    assert int(eng.step_counter.item()) == n
     ref_caches = [(k.clone(), v.clone()) for k, v in caches]
     cur, pos, ref = list(tokens), list(positions), []
     for _ in range(n):
