@@ -335,19 +335,39 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
   for (int i = threadIdx.x; i < G * S; i += blockDim.x)
     s_w[i / S][i % S] = load_coherent(lse_out + (long)(kvh * G + i / S) * S + i % S);
   __syncthreads();
+  // split weights exp(lse_s - max lse), once per (head, split); empty splits: exp(-inf) = 0
+  __shared__ float s_max[G];
+  if (threadIdx.x < G) {
+    float M = -INFINITY;
+    for (int s = 0; s < S; ++s) M = fmaxf(M, s_w[threadIdx.x][s]);
+    s_max[threadIdx.x] = M;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < G * S; i += blockDim.x) {
+    const float M = s_max[i / S];
+    s_w[i / S][i % S] = M != -INFINITY ? __expf(s_w[i / S][i % S] - M) : 0.f;
+  }
+  __syncthreads();
+  // The partials are read kMergeBatch splits at a time, every load of a batch
+  // issued before the first is used (unconditional, index clamped to the last
+  // split; the weight of a clamped duplicate is 0), so a batch costs one round
+  // trip to the coherence point instead of one per split.
+  constexpr int kMergeBatch = 8;
   for (int t = threadIdx.x; t < G * kD; t += blockDim.x) {
     const int g = t / kD;
     const int d = t % kD;
     const int h = kvh * G + g;
-    float M = -INFINITY;
-    for (int s = 0; s < S; ++s) M = fmaxf(M, s_w[g][s]);
     float num = 0.f, den = 0.f;
-    if (M != -INFINITY) {
-      const float* op = o_part + (long)h * S * kD + d;
-      for (int s = 0; s < S; ++s) {
-        const float w = __expf(s_w[g][s] - M);   // empty splits: exp(-inf) = 0
+    float* op = o_part + (long)h * S * kD + d;
+    for (int s0 = 0; s0 < S; s0 += kMergeBatch) {
+      float ov[kMergeBatch];
+#pragma unroll
+      for (int u = 0; u < kMergeBatch; ++u) ov[u] = load_coherent(op + (long)min(s0 + u, S - 1) * kD);
+#pragma unroll
+      for (int u = 0; u < kMergeBatch; ++u) {
+        const float w = s0 + u < S ? s_w[g][s0 + u] : 0.f;
         den += w;
-        num = __builtin_fmaf(w, load_coherent(const_cast<float*>(op) + (long)s * kD), num);
+        num = __builtin_fmaf(w, ov[u], num);
       }
     }
     const float o = den > 0.f ? num / den : 0.f;

@@ -50,10 +50,9 @@ __device__ __forceinline__ u32x4 bpermute4(int addr, const u32x4& v) {
                (unsigned)__builtin_amdgcn_ds_bpermute(addr, (int)v.z), (unsigned)__builtin_amdgcn_ds_bpermute(addr, (int)v.w)};
 }
 
-// rstd of sequence seq from `parts` partial sums of squares ([parts][8]) over
-// n elements; every lane of the calling wave gets the same value.
 // Partial sums of squares of sequence seq ([parts][8], parts <= 256): four per
-// lane, loaded ahead of their use; ss_rstd() finishes the reduction.
+// lane, loaded ahead of their use; ss_rstd() finishes the reduction (rstd over
+// n elements, the same value in every lane of the calling wave).
 constexpr int kMaxSsParts = 4 * kWave;
 struct SsPart {
   float v[4] = {0.f, 0.f, 0.f, 0.f};
@@ -257,11 +256,22 @@ __global__ __launch_bounds__(512) void gemv8_kernel(const Gemv8Args a) {
         __syncthreads();
         if (!s_last) return false;
         if (t < OUT) {
+          // every partial's load issued before the first is used (unconditional,
+          // index clamped; a clamped duplicate adds 0): one round trip, not ksplit
+          constexpr int kMaxSplit = kBatchMaxKsplit;
+          float p[kMaxSplit], p2[kMaxSplit];
+#pragma unroll
+          for (int q = 0; q < kMaxSplit; ++q) {
+            const long o = (long)min(q, a.ksplit - 1) * (NA * OUT) + t;
+            p[q] = load_coherent(kp + o);
+            if constexpr (DUAL) p2[q] = load_coherent(kp + o + OUT);
+          }
           v = 0.f;
           v2 = 0.f;
-          for (int q = 0; q < a.ksplit; ++q) {
-            v += load_coherent(kp + (long)q * (NA * OUT) + t);
-            if constexpr (DUAL) v2 += load_coherent(kp + (long)q * (NA * OUT) + OUT + t);
+#pragma unroll
+          for (int q = 0; q < kMaxSplit; ++q) {
+            v += q < a.ksplit ? p[q] : 0.f;
+            if constexpr (DUAL) v2 += q < a.ksplit ? p2[q] : 0.f;
           }
         }
       }
@@ -486,7 +496,9 @@ int launch8(const Gemv8Args& a, unsigned gx, hipStream_t s) {
 }  // namespace
 
 int gemv8_launch(const Gemv8Args& a, int epi, hipStream_t s) {
-  if (a.nseq < 1 || a.nseq > kB || a.ksplit < 1 || a.K % a.ksplit != 0 || a.xb == nullptr) return QD_ERR_SHAPE;
+  if (a.nseq < 1 || a.nseq > kB || a.ksplit < 1 || a.ksplit > kBatchMaxKsplit || a.K % a.ksplit != 0 ||
+      a.xb == nullptr)
+    return QD_ERR_SHAPE;
   if ((a.in_ss != nullptr && (a.in_parts < 1 || a.in_parts > kMaxSsParts)) ||
       (a.pre_ss != nullptr && (a.pre_parts < 1 || a.pre_parts > kMaxSsParts)))
     return QD_ERR_SHAPE;

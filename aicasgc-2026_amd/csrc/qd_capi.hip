@@ -389,7 +389,7 @@ struct StepBuffers {
   long* part_idx;
 };
 
-constexpr int kBatchMaxKsplit = 6;
+using qd::kBatchMaxKsplit;
 constexpr int kBatchCounters = 1024;
 
 int batch_of(const qd_model_desc* d) { return d->batch > 1 ? d->batch : 1; }

@@ -188,6 +188,7 @@ int decode_persistent_launch(const PersistArgs& a, hipStream_t s);
 // ---------------------------------------------------------------- batch step
 
 constexpr int kBatchMax = 8;
+constexpr int kBatchMaxKsplit = 6;   // K ranges of one batch-GEMV row group
 
 // Batch GEMV on MFMA: y[b][r] = f[b] * (W[r] . u[b]) for b < nseq, where u is
 // the input's operand image (u = x * gamma * s, written by the producer with
