@@ -32,7 +32,7 @@
 namespace qd {
 
 namespace {
-constexpr int kFusedMergeMaxSplits = 64;
+constexpr int kFusedMergeMaxSplits = 64;   // splits per kv head the fused merge accepts
 constexpr int kD = 128;
 constexpr int kHalf = 64;
 constexpr int kSlots = 16;
@@ -51,16 +51,12 @@ __device__ __forceinline__ void head_norm_rope(float x0, float x1, unsigned w0, 
   o1 = n1 * c + n0 * s;
 }
 
-// cos/sin of frequency slot j (inverse frequency inv_freq_j) from the (T, H, W)
-// rope positions (interleaved M-RoPE: j % 3 == 1 (j < 3*sec_h) -> H,
-// j % 3 == 2 (j < 3*sec_w) -> W, else T).
-__device__ __forceinline__ void mrope_cs(long pt, long ph, long pw, float inv_freq_j, int sec_h, int sec_w, int j,
-                                         float& c, float& s) {
-  long p = pt;
-  if (j % 3 == 1 && j < 3 * sec_h) p = ph;
-  else if (j % 3 == 2 && j < 3 * sec_w) p = pw;
-  const float f = (float)p * inv_freq_j;
-  sincosf(f, &s, &c);
+// Position stream of frequency slot j under interleaved M-RoPE: 1 (H) for
+// j % 3 == 1 (j < 3*sec_h), 2 (W) for j % 3 == 2 (j < 3*sec_w), else 0 (T).
+__device__ __forceinline__ int mrope_stream(int j, int sec_h, int sec_w) {
+  if (j % 3 == 1 && j < 3 * sec_h) return 1;
+  if (j % 3 == 2 && j < 3 * sec_w) return 2;
+  return 0;
 }
 
 // Online-softmax update of one slot with the kUnroll positions t, t+16, ...
@@ -180,8 +176,14 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
   unsigned pw[kPre][2] = {};   // fp16 bits, one per register (packing would wait for the loads)
   float ifq = 0.f;
   float q[G][8];
+  // (A load issued behind the K/V rows of every workgroup would wait for them in
+  // the memory queues, several microseconds at launch.  The rope position of
+  // rotary pair j is a per-lane vector load: a scalar load is waited for with
+  // every other outstanding scalar load, and the K/V addressing has some.)
+  long rpj = 0;
   if constexpr (FUSED_ROPE) {
     ifq = a.inv_freq[j];
+    rpj = rope_pos[mrope_stream(j, a.sec_h, a.sec_w)];
 #pragma unroll
     for (int i = 0; i < kPre; ++i) {
       const int item = w + 4 * i;
@@ -204,14 +206,16 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
   }
   constexpr int kStep = kSlots * kUnroll;
   u32x4 kk[kUnroll], vv[kUnroll], kn[kUnroll], vn[kUnroll];
+  __builtin_amdgcn_sched_barrier(0);   // every prologue input is requested before the K/V rows
   load_kv_batch(kb, vb, a.stride_s, wave_t0 + row_off, t1, kk, vv);
   load_kv_batch(kb, vb, a.stride_s, wave_t0 + kStep + row_off, t1, kn, vn);
+  __builtin_amdgcn_sched_barrier(0);   // both batches issued before the prologue's math waits
 
   __shared__ float s_q[G][kD];
   __shared__ __align__(16) uint16_t s_kv[2][kD];   // new token's K_rot and V, fp16 as cached
   if constexpr (FUSED_ROPE) {
     float c, s;
-    mrope_cs(rope_pos[0], rope_pos[1], rope_pos[2], ifq, a.sec_h, a.sec_w, j, c, s);
+    sincosf((float)rpj * ifq, &s, &c);
 #pragma unroll
     for (int i = 0; i < kPre; ++i) {
       const int item = w + 4 * i;
@@ -325,49 +329,52 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
 
   // ---- fused merge: the last split of this kv head to finish combines all of them
   __shared__ int s_last;
-  __shared__ float s_w[G][kFusedMergeMaxSplits];
   stores_done();
   __syncthreads();
   if (threadIdx.x == 0) s_last = arrive_last(a.done + (long)bq * a.Hkv + kvh, (unsigned)a.n_split);
   __syncthreads();
   if (!s_last) return;
   const int S = a.n_split;
-  for (int i = threadIdx.x; i < G * S; i += blockDim.x)
-    s_w[i / S][i % S] = load_coherent(lse_out + (long)(kvh * G + i / S) * S + i % S);
-  __syncthreads();
-  // split weights exp(lse_s - max lse), once per (head, split); empty splits: exp(-inf) = 0
-  __shared__ float s_max[G];
-  if (threadIdx.x < G) {
-    float M = -INFINITY;
-    for (int s = 0; s < S; ++s) M = fmaxf(M, s_w[threadIdx.x][s]);
-    s_max[threadIdx.x] = M;
-  }
-  __syncthreads();
-  for (int i = threadIdx.x; i < G * S; i += blockDim.x) {
-    const float M = s_max[i / S];
-    s_w[i / S][i % S] = M != -INFINITY ? __expf(s_w[i / S][i % S] - M) : 0.f;
-  }
-  __syncthreads();
-  // The partials are read kMergeBatch splits at a time, every load of a batch
-  // issued before the first is used (unconditional, index clamped to the last
-  // split; the weight of a clamped duplicate is 0), so a batch costs one round
-  // trip to the coherence point instead of one per split.
+  // Thread (g, d) reads the LSEs and partials of kMergeBatch splits at a time,
+  // every load of a batch issued before the first is used (unconditional, index
+  // clamped to the last split; a clamped duplicate gets weight 0), so a batch
+  // costs one round trip to the coherence point.  Weights are exp(lse_s - M)
+  // with M the running maximum, rescaled when a later batch raises it (with
+  // S <= kMergeBatch: exactly the maximum over all splits); empty splits have
+  // lse = -inf and weight 0.
   constexpr int kMergeBatch = 8;
   for (int t = threadIdx.x; t < G * kD; t += blockDim.x) {
     const int g = t / kD;
     const int d = t % kD;
     const int h = kvh * G + g;
-    float num = 0.f, den = 0.f;
+    float mrun = -INFINITY, num = 0.f, den = 0.f;
     float* op = o_part + (long)h * S * kD + d;
+    float* lp = lse_out + (long)h * S;
     for (int s0 = 0; s0 < S; s0 += kMergeBatch) {
-      float ov[kMergeBatch];
-#pragma unroll
-      for (int u = 0; u < kMergeBatch; ++u) ov[u] = load_coherent(op + (long)min(s0 + u, S - 1) * kD);
+      float lv[kMergeBatch], ov[kMergeBatch];
 #pragma unroll
       for (int u = 0; u < kMergeBatch; ++u) {
-        const float w = s0 + u < S ? s_w[g][s0 + u] : 0.f;
-        den += w;
-        num = __builtin_fmaf(w, ov[u], num);
+        const int s = min(s0 + u, S - 1);
+        lv[u] = load_coherent(lp + s);
+        ov[u] = load_coherent(op + (long)s * kD);
+      }
+      float bm = -INFINITY;
+#pragma unroll
+      for (int u = 0; u < kMergeBatch; ++u)
+        if (s0 + u < S) bm = fmaxf(bm, lv[u]);
+      if (bm > mrun) {
+        const float c = __expf(mrun - bm);   // mrun = -inf: c = 0 and num = den = 0 stay 0
+        num *= c;
+        den *= c;
+        mrun = bm;
+      }
+      if (mrun != -INFINITY) {
+#pragma unroll
+        for (int u = 0; u < kMergeBatch; ++u) {
+          const float w = s0 + u < S ? __expf(lv[u] - mrun) : 0.f;
+          den += w;
+          num = __builtin_fmaf(w, ov[u], num);
+        }
       }
     }
     const float o = den > 0.f ? num / den : 0.f;
