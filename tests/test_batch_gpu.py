@@ -130,11 +130,12 @@ def _fill_caches(eng, positions, seed):
     return caches
 
 
-def test_batch_step_two_layers_matches_oracle(cuda, two_layer_weights):
+@pytest.mark.parametrize("positions", [[5, 17, 0, 63, 100, 33, 1, 77],
+                                       [127, 0, 126, 64, 1, 2, 120, 31]])   # last cache row, empty prefix
+def test_batch_step_two_layers_matches_oracle(cuda, two_layer_weights, positions):
     from qwen3vl_hip.engine import BatchDecodeEngine
 
     w = two_layer_weights
-    positions = [5, 17, 0, 63, 100, 33, 1, 77]
     rope = [p + 11 for p in positions]
     tokens = [123, 4000, 7, 8191, 55, 1024, 2048, 3]
     eng = BatchDecodeEngine(w, batch=8, capacity=128, keep_logits=True)
