@@ -12,17 +12,19 @@
 // the consumer's factor f = rstd / s applies the RMSNorm, rstd coming from
 // per-row-group partial sums of squares written by the same producer.
 //
-// A workgroup (8 waves) owns 16 rows (the MFMA M dimension; 16 gate + 16 up
-// rows for the SiLU epilogue) and a K range of KW (1024, 2048, 3072 or 6144); wave w owns
-// the slice [w KW/8, (w+1) KW/8) and keeps its image tiles in registers.  W is
-// loaded in coalesced 128-byte row pieces and moved into the MFMA A layout
-// (row lane % 16, k 8 (lane / 16) .. +8) with ds_bpermute: loading the A layout
-// directly would make every lane of a load touch a different row.  The 8
-// K-slice partials are summed through LDS.  When K > KW the
-// row group's K ranges run in separate workgroups (grid y); each publishes its
-// partial and the last to arrive sums them in a fixed order and runs the
-// epilogue.  The lm_head (EPI_ARGMAX) grid loops over row groups, loading the
-// next group's weights before it reduces the current one.
+// A workgroup (8 waves) owns RG rows: 16 (the MFMA M dimension) or 8 (A rows
+// 8..15 zero, twice the workgroups without a K split); RG gate + RG up rows
+// for the SiLU epilogue.  It covers a K range of KW (1024, 2048, 3072 or 6144);
+// wave w owns the slice [w KW/8, (w+1) KW/8) and keeps its image tiles in
+// registers.  W is loaded in coalesced 128-byte row pieces and moved into the
+// MFMA A layout (row lane % 16, k 8 (lane / 16) .. +8) with ds_bpermute:
+// loading the A layout directly would make every lane of a load touch a
+// different row.  The 8 K-slice partials are summed through LDS.  When K > KW
+// the row group's K ranges run in separate workgroups (grid y); each publishes
+// its partial and the last to arrive sums them in a fixed order and runs the
+// epilogue.  The lm_head (EPI_ARGMAX) runs one workgroup per CU, each looping
+// over row groups with two weight buffers alternating roles (the next group's
+// weights in flight while the current one is reduced).
 //
 // Weights are loaded once per batch step (every weight byte serves all 8
 // sequences); the work is bound by HBM (16 flops per 2-byte weight).
