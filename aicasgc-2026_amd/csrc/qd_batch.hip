@@ -42,7 +42,6 @@ namespace {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 
 constexpr int kB = kBatchMax;     // sequences per batch step (8)
-constexpr int kRG = 16;           // rows per row group (MFMA M; 8 with zero rows)
 constexpr int kWaves = 8;         // K slices per workgroup
 constexpr int kKT = 32;           // K per MFMA
 
@@ -108,7 +107,6 @@ __global__ __launch_bounds__(512) void gemv8_kernel(const Gemv8Args a) {
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int lane = lane_id();
   const int m = lane & 15;
-  const int kg = (lane >> 4) * 8;
   const int t = threadIdx.x;
   const long kb = (long)blockIdx.y * KW + (long)w * KS;
   const long rows = DUAL ? a.up_offset : a.N;
