@@ -125,6 +125,16 @@ struct Spin {
 // Waits until every word of v[k] (16 bytes loaded from byte offset
 // off0 + k * step) shows parity `par`.  A lane that is still waiting re-polls
 // all of its words (branch-free: one wait per poll instead of one per word).
+// Re-issues the N loads of await4 as straight-line code (a loop nested in the
+// wait loop below is not unrolled by this compiler).
+template <int K, int N>
+__device__ __forceinline__ void repoll4(Rsrc r, unsigned off0, unsigned step, u32x4 (&v)[N]) {
+  if constexpr (K < N) {
+    v[K] = peek4(r, off0 + K * step);
+    repoll4<K + 1, N>(r, off0, step, v);
+  }
+}
+
 template <int N>
 __device__ __forceinline__ void await4(Rsrc r, unsigned off0, unsigned step, u32x4 (&v)[N], unsigned par,
                                        Spin& sp) {
@@ -140,8 +150,7 @@ __device__ __forceinline__ void await4(Rsrc r, unsigned off0, unsigned step, u32
     }
     --sp.left;
     __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-    for (int k = 0; k < N; ++k) v[k] = peek4(r, off0 + k * step);
+    repoll4<0, N>(r, off0, step, v);
   }
 }
 
@@ -252,16 +261,6 @@ __device__ __forceinline__ void rows_dot_norm(const u32x4 (&w)[R][KCH], const fl
   }
 #pragma unroll
   for (int r = 0; r < R; ++r) y[r] = wave_sum(acc[r]);
-}
-
-__device__ __forceinline__ void head_norm_rope_p(float x0, float x1, const uint16_t* w, float eps, float c, float s,
-                                                 int j, float& o0, float& o1) {
-  const float ss = wave_sum(x0 * x0 + x1 * x1);
-  const float rstd = rsqrtf(ss / (float)D + eps);
-  const float n0 = (x0 * rstd) * h2f(w[j]);
-  const float n1 = (x1 * rstd) * h2f(w[j + 64]);
-  o0 = n0 * c - n1 * s;
-  o1 = n1 * c + n0 * s;
 }
 
 // Weight streaming.  A wave's vector-memory loads complete in issue order, so a
