@@ -71,7 +71,7 @@ void argmax_ws(void* ws, GemvArgs& a) {
   a.part_val = reinterpret_cast<float*>(b + kArgmaxHeader + (size_t)qd::kMaxArgmaxBlocks * sizeof(long));
 }
 
-// Attention workspace: [reserved (256 B)] [o_part Hq*S*128 f32] [lse Hq*S f32].
+// Attention workspace: [arrival counters, one per kv head (256 B)] [o_part Hq*S*128 f32] [lse Hq*S f32].
 size_t attn_ws_bytes(int Hq, int Hkv, int S_) {
   (void)Hkv;
   return 256 + (size_t)Hq * S_ * 128 * 4 + (size_t)Hq * S_ * 4;
@@ -325,6 +325,15 @@ int qd_attention_decode(const void* q, int q_dtype, long q_stride, const void* k
   QD_REQUIRE(out_dtype == QD_F16 || out_dtype == QD_F32, QD_ERR_ARG, "bad out dtype");
   a.out = out;
   attn_ws(workspace, a);
+  if (q_dtype == out_dtype && n_split <= 16 && Hkv <= 64) {
+    // one launch: the last split of each kv head to finish merges them all
+    // (arrival counters in the workspace header: zeroed once, self-resetting).
+    // It reads the partials 8 splits per round trip; with more than 16 splits
+    // the merge kernel, which reads them all in parallel, is faster.
+    a.done = reinterpret_cast<unsigned*>(workspace);
+    return q_dtype == QD_F16 ? qd::attention_partial_launch<u16>(a, S(stream))
+                             : qd::attention_partial_launch<float>(a, S(stream));
+  }
   st = q_dtype == QD_F16 ? qd::attention_partial_launch<u16>(a, S(stream))
                          : qd::attention_partial_launch<float>(a, S(stream));
   if (st) return st;

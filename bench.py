@@ -16,7 +16,9 @@ Prints one JSON line: ms/token over the timed steps (value), tokens/s, the
 step's achieved HBM GB/s (algorithmic bytes: weights + K/V[0:L] + activations,
 each once), the same at a 4096-token context, the dominant kernel's roofline
 entry and the CPU baseline (the fp32 PyTorch restatement of the reference path
-on this host's cores).
+on this host's cores); beside it the batch-8 workload (config 4) and configs
+0-2 (one layer step, the five GEMVs, attention at L = 256..8192), each timed on
+cold operands against its roofline with the CPU time of the same call.
 
     python bench.py [--gpus 1] [--steps 250] [--warmup 5]
 """
@@ -24,6 +26,7 @@ on this host's cores).
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import os
 import platform
@@ -143,6 +146,166 @@ def cpu_baseline_batch8(weights_gpu, n_steps: int = 2) -> dict:
             "sample": f"median of {n_steps} batch-8 steps of the oracle's fp32 restatement at the KV lengths above"}
 
 
+ROTATE_BYTES = 512 << 20   # cold caches: every call reads a different copy (MALL: 256 MB)
+
+
+def _graph_us(fns, reps: int) -> float:
+    """Average microseconds per call of ``fns`` (each enqueues one call on the
+    current stream): one HIP graph holds every call once, events bracket
+    ``reps`` replays."""
+    import torch
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for f in fns:   # lazy initialisation outside the capture
+            f()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for f in fns:
+            f()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1000.0 / (reps * len(fns))
+
+
+def _cpu_ms(fn, n: int, warmup: int = 2) -> float:
+    times = []
+    for i in range(warmup + n):
+        t0 = time.perf_counter()
+        fn()
+        if i >= warmup:
+            times.append(time.perf_counter() - t0)
+    times.sort()
+    return round(1000.0 * times[len(times) // 2], 3)
+
+
+def bench_configs012(w, cpu: bool, reps: int = 5) -> dict:
+    """Configs 0-2 (one layer step, the five GEMVs, attention at four lengths)
+    against their HBM rooflines, each call on a cold copy of its operands
+    (copies rotated through >= 512 MB), with the oracle's fp32 time on this
+    host beside each (``cpu``)."""
+    import ctypes
+
+    import torch
+
+    from oracle import qwen3vl_oracle as O
+    from qwen3vl_hip import _lib
+    from qwen3vl_hip import synthetic as syn
+    from qwen3vl_hip.engine import DecodeEngine
+
+    lib = _lib.lib()
+    dev = torch.device("cuda:0")
+    shape = w.shape
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    gen = torch.Generator(device=dev).manual_seed(20)
+    out = {"method": ("GPU: HIP events around replays of one HIP graph that calls the kernel once per operand "
+                      f"copy (copies rotated through >= {ROTATE_BYTES >> 20} MiB, above the 256 MB MALL), "
+                      f"{reps} replays; roofline = algorithmic bytes / 8 TB/s.  CPU: the oracle's fp32 PyTorch "
+                      f"restatement, median of N calls after 2 warm-up, torch threads={cores}")}
+
+    # ---- config 0: one decoder layer, cache_position 512 (K/V rows 0..511 filled)
+    nl = max(4, -(-ROTATE_BYTES // 100_672_000))
+    engines = []
+    for i in range(nl):
+        one = syn.ModelWeights([w.layers[i]], w.embed_tokens, w.final_norm_weight, shape)
+        e = DecodeEngine(one, capacity=640)
+        e.k_caches[0][:, :, :512].normal_(generator=gen)
+        e.v_caches[0][:, :, :512].normal_(generator=gen)
+        e.set_state(4242, 512, 512)
+        engines.append(e)
+    c0 = {"bytes": persistent_launch_bytes(513, dataclasses.replace(shape, num_layers=1))}
+    if engines[0].step_mode == "persistent":
+        c0["persistent_us"] = round(_graph_us([e.layers_persistent for e in engines], reps), 2)
+        if any(e.status() for e in engines):
+            raise RuntimeError("persistent one-layer step reported a failed hand-off")
+    chain = ["qkv", "attn", "attn_merge", "o_proj", "gate_up", "down"]
+    c0["chain_us"] = round(_graph_us([lambda e=e: e.run_phases(chain, 0, 1) for e in engines], reps), 2)
+    best = min(v for k, v in c0.items() if k.endswith("_us"))
+    c0.update(roofline_us=round(c0["bytes"] / (PEAK_HBM_GBPS * 1e3), 2), frac=round(c0["bytes"] / (best * 1e-6) /
+                                                                                        1e9 / PEAK_HBM_GBPS, 4))
+    del engines
+    if cpu:
+        lw = {k: v.detach().to("cpu", torch.float32) for k, v in w.layers[0].tensors().items()}
+        kc = syn.normal(5, ("k",), (1, shape.num_kv_heads, 513, shape.head_dim))
+        vc = syn.normal(5, ("v",), (1, shape.num_kv_heads, 513, shape.head_dim))
+        x = syn.normal(5, ("x",), (shape.hidden,)).float()
+        cos, sin = O.mrope_cos_sin(torch.full((3, 1), 512, dtype=torch.int64))
+        c0["cpu_ms"] = _cpu_ms(lambda: O.decode_layer(lw, x, kc, vc, 512, cos[0], sin[0]), 10)
+        del lw
+    out["config0_layer_step"] = c0
+
+    # ---- config 1: the decode GEMVs (plain y = W x, fp16 in and out)
+    c1 = {}
+    for name, (n, k) in syn.GEMV_SHAPES.items():
+        copies = max(4, -(-ROTATE_BYTES // (2 * n * k)))
+        ws = [torch.randn(n, k, generator=gen, device=dev, dtype=torch.float16).mul_(0.02) for _ in range(copies)]
+        xs = [torch.randn(k, generator=gen, device=dev, dtype=torch.float16) for _ in range(copies)]
+        ys = [torch.empty(n, device=dev, dtype=torch.float16) for _ in range(copies)]
+
+        def call(i, n=n, k=k, ws=ws, xs=xs, ys=ys):
+            _lib.check(lib.qd_matvec_f16(_lib.ptr(xs[i]), _lib.ptr(ws[i]), None, _lib.ptr(ys[i]), n, k,
+                                         _lib.stream()), "qd_matvec_f16")
+
+        us = _graph_us([lambda i=i: call(i) for i in range(copies)], reps)
+        nbytes = 2 * n * k + 2 * k + 2 * n
+        r = {"shape": [n, k], "us": round(us, 2), "bytes": nbytes, "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+             "roofline_us": round(nbytes / (PEAK_HBM_GBPS * 1e3), 2),
+             "frac": round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)}
+        if cpu:
+            wc, xc = ws[0].float().cpu(), xs[0].float().cpu()
+            r["cpu_ms"] = _cpu_ms(lambda: O.gemv(xc, wc), 20 if n * k < 1e8 else 5)
+            del wc
+        c1[name] = r
+        del ws, xs, ys
+    out["config1_gemv"] = c1
+
+    # ---- config 2: split-KV attention, valid length L = T (cache_position L - 1)
+    c2 = {}
+    hq, hkv, d = shape.num_heads, shape.num_kv_heads, shape.head_dim
+    scale = 1.0 / (d ** 0.5)
+    for L in (256, 1024, 4096, 8192):
+        kv = 2 * 2 * hkv * L * d
+        copies = min(512, max(4, -(-ROTATE_BYTES // kv)))
+        ks = [torch.randn(hkv, L, d, generator=gen, device=dev, dtype=torch.float16) for _ in range(copies)]
+        vs = [torch.randn(hkv, L, d, generator=gen, device=dev, dtype=torch.float16) for _ in range(copies)]
+        q = torch.randn(hq, d, generator=gen, device=dev, dtype=torch.float16)
+        o = torch.empty(hq, d, device=dev, dtype=torch.float16)
+        cp = torch.full((1,), L - 1, dtype=torch.int64, device=dev)
+        n_split = int(lib.qd_attention_default_splits(L))
+        wsb = torch.zeros(int(lib.qd_attention_workspace_bytes(hq, hkv, n_split)), dtype=torch.uint8, device=dev)
+
+        def acall(i, L=L, ks=ks, vs=vs, q=q, o=o, cp=cp, n_split=n_split, wsb=wsb):
+            _lib.check(lib.qd_attention_decode(
+                _lib.ptr(q), _lib.QD_F16, d, _lib.ptr(ks[i]), _lib.ptr(vs[i]), L * d, d, L, _lib.ptr(cp),
+                ctypes.c_float(scale), _lib.ptr(o), _lib.QD_F16, hq, hkv, n_split, _lib.ptr(wsb), _lib.stream()),
+                "qd_attention_decode")
+
+        us = _graph_us([lambda i=i: acall(i) for i in range(copies)], reps)
+        nbytes = kv + 2 * 2 * hq * d
+        r = {"us": round(us, 2), "splits": n_split, "bytes": nbytes, "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+             "roofline_us": round(nbytes / (PEAK_HBM_GBPS * 1e3), 3),
+             "frac": round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)}
+        if cpu:
+            qc = q.float().cpu()
+            kc, vc = ks[0].cpu().unsqueeze(0), vs[0].cpu().unsqueeze(0)
+            r["cpu_ms"] = _cpu_ms(lambda: O.decode_attention(qc, kc, vc, L - 1, scale), 20)
+        c2[f"L{L}"] = r
+        del ks, vs
+    out["config2_attention"] = c2
+    torch.cuda.empty_cache()
+    return out
+
+
 def _cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -213,6 +376,8 @@ def main() -> int:
     ap.add_argument("--step-mode", choices=["auto", "chain", "persistent"], default="auto")
     ap.add_argument("--batch8-steps", type=int, default=64,
                     help="timed steps of the batch-8 workload (config 4); 0 skips it")
+    ap.add_argument("--no-configs012", action="store_true",
+                    help="skip configs 0-2 (one layer, the GEMVs, attention) against their rooflines")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -344,6 +509,16 @@ def main() -> int:
         b8 = bench_batch8(w, args.batch8_steps)
         log(f"batch8: {b8['ms_per_step']:.4f} ms/step, {b8['tokens_per_s']:.0f} tok/s, {b8['achieved_GBps']:.1f} GB/s")
 
+    # ---- configs 0-2 against their rooflines (cold operands), CPU beside them
+    c012 = None
+    if not args.no_configs012:
+        c012 = bench_configs012(w, cpu=not args.no_cpu)
+        c0 = c012["config0_layer_step"]
+        log("config0 one layer: " + ", ".join(f"{k} {v}" for k, v in c0.items()))
+        log("config1 GEMV us: " + ", ".join(f"{n} {r['us']} ({r['frac']:.2f})" for n, r in c012["config1_gemv"].items()))
+        log("config2 attention us: " + ", ".join(f"{n} {r['us']} ({r['frac']:.2f})"
+                                                 for n, r in c012["config2_attention"].items()))
+
     # ---- reference stream: a plain 256 MiB device copy (known bytes; also the
     # scale for the PMC FETCH_SIZE / WRITE_SIZE counters in profiles/)
     src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
@@ -419,6 +594,7 @@ def main() -> int:
         "device_copy_GBps": round(copy_gbps, 1),
         "tokens_head": tokens[:8],
         "batch8": b8,
+        "configs012": c012,
     }
     print(json.dumps(out), flush=True)
     return 0

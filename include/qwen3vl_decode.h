@@ -170,8 +170,11 @@ int qd_add_f16(const void* a, const void* b, void* out, long n, void* stream);
  *   L = min(cache_position[0] + 1, T); out[h] = softmax(q_h K[:L]^T * scale) V[:L]
  * for q head h on kv head h / (Hq/Hkv).  head_dim 128.  Each workgroup owns
  * one (kv head, split) and serves every q head of the group, so K/V is read
- * once.  Partials (normalised output + LSE) go to the workspace and a second
- * launch merges the splits (no cross-workgroup waiting inside a launch).
+ * once.  Partials (normalised output + LSE) go to the workspace; the last
+ * split of each kv head to finish merges them (an arrival counter per kv head
+ * in the workspace, which resets itself; no workgroup waits on another).
+ * When q_dtype != out_dtype, n_split > 16 or Hkv > 64 a second launch merges
+ * instead (faster for many splits: it reads all partials in parallel).
  * q: [Hq,128] with row stride q_stride (q_dtype); caches fp16 with head
  * stride cache_stride_h and row stride cache_stride_s; out [Hq,128] out_dtype.
  * Workspace: qd_attention_workspace_bytes(Hq, Hkv, n_split) bytes, zeroed

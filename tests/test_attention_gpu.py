@@ -51,15 +51,18 @@ def test_attention_split_count_invariance(cuda, split_k):
     assert_close_rel(out, ref, what=f"split_k={split_k}")
 
 
-def test_attention_partial_merge_matches_fused(cuda):
+@pytest.mark.parametrize("L", [1024, 4096])   # 16 splits: one launch; 64: partials + merge kernel
+def test_attention_partial_merge_matches_fused(cuda, L):
     import cuda_decode_attention as A
     from qwen3vl_hip import synthetic as syn
 
-    q, kc, vc, pos = syn.attention_inputs(4096)
+    q, kc, vc, pos = syn.attention_inputs(L)
     fused = _run(A.decode_attn_v4_fused, q, kc, vc, pos, cuda)
     two = _run(A.decode_attn_v4_splitkv, q, kc, vc, pos, cuda)
-    # same partials, same merge order: bit-identical
-    assert torch.equal(fused.cpu(), two.cpu())
+    # same partials; the in-kernel merge (last split of a kv head) and the merge
+    # kernel sum the splits in different orders, so the fp16 outputs may differ
+    # by one rounding step: at most 2^-10 of the largest output
+    assert_close_rel(fused.cpu(), two.cpu(), rel=2.0 ** -10, what="one-launch vs two-launch merge")
 
 
 def test_attention_length_one_returns_v0(cuda):
@@ -83,13 +86,14 @@ def test_attention_equal_keys_give_mean_of_values(cuda):
     assert_close_rel(out, expect, what="equal keys")
 
 
-def test_attention_graph_replay_self_resets(cuda):
+@pytest.mark.parametrize("T", [1024, 2048])   # one launch with arrival counters; two launches
+def test_attention_graph_replay_self_resets(cuda, T):
     """Capture once, replay at several cache positions: the arrival counters
     reset themselves, so every replay matches the eager result and the oracle."""
     import cuda_decode_attention as A
     from qwen3vl_hip import synthetic as syn
 
-    q, kc, vc, _ = syn.attention_inputs(2048)
+    q, kc, vc, _ = syn.attention_inputs(T)
     qd, kd, vd = q.to(cuda), kc.to(cuda), vc.to(cuda)
     cp = torch.tensor([100], dtype=torch.int64, device=cuda)
     ws: dict = {}
@@ -98,7 +102,7 @@ def test_attention_graph_replay_self_resets(cuda):
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         out = A.decode_attn_v4_cta_qhead_splitkv_fused(qd, kd, vd, SCALE, 2, cp, workspace=ws)
-    for pos in (100, 2047, 5, 999, 1500):
+    for pos in (100, T - 1, 5, T // 2 - 1, T + 100):
         cp.fill_(pos)
         g.replay()
         torch.cuda.synchronize()
