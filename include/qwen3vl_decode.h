@@ -178,7 +178,8 @@ int qd_add_f16(const void* a, const void* b, void* out, long n, void* stream);
  * q: [Hq,128] with row stride q_stride (q_dtype); caches fp16 with head
  * stride cache_stride_h and row stride cache_stride_s; out [Hq,128] out_dtype.
  * Workspace: qd_attention_workspace_bytes(Hq, Hkv, n_split) bytes, zeroed
- * once at allocation.  Replaces decode_attn_v4_cta_qhead_splitkv_fused
+ * once at allocation; calls that share a workspace must be ordered (one
+ * stream), since its counters and partials are reused by every call.  Replaces decode_attn_v4_cta_qhead_splitkv_fused
  * (cuda_decode_attention.py:489-558 -> decode_attention_v4_kernel.cu:646-910)
  * and decode_attn_v4_fused (cuda_decode_attention.py:305-392). */
 size_t qd_attention_workspace_bytes(int Hq, int Hkv, int n_split);
