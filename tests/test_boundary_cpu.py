@@ -158,3 +158,33 @@ def test_roofline_bytes_match_the_stated_figures():
     assert roofline_bytes_step(0) == 3_441_154_048
     assert roofline_bytes_step(4096) == 3_910_916_096
     assert roofline_bytes_step(4096) == O.roofline_bytes_step(4096)
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """The bench measures one GPU; asking for more exits with status 2 and a
+    message, before anything touches a device."""
+    import subprocess
+    import sys
+
+    repo = Path(__file__).resolve().parents[1]
+    r = subprocess.run([sys.executable, str(repo / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr
+    assert r.stdout == ""
+
+
+def test_bench_batch8_and_config_bytes_are_consistent():
+    """The batch-8 step bytes and the one-layer bytes bench.py reports follow
+    the same per-weight / per-K/V-row accounting as the batch-1 step."""
+    import dataclasses
+
+    import bench
+    from qwen3vl_hip.config import QWEN3VL_2B
+    from qwen3vl_hip.engine import roofline_bytes_batch_step, roofline_bytes_step
+
+    one = dataclasses.replace(QWEN3VL_2B, num_layers=1)
+    # one layer at cache position 512: weights + norms, K/V rows 0..512, embedding row + fp32 hidden
+    assert bench.persistent_launch_bytes(513, one) == 100_672_000 + 4096 * 513 + 2 * 2048 + 4 * 2048
+    # a batch of one sequence reads what the batch-1 step reads
+    assert roofline_bytes_batch_step([4096]) == roofline_bytes_step(4096)
