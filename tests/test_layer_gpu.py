@@ -2,8 +2,10 @@
 
 Two product paths are checked: the drop-in ``OptimizedDecoderLayer`` built
 from a transformers ``Qwen3VLTextDecoderLayer`` (fp16 activations between
-kernels, HF fp16 cos/sin), and the native decode step of the engine (fp32
-activations between kernels, device-side M-RoPE) on a 1-layer model.
+kernels, HF fp16 cos/sin; on a stand-in cache and on transformers' own
+``StaticCache`` over consecutive steps), and the native decode step of the
+engine (fp32 activations between kernels, device-side M-RoPE) on a 1-layer
+model.
 """
 
 from __future__ import annotations
@@ -65,6 +67,40 @@ def test_optimized_decoder_layer_config0(cuda):
     assert_close_rel(out.reshape(-1), ref, what="OptimizedDecoderLayer decode step")
     assert_close_rel(kc[0, :, 512].cpu(), kc_ref[0, :, 512].float(), what="layer K write")
     assert torch.equal(kc[0, :, :512].cpu(), inp.k_cache[0, :, :512])
+
+
+def test_optimized_decoder_layer_with_transformers_static_cache(cuda):
+    """The drop-in layer on transformers' own StaticCache (lazily initialised by
+    the layer on its first call): three consecutive decode steps, each reading
+    the K/V rows the previous ones wrote, against the oracle step by step."""
+    from transformers.cache_utils import StaticCache
+    from transformers.models.qwen3_vl.configuration_qwen3_vl import Qwen3VLTextConfig
+
+    import optimized_layer
+    from qwen3vl_hip import synthetic as syn
+
+    inp = syn.layer_step_inputs(seed=3, cache_position=0, capacity=64)
+    lw = inp.weights
+    layer = optimized_layer.OptimizedDecoderLayer(_hf_layer(lw)).to(cuda).half()
+    cfg = Qwen3VLTextConfig(hidden_size=2048, intermediate_size=6144, num_attention_heads=16,
+                            num_key_value_heads=8, head_dim=128, rms_norm_eps=1e-6, num_hidden_layers=1,
+                            vocab_size=1024)
+    cache = StaticCache(config=cfg, max_cache_len=64)
+    kc_ref = torch.zeros(1, 8, 64, 128, dtype=torch.float16)
+    vc_ref = torch.zeros_like(kc_ref)
+    for pos in range(3):
+        h = syn.normal(3, ("x", 100 + pos), (1, 1, 2048))
+        cos, sin = O.mrope_cos_sin(torch.full((3, 1), pos, dtype=torch.int64))
+        cos16, sin16 = cos.half().view(1, 1, 128), sin.half().view(1, 1, 128)
+        cp = torch.tensor([pos], dtype=torch.int64, device=cuda)
+        out = layer(h.to(cuda), (cos16.to(cuda), sin16.to(cuda)), past_key_values=cache, cache_position=cp)
+        ref = O.decode_layer(lw.tensors(), h.reshape(-1), kc_ref, vc_ref, pos, cos16.float().reshape(128),
+                             sin16.float().reshape(128))
+        assert_close_rel(out.reshape(-1), ref, what=f"drop-in layer on StaticCache, step at {pos}")
+    keys = cache.layers[0].keys
+    assert keys.device.type == "cuda" and keys.shape == (1, 8, 64, 128)
+    assert_close_rel(keys[0, :, :3].cpu(), kc_ref[0, :, :3].float(), what="StaticCache K rows 0..2")
+    assert torch.count_nonzero(keys[0, :, 3:]) == 0   # rows past the last step untouched
 
 
 def test_engine_phases_match_oracle_intermediates(cuda):
