@@ -352,11 +352,16 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
   u32x4 wo[1][4];                 // W_o row gw
   uint16_t nw0 = 0, nw1 = 0;      // q/k head-norm weights of rotary pair `lane`
 
-  auto issue_qkv = [&](const PersistLayer& Lx) {
-    load_row<4>(Lx.qkv + (long)(2 * gw) * H, lane, wq[0]);
-    load_row<4>(Lx.qkv + (long)(2 * gw + 1) * H, lane, wq[1]);
+  // rs: row stride of the weight loads (H; 0 after the last layer, when every
+  // wave re-reads one row that the L2 already holds instead of fetching rows
+  // nobody uses); tl: end of this workgroup's K/V rows (t1; t0 after the last
+  // layer: none).  The loads stay unconditional, so register liveness and the
+  // wait counts are the same on every layer.
+  auto issue_qkv = [&](const PersistLayer& Lx, long rs) {
+    load_row<4>(Lx.qkv + (long)(2 * gw) * rs, lane, wq[0]);
+    load_row<4>(Lx.qkv + (long)(2 * gw + 1) * rs, lane, wq[1]);
   };
-  auto issue_kvwo = [&](const PersistLayer& Lx) {
+  auto issue_kvwo = [&](const PersistLayer& Lx, long rs, int tl) {
     const int slot = w * 4 + (lane >> 4);
     const int dl = (lane & 15) * 8;
     const uint16_t* kb = Lx.k_cache + (long)kvh * a.T * D + dl;
@@ -366,12 +371,12 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
       const int tt = t0 + slot + u * SLOTS;
       kk[u] = u32x4{0u, 0u, 0u, 0u};
       vv[u] = u32x4{0u, 0u, 0u, 0u};
-      if (tt < t1 && tt != pos) {
+      if (tt < tl && tt != pos) {
         kk[u] = ld_stream(kb + (long)tt * D);
         vv[u] = ld_stream(vb + (long)tt * D);
       }
     }
-    load_row<4>(Lx.o_proj + (long)gw * H, lane, wo[0]);
+    load_row<4>(Lx.o_proj + (long)gw * rs, lane, wo[0]);
     const uint16_t* nw = (w == 2) ? Lx.k_norm : Lx.q_norm;
     nw0 = nw[lane];
     nw1 = nw[lane + 64];
@@ -397,16 +402,20 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
     *reinterpret_cast<u32x4*>(s_gin + tid * 8) = gi;
     *reinterpret_cast<u32x4*>(s_gpost + tid * 8) = gp;
   }
-  issue_qkv(a.layers[0]);
-  issue_kvwo(a.layers[0]);
+  issue_qkv(a.layers[0], H);
+  issue_kvwo(a.layers[0], H, t1);
 
   for (int l = 0; l < a.num_layers; ++l) {
     const PersistLayer& Lw = a.layers[l];
     const unsigned par = parity_of(ep, a.num_layers, l);
-    // The next layer's weights are issued unconditionally (the last layer
-    // re-issues its own, unused): a conditional issue would leave the previous
-    // values live to the end of the iteration on the path that skips it.
+    // The next layer's weights are issued unconditionally (a conditional issue
+    // would leave the previous values live to the end of the iteration on the
+    // path that skips it); after the last layer the loads are made cheap
+    // instead (row stride 0, no K/V rows).
     const PersistLayer& Ln = a.layers[l + 1 < a.num_layers ? l + 1 : l];
+    const bool more = l + 1 < a.num_layers;
+    const long rs_n = more ? (long)H : 0L;
+    const int tl_n = more ? t1 : t0;
     u32x4 wgu[6][4];              // W_gate/up rows 3gw..3gw+2 (+I)
     u32x4 wd[1][12];              // W_down row gw
 
@@ -636,8 +645,8 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
     }
     QD_FRESH_LANE();
     if (streamer) {
-      issue_qkv(Ln);
-      issue_kvwo(Ln);
+      issue_qkv(Ln, rs_n);
+      issue_kvwo(Ln, rs_n, tl_n);
     }
 
     // ================================================================ DOWN
@@ -649,7 +658,7 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
       // every wave finished this layer's norms before the barrier above
       *reinterpret_cast<u32x4*>(s_gin + tid * 8) = gi_next;
       *reinterpret_cast<u32x4*>(s_gpost + tid * 8) = gp_next;
-      issue_qkv(Ln);
+      issue_qkv(Ln, rs_n);
     }
     {
       float y[1];
@@ -662,7 +671,7 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
       if (!streamer) {
         puts_done();
         // the next layer's K/V rows and W_o row: in flight across the x hand-off
-        issue_kvwo(Ln);
+        issue_kvwo(Ln, rs_n, tl_n);
       }
     }
   }
