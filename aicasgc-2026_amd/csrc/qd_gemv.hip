@@ -388,13 +388,14 @@ int gemv_silu(const GemvArgs& a, hipStream_t s) {
 template <int PRO, typename TX, typename TY>
 int gemv_argmax(const GemvArgs& a, hipStream_t s) {
   if (!has_fixed_k(a.K)) return QD_ERR_SHAPE;
-  // 2 blocks of 4 waves per CU, each looping over row groups with the next
-  // group's rows in flight: 96.5-97 us for the 151936 x 2048 lm_head against
-  // 100-102 us with 1, 3 or 4 per CU (same-box sweep)
-  long max_blocks = (long)qd_host::cu_count() * 2;
+  // 4 blocks of 4 waves per CU, each wave looping over pairs of rows with the
+  // next pair in flight: 94.8-95.3 us for the 151936 x 2048 lm_head, against
+  // 95.6-95.9 with 6 or 8 blocks and 96.4 with 4 rows per wave at 2 blocks
+  // (same-box sweeps; 4 rows at 4 blocks: 100-102 us)
+  long max_blocks = (long)qd_host::cu_count() * 4;
   if (max_blocks > kMaxArgmaxBlocks) max_blocks = kMaxArgmaxBlocks;
   long blocks = 0;
-  int st = launch_k<4, PRO, EPI_ARGMAX, TX, TY>(a, a.K, 1, max_blocks, s, &blocks);
+  int st = launch_k<2, PRO, EPI_ARGMAX, TX, TY>(a, a.K, 1, max_blocks, s, &blocks);
   if (st != QD_OK) return st;
   hipLaunchKernelGGL(argmax_reduce_kernel, dim3(1), dim3(kThreads), 0, s, a, (int)blocks);
   return qd_host::launch_status("argmax_reduce_kernel");
