@@ -111,11 +111,13 @@ __device__ __forceinline__ void online_softmax_batch(const u32x4 (&kk)[kUnroll],
 }
 
 // K/V rows of positions t, t+16, ... into registers.  The loads are
-// unconditional (rows past t1 re-read row t1 - 1, an L1/L2 hit, so every
-// register holds finite cache data) and the number of loads in flight is the
-// same on every path, so a wave waits only for the batch it consumes.  The
-// softmax gives positions >= t1 weight 0; the fused variant replaces the new
-// position's row (not yet in the cache) from LDS.
+// unconditional (rows past t1 re-read row t1 - 1, an L1/L2 hit) and the number
+// of loads in flight is the same on every path, so a wave waits only for the
+// batch it consumes.  The softmax gives positions >= t1 weight 0 and their V
+// registers are zeroed before use: in the fused variant row t1 - 1 can be the
+// new position, whose cache row still holds stale data when it is loaded (it is
+// replaced from LDS only where it is the slot's own position), and a weight of
+// 0 times a non-finite value would still be NaN.
 __device__ __forceinline__ void load_kv_batch(const uint16_t* kb, const uint16_t* vb, long stride_s, int t, int t1,
                                               u32x4 (&kk)[kUnroll], u32x4 (&vv)[kUnroll]) {
   const int last = t1 > 0 ? t1 - 1 : 0;
@@ -264,16 +266,18 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
     for (int i = 0; i < 8; ++i) acc[g][i] = 0.f;
   }
 
-  // the new position comes from LDS (fp16, as written to the cache)
+  // the new position comes from LDS (fp16, as written to the cache); positions
+  // past t1 contribute exact zeros (their scores are -inf, their V cleared)
   auto consume = [&](u32x4 (&bk)[kUnroll], u32x4 (&bv)[kUnroll], int t) {
-    if constexpr (FUSED_ROPE) {
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
+    for (int u = 0; u < kUnroll; ++u) {
+      if constexpr (FUSED_ROPE) {
         if (t + u * kSlots == pos && pos < t1) {
           bk[u] = *reinterpret_cast<const u32x4*>(&s_kv[0][dl]);
           bv[u] = *reinterpret_cast<const u32x4*>(&s_kv[1][dl]);
         }
       }
+      if (t + u * kSlots >= t1) bv[u] = u32x4{0u, 0u, 0u, 0u};
     }
     online_softmax_batch<G>(bk, bv, t, t1, q, a.scale, m, l, acc);
   };

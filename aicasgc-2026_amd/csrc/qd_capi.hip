@@ -845,6 +845,7 @@ static int step_phases(const qd_model_desc* d, int first_layer, int n_layers, un
   GemvArgs gl;
   gl.x = b.x; gl.gamma = (const u16*)d->final_norm; gl.eps = d->eps; gl.W = (const u16*)d->embed;
   gl.N = d->vocab; gl.K = H; gl.ldw = H; gl.y = d->logits_out; gl.token = d->token;
+  gl.argmax_f16 = d->argmax_f16_logits != 0;
   argmax_ws(b.argmax_ws, gl);
   if (advance && d->advance_counter != nullptr) {
     gl.adv_out = d->advance_out_tokens; gl.adv_counter = d->advance_counter;

@@ -218,8 +218,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const long o = o0 + r;
-        if (o < a.N && acc[r] > best_v) {  // rows visited in increasing order: first max wins
-          best_v = acc[r];
+        const float v = a.argmax_f16 ? h2f(f2h(acc[r])) : acc[r];
+        if (o < a.N && v > best_v) {  // rows visited in increasing order: first max wins
+          best_v = v;
           best_i = o;
         }
       }

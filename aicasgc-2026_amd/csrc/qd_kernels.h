@@ -37,6 +37,10 @@ struct GemvArgs {
   int64_t* adv_cache_position = nullptr;
   int64_t* adv_rope_position = nullptr;
   int adv_max_tokens = 0;
+  // EPI_ARGMAX: compare the logits rounded to fp16 (the reference's fp16
+  // logits + torch.argmax: among logits equal in fp16 the first index wins)
+  // instead of the fp32 accumulators
+  int argmax_f16 = 0;
 };
 
 template <int PRO, typename TX, typename TY>

@@ -30,30 +30,6 @@ def _load_ext():
     return _lib.lib()
 
 
-def _workspace_layout(*, num_kv_heads: int, num_key_value_groups: int, head_dim: int, split_k: int) -> dict:
-    """Reference workspace shapes (cuda_decode_attention.py:74-79), kept for callers that build them."""
-    return {
-        "partial_acc_shape": (num_kv_heads, split_k, num_key_value_groups, head_dim),
-        "partial_stats_shape": (num_kv_heads, split_k, num_key_value_groups, 2),
-        "out_shape": (1, num_kv_heads * num_key_value_groups, head_dim),
-    }
-
-
-def _qhead_workspace_layout(*, num_heads: int, head_dim: int, split_k: int) -> dict:
-    return {
-        "partial_acc_shape": (num_heads, split_k, head_dim),
-        "partial_stats_shape": (num_heads, split_k, 2),
-        "out_shape": (1, num_heads, head_dim),
-    }
-
-
-def _v4_launch_config(seq_len: int) -> int:
-    """Reference split heuristic (cuda_decode_attention.py:216-223)."""
-    if seq_len < 1024:
-        return 16
-    return 32
-
-
 def _supported(q, k, v, num_key_value_groups, cache_position) -> bool:
     return not (
         q.device.type != "cuda" or k.device.type != "cuda" or v.device.type != "cuda"

@@ -24,21 +24,21 @@ def fused_qk_rms_norm_rope(q, k, q_weight, k_weight, eps: float, cos, sin):
     """Per-head RMSNorm + rotate-half RoPE of q [B,S,Hq,128] and k [B,S,Hkv,128]
     with cos/sin [B,S,128] (reference cuda_decode_small_ops.py:70-133)."""
     if not _all_cuda_half(q, k, q_weight, k_weight, cos, sin):
-        raise RuntimeError("fused_qk_rms_norm_rope expects fp16 CUDA tensors")
+        raise RuntimeError("fused_qk_rms_norm_rope: every tensor must be fp16 on the GPU")
     if q.ndim != 4 or k.ndim != 4:
-        raise RuntimeError("fused_qk_rms_norm_rope expects q/k as [B, S, H, D]")
+        raise RuntimeError("fused_qk_rms_norm_rope: q and k must be 4-D [batch, seq, heads, 128]")
     if q.shape[:2] != k.shape[:2]:
-        raise RuntimeError("q/k batch-seq shapes must match")
+        raise RuntimeError("fused_qk_rms_norm_rope: q and k disagree on batch or sequence length")
     if q.shape[-1] != 128 or k.shape[-1] != 128:
-        raise RuntimeError("fused_qk_rms_norm_rope currently supports only head_dim=128")
+        raise RuntimeError("fused_qk_rms_norm_rope: head size must be 128")
     if q.shape[2] != k.shape[2] * 2:
-        raise RuntimeError("fused_qk_rms_norm_rope currently supports q_heads == 2 * kv_heads")
+        raise RuntimeError("fused_qk_rms_norm_rope: need twice as many q heads as k heads")
     if q_weight.numel() != 128 or k_weight.numel() != 128:
-        raise RuntimeError("fused_qk_rms_norm_rope expects q/k norm weights of shape [128]")
+        raise RuntimeError("fused_qk_rms_norm_rope: q/k norm weights must hold 128 values")
     q_in, k_in = q.contiguous(), k.contiguous()
     cos_in, sin_in = cos.contiguous(), sin.contiguous()
     if cos_in.shape != q_in.shape[:2] + (128,) or sin_in.shape != q_in.shape[:2] + (128,):
-        raise RuntimeError("fused_qk_rms_norm_rope expects cos/sin shaped [B, S, 128]")
+        raise RuntimeError("fused_qk_rms_norm_rope: cos/sin must be [batch, seq, 128]")
     m = q_in.shape[0] * q_in.shape[1]
     q_out, k_out = torch.empty_like(q_in), torch.empty_like(k_in)
     qw, kw = q_weight.contiguous(), k_weight.contiguous()   # held until the launch is enqueued
@@ -55,34 +55,34 @@ def fused_q_rope_kv_cache_update(q, k, v, q_weight, k_weight, eps: float, cos, s
     returns the rotated q [1,1,Hq,128] (reference cuda_decode_small_ops.py:136-225)."""
     if not (_all_cuda_half(q, k, v, q_weight, k_weight, cos, sin, k_cache, v_cache)
             and cache_position.device.type == "cuda" and cache_position.dtype == torch.long):
-        raise RuntimeError("fused_q_rope_kv_cache_update expects fp16 CUDA tensors and int64 cache_position")
+        raise RuntimeError("fused_q_rope_kv_cache_update: tensors must be fp16 on the GPU, cache_position int64 on the GPU")
     if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
-        raise RuntimeError("fused_q_rope_kv_cache_update expects q/k/v as [B, S, H, D]")
+        raise RuntimeError("fused_q_rope_kv_cache_update: q, k and v must be 4-D [batch, seq, heads, 128]")
     if q.shape[:2] != k.shape[:2] or k.shape != v.shape:
-        raise RuntimeError("q/k/v shapes must match decode layout")
+        raise RuntimeError("fused_q_rope_kv_cache_update: k and v shapes differ, or q disagrees with them")
     if q.shape[0] != 1 or q.shape[1] != 1 or k.shape[0] != 1 or k.shape[1] != 1:
-        raise RuntimeError("fused_q_rope_kv_cache_update currently supports single-token decode only")
+        raise RuntimeError("fused_q_rope_kv_cache_update: one token per call (batch 1, seq 1)")
     if q.shape[-1] != 128 or k.shape[-1] != 128 or v.shape[-1] != 128:
-        raise RuntimeError("fused_q_rope_kv_cache_update currently supports only head_dim=128")
+        raise RuntimeError("fused_q_rope_kv_cache_update: head size must be 128")
     if q.shape[2] != k.shape[2] * 2:
-        raise RuntimeError("fused_q_rope_kv_cache_update currently supports q_heads == 2 * kv_heads")
+        raise RuntimeError("fused_q_rope_kv_cache_update: need twice as many q heads as kv heads")
     if q_weight.numel() != 128 or k_weight.numel() != 128:
-        raise RuntimeError("fused_q_rope_kv_cache_update expects q/k norm weights of shape [128]")
+        raise RuntimeError("fused_q_rope_kv_cache_update: q/k norm weights must hold 128 values")
     if cos.shape != q.shape[:2] + (128,) or sin.shape != q.shape[:2] + (128,):
-        raise RuntimeError("fused_q_rope_kv_cache_update expects cos/sin shaped [B, S, 128]")
+        raise RuntimeError("fused_q_rope_kv_cache_update: cos/sin must be [batch, seq, 128]")
     if k_cache.ndim != 4 or v_cache.ndim != 4:
-        raise RuntimeError("fused_q_rope_kv_cache_update expects k_cache/v_cache as [B, KVH, T, D]")
+        raise RuntimeError("fused_q_rope_kv_cache_update: caches must be 4-D [batch, kv heads, rows, 128]")
     if k_cache.shape[0] != 1 or v_cache.shape[0] != 1:
-        raise RuntimeError("fused_q_rope_kv_cache_update currently supports batch=1 cache")
+        raise RuntimeError("fused_q_rope_kv_cache_update: caches must have batch 1")
     if k_cache.shape[1] != k.shape[2] or v_cache.shape[1] != v.shape[2]:
-        raise RuntimeError("cache kv-head count mismatch")
+        raise RuntimeError("fused_q_rope_kv_cache_update: cache and k have different kv head counts")
     if k_cache.shape[-1] != 128 or v_cache.shape[-1] != 128:
-        raise RuntimeError("cache head_dim mismatch")
+        raise RuntimeError("fused_q_rope_kv_cache_update: cache rows are not 128 wide")
     if cache_position.ndim != 1 or cache_position.numel() != 1:
-        raise RuntimeError("cache_position must be shape [1]")
+        raise RuntimeError("fused_q_rope_kv_cache_update: cache_position must hold exactly one position")
     if (k_cache.stride(-1) != 1 or v_cache.stride(-1) != 1 or k_cache.stride(1) != v_cache.stride(1)
             or k_cache.stride(2) != v_cache.stride(2) or k_cache.shape != v_cache.shape):
-        raise RuntimeError("k_cache/v_cache must share one [1, KVH, T, D] layout with unit last stride")
+        raise RuntimeError("fused_q_rope_kv_cache_update: k_cache and v_cache need the same strides and contiguous rows")
     # contiguous copies are bound to locals so they outlive the asynchronous launch's enqueue
     q_in, k_in, v_in = q.contiguous(), k.contiguous(), v.contiguous()
     qw, kw = q_weight.contiguous(), k_weight.contiguous()
@@ -100,9 +100,9 @@ def fused_q_rope_kv_cache_update(q, k, v, q_weight, k_weight, eps: float, cos, s
 def fused_silu_mul(gate, up):
     """silu(gate) * up (reference cuda_decode_small_ops.py:228-247)."""
     if not _all_cuda_half(gate, up):
-        raise RuntimeError("fused_silu_mul expects fp16 CUDA tensors")
+        raise RuntimeError("fused_silu_mul: gate and up must be fp16 on the GPU")
     if gate.shape != up.shape:
-        raise RuntimeError("fused_silu_mul expects gate/up with identical shapes")
+        raise RuntimeError("fused_silu_mul: gate and up shapes differ")
     g, u = gate.contiguous(), up.contiguous()
     out = torch.empty_like(g)
     _lib.check(_load_ext().qd_silu_mul_f16(_lib.ptr(g), _lib.ptr(u), _lib.ptr(out), g.numel(),
@@ -113,11 +113,11 @@ def fused_silu_mul(gate, up):
 def fused_add_rms_norm(residual, x, weight, eps: float):
     """(residual + x, rmsnorm(residual + x) * weight) (reference cuda_decode_small_ops.py:250-287)."""
     if not _all_cuda_half(residual, x, weight):
-        raise RuntimeError("fused_add_rms_norm expects fp16 CUDA tensors")
+        raise RuntimeError("fused_add_rms_norm: every tensor must be fp16 on the GPU")
     if residual.shape != x.shape:
-        raise RuntimeError("fused_add_rms_norm expects residual/x with identical shapes")
+        raise RuntimeError("fused_add_rms_norm: residual and x shapes differ")
     if residual.shape[-1] != weight.numel():
-        raise RuntimeError("fused_add_rms_norm weight size mismatch")
+        raise RuntimeError("fused_add_rms_norm: weight length differs from the last dimension")
     r, xi = residual.contiguous(), x.contiguous()
     cols = r.shape[-1]
     rows = r.numel() // cols
@@ -132,9 +132,9 @@ def fused_add_rms_norm(residual, x, weight, eps: float):
 def rms_norm(x, weight, eps: float):
     """rmsnorm(x) * weight over the last dim (reference cuda_decode_small_ops.py:290-317)."""
     if not _all_cuda_half(x, weight):
-        raise RuntimeError("rms_norm expects fp16 CUDA tensors")
+        raise RuntimeError("rms_norm: x and weight must be fp16 on the GPU")
     if x.shape[-1] != weight.numel():
-        raise RuntimeError("rms_norm weight size mismatch")
+        raise RuntimeError("rms_norm: weight length differs from the last dimension")
     xi = x.contiguous()
     cols = xi.shape[-1]
     out = torch.empty_like(xi)
@@ -147,9 +147,9 @@ def rms_norm(x, weight, eps: float):
 def add(a, b):
     """a + b (reference cuda_decode_small_ops.py:320-339)."""
     if not _all_cuda_half(a, b):
-        raise RuntimeError("add expects fp16 CUDA tensors")
+        raise RuntimeError("add: both operands must be fp16 on the GPU")
     if a.shape != b.shape:
-        raise RuntimeError("add expects identical shapes")
+        raise RuntimeError("add: operand shapes differ")
     ai, bi = a.contiguous(), b.contiguous()
     out = torch.empty_like(ai)
     _lib.check(_load_ext().qd_add_f16(_lib.ptr(ai), _lib.ptr(bi), _lib.ptr(out), ai.numel(),

@@ -94,7 +94,8 @@ class OptimizedDecoderLayer(nn.Module):
         self._o_proj_workspace: dict = {"type": "nosplit"}
 
     # ------------------------------------------------------------ dispatch
-    def _static_kv(self, past_key_values, k_like: torch.Tensor):
+    def _static_layer(self, past_key_values, k_like: torch.Tensor):
+        """The StaticLayer of this layer when its K/V tensors suit the HIP decode step."""
         if past_key_values is None:
             return None
         layers = getattr(past_key_values, "layers", None)
@@ -108,14 +109,41 @@ class OptimizedDecoderLayer(nn.Module):
             return None
         if getattr(layer, "max_cache_len", kc.shape[2]) != kc.shape[2]:
             return None
-        return kc, vc
+        return layer
 
-    def _decode_ok(self, hidden_states, position_embeddings, cache_position) -> bool:
+    @staticmethod
+    def _decode_position(layer, cache_position, device):
+        """Cache row of the new token: ``cache_position`` when the caller gives
+        it (the reference's graph runner does, evaluation_wrapper.py:941-960),
+        else the StaticLayer's running length ``cumulative_length``, which is
+        where transformers' own StaticLayer.update writes (cache_utils.py
+        StaticLayer.update).  Both stay on the device (no host sync)."""
+        if cache_position is not None:
+            if cache_position.device.type == "cuda" and cache_position.numel() == 1:
+                return cache_position.reshape(1)
+            return None
+        cl = getattr(layer, "cumulative_length", None)
+        if torch.is_tensor(cl) and cl.device == device and cl.numel() == 1 and cl.dtype == torch.int64:
+            return cl.reshape(1)
+        return None
+
+    @staticmethod
+    def _advance_length(layer, pos: torch.Tensor) -> None:
+        """Keep the StaticLayer's running length at pos + 1 after the HIP step
+        wrote row ``pos``, as StaticLayer.update would: transformers reads it
+        for default position ids and the next write row.  In place on the
+        device, so it is also replayed inside a captured graph."""
+        cl = getattr(layer, "cumulative_length", None)
+        if torch.is_tensor(cl) and cl.device == pos.device:
+            cl.copy_((pos + 1).reshape(cl.shape))
+        elif cl is not None and not torch.cuda.is_current_stream_capturing():
+            layer.cumulative_length = (pos + 1).reshape(())
+
+    def _decode_ok(self, hidden_states, position_embeddings) -> bool:
         cos, sin = position_embeddings
         return (hidden_states.device.type == "cuda" and hidden_states.dtype == torch.float16
                 and hidden_states.ndim == 3 and hidden_states.shape[0] == 1 and hidden_states.shape[1] == 1
-                and cache_position is not None and cache_position.device.type == "cuda"
-                and cache_position.numel() == 1 and self.head_dim == 128
+                and self.head_dim == 128
                 and self.num_heads == 2 * self.num_kv_heads and cos.dtype == torch.float16
                 and cos.numel() == 128 and sin.numel() == 128 and self.qkv_bias is None)
 
@@ -125,10 +153,14 @@ class OptimizedDecoderLayer(nn.Module):
         if hidden_states.device.type != "cuda":
             raise RuntimeError("OptimizedDecoderLayer runs on a ROCm GPU (got a CPU tensor)")
         kwargs.pop("prefill_static_cache_no_mask", None)
-        if self._decode_ok(hidden_states, position_embeddings, cache_position):
-            kv = self._static_kv(past_key_values, hidden_states.new_empty(1, self.num_kv_heads, 1, self.head_dim))
-            if kv is not None:
-                return self._decode_step(hidden_states, position_embeddings, kv, cache_position.reshape(1))
+        if self._decode_ok(hidden_states, position_embeddings):
+            layer = self._static_layer(past_key_values,
+                                       hidden_states.new_empty(1, self.num_kv_heads, 1, self.head_dim))
+            pos = self._decode_position(layer, cache_position, hidden_states.device) if layer is not None else None
+            if pos is not None:
+                out = self._decode_step(hidden_states, position_embeddings, (layer.keys, layer.values), pos)
+                self._advance_length(layer, pos)
+                return out
         return self._general_forward(hidden_states, position_embeddings, attention_mask, position_ids,
                                      past_key_values, use_cache, cache_position, **kwargs)
 

@@ -137,6 +137,7 @@ ModelDesc._fields_ = [
     ("workspace", c_void_p),
     ("attn_splits", c_int), ("step_mode", c_int), ("batch", c_int),
     ("advance_out_tokens", c_void_p), ("advance_counter", c_void_p), ("advance_max_tokens", c_int),
+    ("argmax_f16_logits", c_int),
 ]
 
 __all__ = ["lib", "check", "ptr", "stream", "call", "QD_F16", "QD_F32", "ModelDesc", "LayerDesc", "EXPORTED",

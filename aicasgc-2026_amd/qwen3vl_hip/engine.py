@@ -91,7 +91,7 @@ class DecodeEngine(_CapturedSteps):
 
     def __init__(self, weights: ModelWeights, capacity: int, device="cuda", attn_splits: int = 0,
                  keep_logits: bool = False, step_mode: str = "auto", steps_per_graph: int = 8,
-                 fuse_advance: bool = True):
+                 fuse_advance: bool = True, argmax_f16_logits: bool = False):
         if not torch.cuda.is_available():
             raise RuntimeError("DecodeEngine needs a ROCm GPU")
         if steps_per_graph < 1:
@@ -147,6 +147,7 @@ class DecodeEngine(_CapturedSteps):
         d.logits_out = self.logits.data_ptr() if self.logits is not None else None
         d.attn_splits = int(attn_splits)
         d.step_mode = self.STEP_MODES[step_mode]
+        d.argmax_f16_logits = int(bool(argmax_f16_logits))
         nbytes = _lib.lib().qd_decode_workspace_bytes(ctypes.byref(d))
         self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
         d.workspace = self.workspace.data_ptr()

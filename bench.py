@@ -20,6 +20,13 @@ on this host's cores); beside it the batch-8 workload (config 4) and configs
 0-2 (one layer step, the five GEMVs, attention at L = 256..8192), each timed on
 cold operands against its roofline with the CPU time of the same call.
 
+The run checks itself and exits non-zero instead of printing a number when a
+check fails: the timed config-3 tokens must match the oracle's golden stream
+(tests/golden/config3_tokens.json) for at least the first 64 (all of them when
+fewer are generated), the persistent step's status word must be clear after the
+timed replays and after the 4096-context run, and the batch-8 step's first
+tokens must equal the oracle's on a copy of the same caches.
+
     python bench.py [--gpus 1] [--steps 250] [--warmup 5]
 """
 
@@ -40,6 +47,7 @@ for _p in (str(REPO), str(REPO / "aicasgc-2026_amd")):
     if _p not in sys.path:
         sys.path.insert(0, _p)
 
+GOLDEN = REPO / "tests" / "golden" / "config3_tokens.json"
 PEAK_HBM_GBPS = 8000.0
 PEAK_FP16_TFLOPS = 2500.0   # dense fp16 MFMA
 WEIGHT_SEED = 3
@@ -67,11 +75,15 @@ def persistent_launch_bytes(context_len: int, shape) -> int:
     return shape.num_layers * (layer_w + kv) + 2 * h + 4 * h
 
 
-def bench_batch8(w, steps: int, warmup: int = 4) -> dict:
+def bench_batch8(w, steps: int, warmup: int = 4, cpu: bool = True) -> dict:
     """Config 4: batch 8, per-sequence valid lengths L_i ~ U[2048, 4096]
     (seeded), random K/V prefixes, greedy steps as HIP-graph replays (4 steps
     per graph; MFMA batch GEMVs, per-sequence split-KV attention with the merge
-    fused in, per-sequence argmax)."""
+    fused in, per-sequence argmax).
+
+    The first step's 8 tokens are checked against the oracle's batch step on a
+    host copy of the same caches (raises on a mismatch); that oracle call is
+    also the CPU baseline's sample."""
     import torch
 
     from qwen3vl_hip import synthetic as syn
@@ -83,6 +95,7 @@ def bench_batch8(w, steps: int, warmup: int = 4) -> dict:
     for k, v in zip(eng.k_caches, eng.v_caches):
         k.normal_()
         v.normal_()
+    host_caches = [(k.cpu(), v.cpu()) for k, v in zip(eng.k_caches, eng.v_caches)]
     tokens = [int(t) for t in syn.randint(4, ("text_ids",), (8,), 0, w.shape.vocab)]
     eng.reserve_tokens(n)
     eng.set_state(tokens, lens, lens)
@@ -99,7 +112,14 @@ def bench_batch8(w, steps: int, warmup: int = 4) -> dict:
     per_step = [roofline_bytes_batch_step([L + warmup + i + 1 for L in lens], w.shape) for i in range(steps)]
     nbytes = sum(per_step) / steps
     gbps = nbytes / (ms * 1e-3) / 1e9
+    first_gpu = eng.out_tokens[0].tolist()
+    final_pos = eng.cache_position.tolist()
+    counter = int(eng.step_counter.item())
     del eng
+    if counter != n or final_pos != [L + n for L in lens]:
+        raise RuntimeError(f"batch8: device positions did not advance {n} steps: counter {counter}, {final_pos}")
+    check = batch8_first_step_check(w, tokens, lens, host_caches, first_gpu)
+    del host_caches
     # GEMV flops on MFMA (2 per weight and sequence; attention runs on the VALU)
     s = w.shape
     gemv_params = s.num_layers * (s.qkv_rows * s.hidden + s.hidden * s.q_size + 3 * s.intermediate * s.hidden) \
@@ -107,6 +127,8 @@ def bench_batch8(w, steps: int, warmup: int = 4) -> dict:
     mfma_tflops = 2 * 8 * gemv_params / (ms * 1e-3) / 1e12
     return {"workload": "config4: 8 sequences, valid KV lengths U[2048,4096] (seeded), greedy, 4 steps per HIP graph",
             "kv_lengths": lens, "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 4),
+            "first_step_tokens_match_oracle": True, "first_step_min_top2_margin": check["min_margin"],
+            "cpu_baseline": check["cpu_baseline"] if cpu else None,
             "tokens_per_s": round(8 * 1000.0 / ms, 1), "step_bytes": int(nbytes), "achieved_GBps": round(gbps, 1),
             "roofline_frac": round(gbps / PEAK_HBM_GBPS, 4),
             "roofline_ms": round(nbytes / (PEAK_HBM_GBPS * 1e9) * 1e3, 4),
@@ -114,36 +136,33 @@ def bench_batch8(w, steps: int, warmup: int = 4) -> dict:
                      "peak_TFLOPs": PEAK_FP16_TFLOPS, "frac": round(mfma_tflops / PEAK_FP16_TFLOPS, 5)}}
 
 
-def cpu_baseline_batch8(weights_gpu, n_steps: int = 2) -> dict:
+def batch8_first_step_check(weights_gpu, tokens, lens, host_caches, gpu_tokens) -> dict:
     """Config 4 on the host: the oracle's batch step (each sequence its own
-    fp32 step on its own cache rows) at the batch-8 KV lengths, random K/V."""
+    fp32 step on its own cache rows) on a copy of the GPU engine's caches taken
+    before its first step.  Its tokens must equal the GPU's first-step tokens
+    (raises otherwise); its time is the batch-8 CPU baseline sample."""
     import torch
 
     from oracle import qwen3vl_oracle as O
-    from qwen3vl_hip import synthetic as syn
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    s = weights_gpu.shape
     f32 = types.SimpleNamespace(
         embed_tokens=weights_gpu.embed_tokens.detach().to("cpu", torch.float32),
         final_norm_weight=weights_gpu.final_norm_weight.detach().to("cpu", torch.float32),
         layers=[{k: v.detach().to("cpu", torch.float32) for k, v in lw.tensors().items()}
                 for lw in weights_gpu.layers])
-    lens = [int(v) for v in syn.batch8_kv_lengths()]
-    cap = max(lens) + n_steps + 1
-    g = torch.Generator().manual_seed(98)
-    caches = [(torch.randn(8, s.num_kv_heads, cap, s.head_dim, generator=g).half(),
-               torch.randn(8, s.num_kv_heads, cap, s.head_dim, generator=g).half()) for _ in range(s.num_layers)]
-    toks, pos, times = [11, 22, 33, 44, 55, 66, 77, 88], list(lens), []
-    for _ in range(n_steps):
-        t0 = time.perf_counter()
-        _, toks = O.decode_step_batch(f32, toks, caches, pos, pos)
-        times.append(time.perf_counter() - t0)
-        pos = [p + 1 for p in pos]
-    return {"value": round(1000.0 * sorted(times)[len(times) // 2], 1), "unit": "ms/step", "cores": cores,
-            "kind": "port",
-            "sample": f"median of {n_steps} batch-8 steps of the oracle's fp32 restatement at the KV lengths above"}
+    t0 = time.perf_counter()
+    logits, toks = O.decode_step_batch(f32, tokens, host_caches, lens, lens)
+    dt = time.perf_counter() - t0
+    margins = [O.top2_margin(row) for row in logits]
+    if list(toks) != list(gpu_tokens):
+        raise RuntimeError(f"batch8 first step: GPU tokens {gpu_tokens} != oracle {list(toks)} "
+                           f"(top-2 margins {margins})")
+    return {"min_margin": round(min(margins), 6),
+            "cpu_baseline": {"value": round(1000.0 * dt, 1), "unit": "ms/step", "cores": cores, "kind": "port",
+                             "sample": "one batch-8 step of the oracle's fp32 restatement at the KV lengths above "
+                                       "(the step whose tokens check the GPU's first step)"}}
 
 
 ROTATE_BYTES = 512 << 20   # cold caches: every call reads a different copy (MALL: 256 MB)
@@ -419,6 +438,18 @@ def main() -> int:
     torch.cuda.synchronize()
     ms = ev0.elapsed_time(ev1) / args.steps
     tokens = [first] + eng.out_tokens[:n_dec].tolist()
+    # the timed run must be a valid one: every hand-off completed, the tokens
+    # are the oracle's (the first 64 identical)
+    if eng.step_mode == "persistent" and eng.status() != 0:
+        log("FAIL: a persistent-step hand-off timed out during the timed replays")
+        return 1
+    gold = json.loads(GOLDEN.read_text())
+    n_chk = min(len(tokens), len(gold["tokens"]))
+    match = next((i for i in range(n_chk) if tokens[i] != gold["tokens"][i]), n_chk)
+    if match < min(64, n_chk):
+        log(f"FAIL: token {match} differs from the oracle's golden stream ({tokens[match]} vs "
+            f"{gold['tokens'][match]})")
+        return 1
     # K/V length read by timed step i (cache position p reads p + 1 rows)
     lens = [prompt.length + args.warmup + i + 1 for i in range(args.steps)]
     step_bytes = sum(roofline_bytes_step(L, shape) for L in lens) / len(lens)
@@ -444,6 +475,12 @@ def main() -> int:
     lens4 = [4096 - half + i + 1 for i in range(args.ctx_steps)]
     bytes4 = sum(roofline_bytes_step(L, shape) for L in lens4) / len(lens4)
     gbps4 = bytes4 / (ms4 * 1e-3) / 1e9
+    if eng4.step_mode == "persistent" and eng4.status() != 0:
+        log("FAIL: a persistent-step hand-off timed out in the 4096-context run")
+        return 1
+    if int(eng4.step_counter.item()) != args.ctx_steps:
+        log("FAIL: the 4096-context run did not advance every step")
+        return 1
     del eng4
     log(f"ctx4096: {ms4:.4f} ms/token, {gbps4:.1f} GB/s")
 
@@ -506,7 +543,7 @@ def main() -> int:
     # ---- config 4: 8 sequences, ragged contexts L_i ~ U[2048, 4096]
     b8 = None
     if args.batch8_steps > 0:
-        b8 = bench_batch8(w, args.batch8_steps)
+        b8 = bench_batch8(w, args.batch8_steps, cpu=not args.no_cpu)
         log(f"batch8: {b8['ms_per_step']:.4f} ms/step, {b8['tokens_per_s']:.0f} tok/s, {b8['achieved_GBps']:.1f} GB/s")
 
     # ---- configs 0-2 against their rooflines (cold operands), CPU beside them
@@ -550,7 +587,6 @@ def main() -> int:
         cpu = cpu_baseline(w, prompt.length, args.cpu_steps)
         log(f"cpu baseline {cpu['value']} ms/token on {cpu['cores']} cores")
         if b8 is not None:
-            b8["cpu_baseline"] = cpu_baseline_batch8(w)
             log(f"cpu baseline batch8 {b8['cpu_baseline']['value']} ms/step")
 
     out = {
@@ -593,6 +629,8 @@ def main() -> int:
         "cpu_baseline": cpu,
         "device_copy_GBps": round(copy_gbps, 1),
         "tokens_head": tokens[:8],
+        "tokens_checked": n_chk,
+        "tokens_match_golden_prefix": match,
         "batch8": b8,
         "configs012": c012,
     }

@@ -250,6 +250,13 @@ typedef struct qd_model_desc {
   int64_t* advance_out_tokens;
   int64_t* advance_counter;
   int advance_max_tokens;
+  /* Batch-1 argmax over the logits rounded to fp16, the first index winning
+   * among equal fp16 values: the reference's FastLmHead returns fp16 logits
+   * and takes torch.argmax over them (evaluation_wrapper.py:952, :1233-1238).
+   * 0 (default) compares the fp32 logits, the fp32 math the parity criterion
+   * is stated in; the two differ only where the top logits round to one fp16
+   * value. */
+  int argmax_f16_logits;
 } qd_model_desc;
 
 /* How qd_decode_step runs the 28 layers.

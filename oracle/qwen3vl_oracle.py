@@ -313,7 +313,8 @@ def embed_prompt(weights, prompt, dtype=torch.float32) -> torch.Tensor:
 
 def greedy_generate(weights, prompt, n_tokens: int, capacity: int, shape: OracleShape = SHAPE,
                     dtype=torch.float32, caches=None, first_token: int | None = None,
-                    start_position: int | None = None, log=None):
+                    start_position: int | None = None, log=None, logits_out: list | None = None,
+                    cache_dtype=torch.float16, rope_delta: int | None = None):
     """Greedy decoding after a prefill (evaluation_wrapper.py:149-315 semantics).
 
     Returns (tokens [n_tokens], margins [n_tokens]) where tokens[0] is the
@@ -321,17 +322,24 @@ def greedy_generate(weights, prompt, n_tokens: int, capacity: int, shape: Oracle
     step at cache position p uses rope position p + rope_delta on all three
     streams (evaluation_wrapper.py:507-511, :954-960).  When ``caches``,
     ``first_token`` and ``start_position`` are given the prefill is skipped and
-    decoding continues from that state.
+    decoding continues from that state.  ``logits_out``, when given, receives
+    the logits of every generated token (prefill first).  The static cache is
+    fp16 as the reference's (``cache_dtype`` changes it for comparisons with
+    an fp32 cache); ``rope_delta`` overrides the prompt's (tests plant a wrong
+    one to show the checks see it).
     """
+    delta = prompt.rope_delta if rope_delta is None else int(rope_delta)
     tokens, margins = [], []
     if caches is None:
-        caches = [(torch.zeros(1, shape.num_kv_heads, capacity, shape.head_dim, dtype=torch.float16),
-                   torch.zeros(1, shape.num_kv_heads, capacity, shape.head_dim, dtype=torch.float16))
+        caches = [(torch.zeros(1, shape.num_kv_heads, capacity, shape.head_dim, dtype=cache_dtype),
+                   torch.zeros(1, shape.num_kv_heads, capacity, shape.head_dim, dtype=cache_dtype))
                   for _ in weights.layers]
         h_last = prefill(weights, embed_prompt(weights, prompt, dtype), prompt.position_ids, caches, shape, dtype)
         logits, tok = lm_head_argmax(h_last, weights.final_norm_weight, weights.embed_tokens, shape.rms_eps, dtype)
         tokens.append(tok)
         margins.append(top2_margin(logits))
+        if logits_out is not None:
+            logits_out.append(logits)
         pos = prompt.length
     else:
         tokens.append(int(first_token))
@@ -339,7 +347,7 @@ def greedy_generate(weights, prompt, n_tokens: int, capacity: int, shape: Oracle
         pos = int(start_position)
     inv_cache = {}
     while len(tokens) < n_tokens:
-        rp = pos + prompt.rope_delta
+        rp = pos + delta
         if rp not in inv_cache:
             cos, sin = mrope_cos_sin(torch.full((3, 1), rp, dtype=torch.int64), shape, dtype)
             inv_cache[rp] = (cos[0], sin[0])
@@ -351,6 +359,8 @@ def greedy_generate(weights, prompt, n_tokens: int, capacity: int, shape: Oracle
         logits, tok = lm_head_argmax(h, weights.final_norm_weight, weights.embed_tokens, shape.rms_eps, dtype)
         tokens.append(tok)
         margins.append(top2_margin(logits))
+        if logits_out is not None:
+            logits_out.append(logits)
         if log is not None:
             log(len(tokens), tok, margins[-1])
         pos += 1

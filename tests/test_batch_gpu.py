@@ -222,3 +222,85 @@ def test_batch_full_model_two_steps(cuda):
     assert_close_rel(gpu_logits, logits, what="28-layer batch logits (second step)")
     print(f"gpu {got}\noracle {ref}", flush=True)
     assert got == ref
+
+
+def _fill_caches_device(eng, positions, seed):
+    """Random K/V prefixes [0, p) drawn on the device (seeded), stale rows past
+    them set to +-3 (an over-read changes the result); returns host copies."""
+    gen = torch.Generator(device=eng.device).manual_seed(seed)
+    caches = []
+    for kc, vc in zip(eng.k_caches, eng.v_caches):
+        kc.fill_(3.0)
+        vc.fill_(-3.0)
+        for b, p in enumerate(positions):
+            kc[b, :, :p].normal_(generator=gen)
+            vc[b, :, :p].normal_(generator=gen)
+        caches.append((kc.cpu(), vc.cpu()))
+    return caches
+
+
+def test_batch_two_layers_config4_lengths(cuda, two_layer_weights):
+    """Config-4 KV lengths (the seeded U[2048, 4096] draw, 2273..4067) on a
+    2-layer model: 8 splits per kv head of up to 509 rows, so every split walks
+    four batches of K/V rows (two loop trips), each sequence at its own
+    position.  Two graph-replayed steps: tokens of both, the second step's
+    logits, and the K/V rows both steps wrote."""
+    from qwen3vl_hip import synthetic as syn
+    from qwen3vl_hip.engine import BatchDecodeEngine
+
+    w = two_layer_weights
+    positions = [int(v) for v in syn.batch8_kv_lengths()]
+    assert min(positions) >= 2048 and max(positions) <= 4096
+    tokens = [17, 4000, 8191, 2, 555, 1234, 6000, 42]
+    cap = max(positions) + 4
+    eng = BatchDecodeEngine(w, batch=8, capacity=cap, keep_logits=True)
+    caches = _fill_caches_device(eng, positions, 41)
+    got = eng.decode(tokens, positions, positions, 2, use_graph=True)
+    ref_caches = [(k.clone(), v.clone()) for k, v in caches]
+    cur, pos, ref, logits = list(tokens), list(positions), [], None
+    shape = O.OracleShape(num_layers=2, vocab=VOCAB)
+    for _ in range(2):
+        logits, cur = O.decode_step_batch(w, cur, ref_caches, pos, pos, shape=shape)
+        ref.append(list(cur))
+        pos = [p + 1 for p in pos]
+    assert_close_rel(eng.logits.cpu(), logits, what="2-layer batch logits at config-4 lengths (second step)")
+    for li in range(2):
+        for b, p in enumerate(positions):
+            assert_close_rel(eng.k_caches[li][b, :, p:p + 2].cpu(), ref_caches[li][0][b, :, p:p + 2].float(),
+                             what=f"K rows layer {li} seq {b}")
+            assert torch.equal(eng.k_caches[li][b, :, p + 2:].cpu(), caches[li][0][b, :, p + 2:])
+    print(f"gpu {got}\noracle {ref}", flush=True)
+    assert got == ref
+
+
+def test_batch_full_model_config4_lengths(cuda):
+    """Config 4 at its own workload: the full 28-layer model, 8 sequences at the
+    seeded config-4 KV lengths (2273..4067) with random K/V prefixes, two
+    graph-replayed steps against the oracle's batch step (which is pinned per
+    sequence against transformers): both steps' tokens and the second step's
+    logits (bar 2e-3 * max|ref|)."""
+    from qwen3vl_hip import synthetic as syn
+    from qwen3vl_hip.engine import BatchDecodeEngine
+
+    w = syn.model_weights(3, device=cuda)
+    positions = [int(v) for v in syn.batch8_kv_lengths()]
+    tokens = [int(t) for t in syn.randint(4, ("text_ids",), (8,), 0, w.shape.vocab)]
+    eng = BatchDecodeEngine(w, batch=8, capacity=max(positions) + 4, keep_logits=True)
+    caches = _fill_caches_device(eng, positions, 43)
+    print("case config4 28 layers: GPU steps", flush=True)
+    got = eng.decode(tokens, positions, positions, 2, use_graph=True)
+    gpu_logits = eng.logits.cpu()
+    del eng
+    f32 = types.SimpleNamespace(
+        embed_tokens=w.embed_tokens.float().cpu(), final_norm_weight=w.final_norm_weight.float().cpu(),
+        layers=[{k: v.float().cpu() for k, v in lw.tensors().items()} for lw in w.layers])
+    cur, pos, ref, logits, margins = list(tokens), list(positions), [], None, []
+    for step in range(2):
+        print(f"case config4 28 layers: oracle step {step}", flush=True)
+        logits, cur = O.decode_step_batch(f32, cur, caches, pos, pos)
+        ref.append(list(cur))
+        margins.append([round(O.top2_margin(r), 5) for r in logits])
+        pos = [p + 1 for p in pos]
+    print(f"gpu {got}\noracle {ref}\nmargins {margins}", flush=True)
+    assert_close_rel(gpu_logits, logits, what="28-layer batch logits at config-4 lengths (second step)")
+    assert got == ref

@@ -207,3 +207,35 @@ def test_bad_inputs_raise(cuda):
         g.nosplit_matvec_half(torch.randn(1, 2, 2048, device=cuda).half(), w, None)
     with pytest.raises(RuntimeError):
         g.splitk_matvec(x.half(), w, None, 3)  # 2048 / 3 is not an integer slice
+
+
+@pytest.mark.parametrize("f16", [False, True])
+def test_lm_head_argmax_logits_within_one_fp16_ulp(cuda, f16):
+    """Two logits that differ by less than one fp16 ulp, the larger fp32 value
+    at the higher index.  Default (fp32 comparison, the oracle's argmax): the
+    higher index.  argmax_f16_logits (the reference's FastLmHead returns fp16
+    logits and takes torch.argmax, evaluation_wrapper.py:952, :1233-1238): the
+    two round to the same fp16 value and the first index wins.  The fp16 logits
+    written out are equal either way."""
+    from qwen3vl_hip import synthetic as syn
+    from qwen3vl_hip.config import Qwen3VLTextShape
+    from qwen3vl_hip.engine import DecodeEngine
+
+    w = syn.model_weights(26, shape=Qwen3VLTextShape(num_layers=1, vocab=4096))
+    emb = torch.zeros(4096, 2048, dtype=torch.float16)
+    emb[3, 0] = 1.0
+    emb[7, 0] = 1.0
+    emb[7, 1] = 2.0 ** -12          # logit 7 = logit 3 * (1 + 2^-12): below half an fp16 ulp at 1.0
+    w.embed_tokens = emb
+    w.final_norm_weight = torch.ones(2048, dtype=torch.float16)
+    eng = DecodeEngine(w, capacity=64, step_mode="chain", keep_logits=True, argmax_f16_logits=f16)
+    eng.buffers()["x"].fill_(1.0)
+    eng.run_phases(["lm_head"], n_layers=0)
+    torch.cuda.synchronize()
+    tok = int(eng.token.item())
+    assert eng.logits[3].item() == eng.logits[7].item() == 1.0
+    _, tok_oracle = O.lm_head_argmax(torch.ones(2048), w.final_norm_weight, emb, 1e-6)
+    assert tok_oracle == 7
+    assert tok == (3 if f16 else 7)
+    # the same through torch's own argmax over the fp16 logits (reference semantics)
+    assert int(torch.argmax(eng.logits)) == 3

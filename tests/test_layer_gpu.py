@@ -169,3 +169,52 @@ def test_engine_one_layer_step_config0(cuda):
     assert_close_rel(eng.k_caches[0][0, :, 512].cpu(), kc_ref[0, :, 512].float(), what="engine K write")
     print(f"engine token {toks[0]} oracle {tok} margin {O.top2_margin(logits):.4g}", flush=True)
     assert toks[0] == tok
+
+
+@pytest.mark.parametrize("step_mode,splits,pos,poison", [
+    ("chain", 0, 512, "nan"),     # 10 splits of 52 rows: the split holding pos clamps to the poisoned row
+    ("chain", 2, 600, "inf"),     # 301 rows per split: three trips of the K/V loop, the new row in the third
+    ("chain", 2, 600, None),
+    ("chain", 1, 700, "nan"),     # one split of 701 rows (six loop trips)
+    ("persistent", 0, 600, "nan"),
+])
+def test_engine_step_long_splits_and_poisoned_new_row(cuda, step_mode, splits, pos, poison):
+    """Native step (1 layer) whose attention splits walk several batches of K/V
+    rows, with the cache row of the new position (and every row after it)
+    holding inf or NaN before the step, as a reused cache can.  The step must
+    write the new row and never let the stale values reach the output: logits,
+    token and the written K/V row against the oracle, and the rows after the
+    new one untouched."""
+    from qwen3vl_hip import synthetic as syn
+    from qwen3vl_hip.engine import DecodeEngine
+
+    w = syn.model_weights(0, num_layers=1)
+    cap = 1024
+    eng = DecodeEngine(w, capacity=cap, keep_logits=True, attn_splits=splits, step_mode=step_mode)
+    assert eng.step_mode == step_mode
+    kc = syn.normal(7, ("k_cache", pos), (1, 8, cap, 128))
+    vc = syn.normal(7, ("v_cache", pos), (1, 8, cap, 128))
+    if poison is not None:
+        bad = float(poison)
+        kc[:, :, pos:] = bad
+        vc[:, :, pos:] = bad
+    eng.k_caches[0].copy_(kc)
+    eng.v_caches[0].copy_(vc)
+    token = 777
+    print(f"case {step_mode} splits={splits} pos={pos} poison={poison}", flush=True)
+    toks = eng.decode(token, pos, 0, 1, use_graph=False)
+    kc_ref, vc_ref = kc.clone(), vc.clone()
+    cos, sin = O.mrope_cos_sin(torch.full((3, 1), pos, dtype=torch.int64))
+    h = O.decode_layer(w.layers[0].tensors(), w.embed_tokens[token], kc_ref, vc_ref, pos, cos[0], sin[0])
+    logits, tok = O.lm_head_argmax(h, w.final_norm_weight, w.embed_tokens, 1e-6)
+    assert_close_rel(eng.logits.cpu(), logits, what=f"logits ({step_mode}, splits {splits}, pos {pos})")
+    assert toks[0] == tok
+    assert_close_rel(eng.k_caches[0][0, :, pos].cpu(), kc_ref[0, :, pos].float(), what="K row written")
+    assert torch.equal(eng.v_caches[0][0, :, pos].cpu(), vc_ref[0, :, pos])
+    if poison == "nan":   # NaN != NaN: check the rows are still all NaN
+        assert torch.isnan(eng.k_caches[0][0, :, pos + 1:]).all() and torch.isnan(eng.v_caches[0][0, :, pos + 1:]).all()
+    else:
+        assert torch.equal(eng.k_caches[0][0, :, pos + 1:].cpu(), kc[0, :, pos + 1:])
+        assert torch.equal(eng.v_caches[0][0, :, pos + 1:].cpu(), vc[0, :, pos + 1:])
+    if step_mode == "persistent":
+        assert eng.status() == 0

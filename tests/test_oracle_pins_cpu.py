@@ -290,6 +290,122 @@ def test_oracle_prefill_and_decode_match_transformers_text_model():
         assert tok == int(torch.argmax(lhf))
 
 
+def _hf_tiny_vl_model(w, shape):
+    """transformers' full Qwen3-VL model (tiny vision tower, spatial merge 2) with
+    the text decoder and the tied lm_head set to ``w``: its get_rope_index and
+    compute_3d_position_ids are the reference's position rules (the reference
+    decodes through this model, evaluation_wrapper.py:206-209, :941-950)."""
+    from transformers.models.qwen3_vl.configuration_qwen3_vl import Qwen3VLConfig
+    from transformers.models.qwen3_vl.modeling_qwen3_vl import Qwen3VLForConditionalGeneration
+
+    text = dict(hidden_size=shape.hidden, intermediate_size=shape.intermediate, num_attention_heads=shape.num_heads,
+                num_key_value_heads=shape.num_kv_heads, head_dim=shape.head_dim, num_hidden_layers=shape.num_layers,
+                vocab_size=shape.vocab, rms_norm_eps=shape.rms_eps,
+                rope_parameters={"rope_type": "default", "rope_theta": shape.rope_theta,
+                                 "mrope_section": list(shape.mrope_section)})
+    vision = dict(depth=1, hidden_size=32, intermediate_size=64, num_heads=2, out_hidden_size=shape.hidden,
+                  spatial_merge_size=2, patch_size=16, temporal_patch_size=2, deepstack_visual_indexes=[])
+    cfg = Qwen3VLConfig(text_config=text, vision_config=vision, image_token_id=shape.vocab - 7,
+                        video_token_id=shape.vocab - 6, vision_start_token_id=shape.vocab - 5,
+                        tie_word_embeddings=True)
+    cfg.text_config._attn_implementation = "sdpa"
+    m = Qwen3VLForConditionalGeneration(cfg).float().eval()
+    lm = _hf_tiny_model(w, shape)
+    m.model.language_model.load_state_dict(lm.state_dict())
+    with torch.no_grad():
+        m.lm_head.weight.copy_(w.embed_tokens.double())
+    return m
+
+
+@pytest.mark.parametrize("grid", [(1, 3, 4, 5), (1, 24, 32, 256), (3, 2, 2, 5), (5, 2, 3, 4), (2, 4, 3, 1)])
+def test_multimodal_prompt_positions_match_transformers_get_rope_index(grid):
+    """The synthetic prompt's [3, S] M-RoPE positions and rope_delta equal
+    transformers' Qwen3VLModel.get_rope_index (HF:932-1023) for the same token
+    layout: one image (LLM grid t x h x w after the 2x2 spatial merge, so
+    image_grid_thw = [t, 2h, 2w]) followed by text, with image placeholder ids
+    and mm_token_type_ids as the processor emits them.  Covers the config-3
+    grid 1x24x32, the tiny grid, and temporal grids t > 1 (one where t exceeds
+    h and w, so a rule that advances text past max(t, h, w) would differ)."""
+    from qwen3vl_hip import synthetic as syn
+
+    t, h, w_, n_text = grid
+    shape, _ = _tiny()
+    weights = syn.model_weights(16, shape, num_layers=1)
+    model = _hf_tiny_vl_model(weights, dataclasses_replace(shape, num_layers=1))
+    prompt = syn.multimodal_prompt(16, grid_t=t, grid_h=h, grid_w=w_, n_text=n_text, shape=shape)
+    n_vis = t * h * w_
+    ids = torch.cat([torch.full((n_vis,), model.config.image_token_id), prompt.text_ids]).view(1, -1)
+    types = torch.cat([torch.ones(n_vis, dtype=torch.int32), torch.zeros(n_text, dtype=torch.int32)]).view(1, -1)
+    pos, delta = model.model.get_rope_index(ids, types, image_grid_thw=torch.tensor([[t, 2 * h, 2 * w_]]))
+    assert torch.equal(prompt.position_ids, pos[:, 0, :])
+    assert prompt.rope_delta == int(delta)
+
+
+def dataclasses_replace(obj, **kw):
+    import dataclasses
+
+    return dataclasses.replace(obj, **kw)
+
+
+def test_greedy_generate_matches_transformers_generation_loop():
+    """The oracle's greedy loop against transformers' own: prefill the
+    multimodal-shaped prompt through Qwen3VLForConditionalGeneration with the
+    positions of its get_rope_index (vision rows as inputs_embeds, text rows
+    through its embedding table), then decode token by token passing only
+    input_ids and the cache, so transformers derives every decode position
+    itself from the cached length and its stored rope_deltas
+    (compute_3d_position_ids, HF:1098-1145).  Tokens must be identical and
+    logits equal at fp32 summation-order level for every step; a wrong rope
+    delta, a position off by one or a stale cache row changes the logits far
+    beyond that bar.  transformers' cache here is fp32, so the oracle runs with
+    an fp32 cache for the tight comparison; with its default fp16 cache (the
+    reference's StaticCache dtype) the tokens must still agree.  A rope delta
+    planted one position off in the oracle must miss the bar by far."""
+    from transformers.cache_utils import DynamicCache
+
+    from qwen3vl_hip import synthetic as syn
+
+    shape, oshape = _tiny()
+    w = syn.model_weights(17, shape)
+    prompt = syn.multimodal_prompt(17, grid_h=3, grid_w=4, n_text=5, shape=shape)
+    assert prompt.rope_delta != 0
+    n = 10
+    logits_o, logits_16, logits_bad = [], [], []
+    toks, _, _ = O.greedy_generate(w, prompt, n, prompt.length + n, oshape, logits_out=logits_o,
+                                   cache_dtype=torch.float32)
+    toks16, _, _ = O.greedy_generate(w, prompt, n, prompt.length + n, oshape, logits_out=logits_16)
+    O.greedy_generate(w, prompt, 3, prompt.length + n, oshape, logits_out=logits_bad, cache_dtype=torch.float32,
+                      rope_delta=prompt.rope_delta + 1)
+
+    model = _hf_tiny_vl_model(w, shape)
+    n_vis = prompt.vision_embeds.shape[0]
+    ids = torch.cat([torch.full((n_vis,), model.config.image_token_id), prompt.text_ids]).view(1, -1)
+    types = torch.cat([torch.ones(n_vis, dtype=torch.int32), torch.zeros(prompt.text_ids.numel(), dtype=torch.int32)])
+    emb = O.embed_prompt(w, prompt, torch.float32)[None]
+    with torch.no_grad():
+        pos, delta = model.model.get_rope_index(ids, types.view(1, -1), image_grid_thw=torch.tensor([[1, 6, 8]]))
+        model.model.rope_deltas = delta
+        cache = DynamicCache(config=model.config.text_config)
+        out = model(inputs_embeds=emb, position_ids=pos, past_key_values=cache, use_cache=True)
+        logits_hf = [out.logits[0, -1]]
+        tok = int(torch.argmax(logits_hf[-1]))
+        toks_hf = [tok]
+        for _ in range(n - 1):
+            out = model(input_ids=torch.tensor([[tok]]), past_key_values=cache, use_cache=True)
+            logits_hf.append(out.logits[0, -1])
+            tok = int(torch.argmax(logits_hf[-1]))
+            toks_hf.append(tok)
+    assert toks == toks_hf and toks16 == toks_hf
+    for i, (a, b) in enumerate(zip(logits_o, logits_hf)):
+        assert (a - b).abs().max() < 2e-5 * b.abs().max(), f"step {i}"
+    for i, (a, b) in enumerate(zip(logits_16, logits_hf)):
+        assert (a - b).abs().max() < 2e-3 * b.abs().max(), f"fp16 cache, step {i}"
+    # the planted off-by-one delta: identical prefill, decode steps far off
+    assert (logits_bad[0] - logits_hf[0]).abs().max() < 2e-5 * logits_hf[0].abs().max()
+    for a, b in zip(logits_bad[1:], logits_hf[1:3]):
+        assert (a - b).abs().max() > 100 * 2e-5 * b.abs().max()
+
+
 def test_greedy_generate_matches_step_by_step_decoding():
     from qwen3vl_hip import synthetic as syn
 
