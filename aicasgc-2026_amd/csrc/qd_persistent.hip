@@ -42,6 +42,24 @@
 
 namespace qd {
 
+// Phase timestamps (library built with -DQD_TRACE only): wave 0 of every
+// workgroup records the 100 MHz real-time clock at fixed points of each layer
+// of the last launch; qd_persistent_trace_read copies them to the host.
+constexpr int kTraceLayers = 32, kTraceEvents = 16;
+#ifdef QD_TRACE
+__device__ unsigned long long qd_trace_stamps[kPersistBlocks * kTraceLayers * kTraceEvents];
+#define QD_TRACE_AT(l, e)                                                                         \
+  do {                                                                                           \
+    if (!STREAM && threadIdx.x == 0)                                                             \
+      qd_trace_stamps[((size_t)blockIdx.x * kTraceLayers + (l)) * kTraceEvents + (e)] =          \
+          __builtin_amdgcn_s_memrealtime();                                                      \
+  } while (0)
+#else
+#define QD_TRACE_AT(l, e) \
+  do {                    \
+  } while (0)
+#endif
+
 namespace {
 
 constexpr int H = kPersistHidden, HQ = kPersistHeads, HKV = kPersistKvHeads, D = kPersistHeadDim,
@@ -420,6 +438,7 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
     u32x4 wd[1][12];              // W_down row gw
 
     // ================================================================ QKV
+    QD_TRACE_AT(l, 0);
     QD_FRESH_LANE();
     if (l == 0) {
       long tok = a.token[0];
@@ -430,6 +449,7 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
       gather4<H / (4 * NA * kWave), NA * kWave>(r_x, s_x, (unsigned)tid, par ^ 1u, sp);
     }
     __syncthreads();
+    QD_TRACE_AT(l, 1);
     QD_FRESH_LANE();
     {
       float y[2];
@@ -437,6 +457,7 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
       if (lane == 0) put2(a.qkv_t + 2 * gw, par, y[0], y[1]);
       if (!streamer) puts_done();
     }
+    QD_TRACE_AT(l, 2);
     QD_FRESH_LANE();
     if (streamer) issue_gu(Lw, wgu);
 
@@ -453,6 +474,7 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
       *reinterpret_cast<f32x4*>(&s_raw[0][0] + tid * 4) = values_of(v[0]);
     }
     __syncthreads();
+    QD_TRACE_AT(l, 3);
     if (w < 4) {
       const int j = lane;
       const float x0 = s_raw[w][j], x1 = s_raw[w][j + 64];
@@ -551,6 +573,7 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
         }
       }
     }
+    QD_TRACE_AT(l, 4);
     QD_FRESH_LANE();
     if (streamer) issue_wd(Lw, wd);
     __syncthreads();
@@ -579,6 +602,7 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
     QD_FRESH_LANE();
     if (poller) {
       puts_done();
+      QD_TRACE_AT(l, 5);
       // lanes 0..31: LSE of split `lane`; every lane: dims (lane / 32) * 4 .. +4 of split lane % 32
       const int s = lane % NS;
       const int k0 = (lane / NS) * 4;
@@ -605,6 +629,7 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
       }
       puts_done();
       gather4<H / (4 * kWave), kWave>(r_att, s_att, (unsigned)lane, par, sp);
+      QD_TRACE_AT(l, 6);
     }
     // waves 1-3 right after the partials, wave 0 after its two polls
     QD_FRESH_LANE();
@@ -612,6 +637,7 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
     __syncthreads();
 
     // ================================================================ O_PROJ
+    QD_TRACE_AT(l, 7);
     QD_FRESH_LANE();
     {
       float y[1];
@@ -619,11 +645,13 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
       if (lane == 0) put(a.r_t + gw, par, y[0] + s_x[gw]);
       if (!streamer) puts_done();
     }
+    QD_TRACE_AT(l, 8);
 
     // ================================================================ GATE_UP
     QD_FRESH_LANE();
     if (!streamer) gather4<H / (4 * NA * kWave), NA * kWave>(r_r, s_r, (unsigned)tid, par, sp);
     __syncthreads();
+    QD_TRACE_AT(l, 9);
     QD_FRESH_LANE();
     u32x4 gi_next, gp_next;
     if (!streamer) {
@@ -643,6 +671,7 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
       }
       if (!streamer) puts_done();
     }
+    QD_TRACE_AT(l, 10);
     QD_FRESH_LANE();
     if (streamer) {
       issue_qkv(Ln, rs_n);
@@ -653,6 +682,7 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
     QD_FRESH_LANE();
     if (!streamer) gather4<I / (4 * NA * kWave), NA * kWave>(r_hid, s_h, (unsigned)tid, par, sp);
     __syncthreads();
+    QD_TRACE_AT(l, 11);
     QD_FRESH_LANE();
     if (!streamer) {
       // every wave finished this layer's norms before the barrier above
@@ -670,6 +700,7 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
       }
       if (!streamer) {
         puts_done();
+        QD_TRACE_AT(l, 12);
         // the next layer's K/V rows and W_o row: in flight across the x hand-off
         issue_kvwo(Ln, rs_n, tl_n);
       }
@@ -731,6 +762,31 @@ __global__ __launch_bounds__(512) void decode_persistent_kernel(const PersistArg
 int decode_persistent_launch(const PersistArgs& a, hipStream_t s) {
   hipLaunchKernelGGL(decode_persistent_kernel, dim3(NB), dim3(NW * kWave), 0, s, a);
   return qd_host::launch_status("decode_persistent_kernel");
+}
+
+extern "C" int qd_persistent_trace_read(uint64_t* dst, size_t n, int* dims) {
+#ifdef QD_TRACE
+  if (dims != nullptr) {
+    dims[0] = kPersistBlocks;
+    dims[1] = kTraceLayers;
+    dims[2] = kTraceEvents;
+  }
+  const size_t total = (size_t)kPersistBlocks * kTraceLayers * kTraceEvents;
+  if (dst == nullptr) return QD_OK;
+  const hipError_t e = hipMemcpyFromSymbol(dst, HIP_SYMBOL(qd_trace_stamps),
+                                           (n < total ? n : total) * sizeof(uint64_t), 0, hipMemcpyDeviceToHost);
+  if (e != hipSuccess) {
+    qd_host::set_error("trace read failed: %s", hipGetErrorString(e));
+    return (int)e;
+  }
+  return QD_OK;
+#else
+  (void)dst;
+  (void)n;
+  (void)dims;
+  qd_host::set_error("this library was built without QD_TRACE (build the traced variant)");
+  return QD_ERR_ARG;
+#endif
 }
 
 int decode_persistent_check_device(char* why, size_t why_len) {

@@ -17,6 +17,7 @@ import torch
 
 PKG_ROOT = Path(__file__).resolve().parent.parent
 LIB_PATH = Path(os.environ.get("QD_LIB_PATH", PKG_ROOT / "libqwen3vl_decode.so"))
+TRACE_LIB_PATH = PKG_ROOT / "libqwen3vl_decode_trace.so"   # -DQD_TRACE build (phase timestamps)
 
 QD_F16 = 0
 QD_F32 = 1
@@ -66,6 +67,7 @@ _SIGS = {
     "qd_decode_step_mode": (c_int, [P]),
     "qd_decode_layers_persistent": (c_int, [P, P]),
     "qd_decode_status": (c_int, [P, POINTER(ctypes.c_uint), c_int]),
+    "qd_persistent_trace_read": (c_int, [P, c_size_t, POINTER(c_int)]),
     "qd_batch_gemv_workspace_bytes": (ctypes.c_size_t, [c_long, c_long]),
     "qd_batch_gemv": (c_int, [P, c_long, P, c_float, P, c_long, c_long, c_long, c_long, P, c_long, P, c_long, c_int,
                               c_int, P, ctypes.c_size_t, P]),

@@ -19,6 +19,7 @@ PKG_ROOT = Path(__file__).resolve().parent.parent          # aicasgc-2026_amd/
 CSRC = PKG_ROOT / "csrc"
 LIB_NAME = "libqwen3vl_decode.so"
 LIB_PATH = PKG_ROOT / LIB_NAME
+TRACE_LIB_PATH = PKG_ROOT / "libqwen3vl_decode_trace.so"   # same sources with -DQD_TRACE
 SOURCES = ["qd_gemv.hip", "qd_attention.hip", "qd_small_ops.hip", "qd_persistent.hip", "qd_batch.hip", "qd_capi.hip"]
 ARCH = os.environ.get("QD_OFFLOAD_ARCH", "gfx950")
 
@@ -43,10 +44,13 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every HIP source into LIB_PATH (always recompiles)."""
-    tmp = LIB_PATH.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-I", str(PKG_ROOT.parent / "include"),
+def build(verbose: bool = False, trace: bool = False) -> Path:
+    """Compile every HIP source into LIB_PATH (always recompiles).  With
+    ``trace`` the persistent step records its phase timestamps
+    (-DQD_TRACE) and the library goes to TRACE_LIB_PATH instead."""
+    out = TRACE_LIB_PATH if trace else LIB_PATH
+    tmp = out.with_suffix(".so.tmp")
+    cmd = [hipcc(), *HIPCC_FLAGS, *(["-DQD_TRACE"] if trace else []), "-I", str(PKG_ROOT.parent / "include"),
            *[str(CSRC / s) for s in SOURCES], "-o", str(tmp)]
     if verbose:
         print(" ".join(cmd), flush=True)
@@ -55,9 +59,9 @@ def build(verbose: bool = False) -> Path:
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stdout}\n{res.stderr}")
     if verbose and res.stderr.strip():
         print(res.stderr, file=sys.stderr)
-    os.replace(tmp, LIB_PATH)
-    return LIB_PATH
+    os.replace(tmp, out)
+    return out
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    print(build(verbose=True, trace="--trace" in sys.argv))

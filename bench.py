@@ -325,6 +325,25 @@ def bench_configs012(w, cpu: bool, reps: int = 5) -> dict:
     return out
 
 
+def phase_trace(contexts) -> list:
+    """Per-link timeline of the persistent step (qwen3vl_hip.phase_trace) in a
+    child process that loads the traced library, so this process's numbers come
+    from the regular one."""
+    import subprocess
+
+    from qwen3vl_hip import _lib
+
+    if not _lib.TRACE_LIB_PATH.exists():
+        raise RuntimeError(f"{_lib.TRACE_LIB_PATH} is not built (__graft_entry__.build() makes it)")
+    env = dict(os.environ, QD_LIB_PATH=str(_lib.TRACE_LIB_PATH),
+               PYTHONPATH=os.pathsep.join([str(REPO / "aicasgc-2026_amd"), os.environ.get("PYTHONPATH", "")]))
+    cmd = [sys.executable, "-u", "-m", "qwen3vl_hip.phase_trace"] + [a for c in contexts for a in ("--ctx", str(c))]
+    r = subprocess.run(cmd, env=env, stdout=subprocess.PIPE, text=True, timeout=600)
+    if r.returncode != 0:
+        raise RuntimeError(f"phase trace failed with status {r.returncode}")
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
 def _cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -397,6 +416,9 @@ def main() -> int:
                     help="timed steps of the batch-8 workload (config 4); 0 skips it")
     ap.add_argument("--no-configs012", action="store_true",
                     help="skip configs 0-2 (one layer, the GEMVs, attention) against their rooflines")
+    ap.add_argument("--phase-trace", type=int, action="append", metavar="CTX",
+                    help="also report the persistent step's per-link timeline at this context (repeatable), from "
+                         "the -DQD_TRACE library run in a child process (qwen3vl_hip.phase_trace)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -581,6 +603,11 @@ def main() -> int:
         except (ValueError, OSError):
             traffic = None
 
+    traced = None
+    if args.phase_trace:
+        log(f"phase trace at contexts {args.phase_trace} ...")
+        traced = phase_trace(args.phase_trace)
+
     cpu = None
     if not args.no_cpu:
         log("cpu baseline ...")
@@ -633,6 +660,7 @@ def main() -> int:
         "tokens_match_golden_prefix": match,
         "batch8": b8,
         "configs012": c012,
+        "phase_trace": traced,
     }
     print(json.dumps(out), flush=True)
     return 0

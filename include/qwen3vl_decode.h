@@ -321,6 +321,21 @@ int qd_decode_step_mode(const qd_model_desc* d);
  * 28, optimized_layer.py:108-469). */
 int qd_decode_layers_persistent(const qd_model_desc* d, void* stream);
 
+/* Phase timeline of the persistent step, for profiling.  A library built with
+ * -DQD_TRACE (libqwen3vl_decode_trace.so, made by the package's build step
+ * next to the main library) has wave 0 of every workgroup record the 100 MHz
+ * real-time clock at 13 points of every layer of each launch (events 0..12:
+ * layer start, x gathered, qkv rows stored, qkv gathered, attention loop done,
+ * split partials stored, merged output gathered, o_proj start, r rows stored, r
+ * gathered, hidden rows stored, hidden gathered, x rows stored).  Writes
+ * dims[3] = {workgroups, layer slots, event slots} and copies
+ * min(n, product of dims) stamps of the last launch, indexed
+ * [(workgroup * layer slots + layer) * event slots + event], to host dst
+ * (synchronous).  The regular library returns QD_ERR_ARG and copies nothing.
+ * No counterpart in the reference (its NVIDIA profiling hooks,
+ * cuda_decode_gemv_ops/profile.py, are out of scope). */
+int qd_persistent_trace_read(uint64_t* dst, size_t n, int* dims);
+
 /* Synchronously reads the persistent step's status word (0 = every hand-off
  * completed; bit 0 = a wait exhausted its spin budget, results of that step
  * are invalid) and clears it when reset != 0. */

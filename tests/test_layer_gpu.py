@@ -209,8 +209,10 @@ def test_engine_step_long_splits_and_poisoned_new_row(cuda, step_mode, splits, p
     logits, tok = O.lm_head_argmax(h, w.final_norm_weight, w.embed_tokens, 1e-6)
     assert_close_rel(eng.logits.cpu(), logits, what=f"logits ({step_mode}, splits {splits}, pos {pos})")
     assert toks[0] == tok
+    # V comes out of an fp32 GEMV whose summation order differs from the
+    # oracle's, so its fp16 rounding may differ by an ulp: same bar as K
     assert_close_rel(eng.k_caches[0][0, :, pos].cpu(), kc_ref[0, :, pos].float(), what="K row written")
-    assert torch.equal(eng.v_caches[0][0, :, pos].cpu(), vc_ref[0, :, pos])
+    assert_close_rel(eng.v_caches[0][0, :, pos].cpu(), vc_ref[0, :, pos].float(), what="V row written")
     if poison == "nan":   # NaN != NaN: check the rows are still all NaN
         assert torch.isnan(eng.k_caches[0][0, :, pos + 1:]).all() and torch.isnan(eng.v_caches[0][0, :, pos + 1:]).all()
     else:
