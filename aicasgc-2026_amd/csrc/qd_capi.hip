@@ -82,6 +82,48 @@ void attn_ws(void* ws, qd::AttnArgs& a) {
   a.lse = reinterpret_cast<float*>(b + 256 + (size_t)a.Hq * a.n_split * 128 * 4);
 }
 
+// Scratch of the no-allocation attention entry point: one array per GPU
+// (each device holds its own copy of a __device__ variable), resolved to its
+// device address once per device with hipGetSymbolAddress and kept for the
+// process.  Host code never uses the name `scratch` itself: on the host it is
+// a stand-in, not a device address.
+constexpr size_t kNoallocScratchBytes = QD_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kNoallocScratchBytes];
+
+__global__ void clear_words_kernel(unsigned* p, int n) {
+  for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0u;
+}
+
+// Device address of this device's scratch array; on the first call for a
+// device the attention arrival counters at its head are cleared on `s` (a
+// kernel, not a memset, so the call also works inside stream capture).
+int noalloc_scratch(hipStream_t s, void** out) {
+  static std::mutex mu;
+  static std::vector<void*> addr;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    qd_host::set_error("hipGetDevice failed: %s", hipGetErrorString(e));
+    return (int)e;
+  }
+  std::lock_guard<std::mutex> lk(mu);
+  if ((int)addr.size() <= dev) addr.resize(dev + 1, nullptr);
+  if (addr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      qd_host::set_error("hipGetSymbolAddress(scratch) failed on device %d: %s", dev, hipGetErrorString(e));
+      return e != hipSuccess ? (int)e : QD_ERR_WORKSPACE;
+    }
+    hipLaunchKernelGGL(clear_words_kernel, dim3(1), dim3(64), 0, s, reinterpret_cast<unsigned*>(p), 64);
+    const int st = qd_host::launch_status("clear_words_kernel");
+    if (st != QD_OK) return st;
+    addr[dev] = p;
+  }
+  *out = addr[dev];
+  return QD_OK;
+}
+
 int check_gemv_ptrs(const void* x, const void* W, const void* y, int N, int K) {
   QD_REQUIRE(x && W && y, QD_ERR_ARG, "null pointer");
   QD_REQUIRE(N > 0 && K > 0 && (K % 8) == 0, QD_ERR_SHAPE, "need N > 0 and K %% 8 == 0 (N=%d K=%d)", N, K);
@@ -339,6 +381,24 @@ int qd_attention_decode(const void* q, int q_dtype, long q_stride, const void* k
   if (st) return st;
   return out_dtype == QD_F16 ? qd::attention_merge_launch<u16>(a, S(stream))
                              : qd::attention_merge_launch<float>(a, S(stream));
+}
+
+int qd_attention_decode_noalloc(const void* q, int q_dtype, long q_stride, const void* k_cache,
+                                const void* v_cache, long cache_stride_h, long cache_stride_s, int T,
+                                const int64_t* cache_position, float scale, void* out, int out_dtype, int Hq, int Hkv,
+                                int n_split, void* stream) {
+  // the size check comes first: an oversized request launches nothing
+  QD_REQUIRE(Hq > 0 && Hkv > 0 && n_split >= 1 && n_split <= 1024, QD_ERR_SHAPE, "bad head or split counts");
+  const size_t need = attn_ws_bytes(Hq, Hkv, n_split);
+  QD_REQUIRE(need <= kNoallocScratchBytes, QD_ERR_WORKSPACE,
+             "qd_attention_decode_noalloc: Hq=%d x n_split=%d needs %zu bytes of scratch, more than the %zu the "
+             "library holds per GPU (use qd_attention_decode with a workspace, or fewer splits)",
+             Hq, n_split, need, kNoallocScratchBytes);
+  void* ws = nullptr;
+  const int st = noalloc_scratch(S(stream), &ws);
+  if (st) return st;
+  return qd_attention_decode(q, q_dtype, q_stride, k_cache, v_cache, cache_stride_h, cache_stride_s, T,
+                             cache_position, scale, out, out_dtype, Hq, Hkv, n_split, ws, stream);
 }
 
 int qd_attention_partial(const void* q, int q_dtype, long q_stride, const void* k_cache, const void* v_cache,

@@ -190,6 +190,26 @@ int qd_attention_decode(const void* q, int q_dtype, long q_stride,
                         void* out, int out_dtype, int Hq, int Hkv, int n_split,
                         void* workspace, void* stream);
 
+/* qd_attention_decode without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference, which
+ * always takes a caller-allocated workspace.  The partials and the arrival
+ * counters live in a library-owned static device array of
+ * QD_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; the call
+ * allocates nothing.  It accepts qd_attention_workspace_bytes(Hq, Hkv, n_split)
+ * <= QD_NOALLOC_SCRATCH_BYTES (Hq = 16: up to 126 splits) and otherwise
+ * returns QD_ERR_WORKSPACE without launching.  Every call on one GPU uses
+ * that GPU's array: calls that overlap in time on one GPU (two streams, two
+ * host threads) race and must be ordered by the caller.  The first call on a
+ * device also enqueues a small kernel that clears the counters. */
+#define QD_NOALLOC_SCRATCH_BYTES (1u << 20)
+int qd_attention_decode_noalloc(const void* q, int q_dtype, long q_stride,
+                                const void* k_cache, const void* v_cache,
+                                long cache_stride_h, long cache_stride_s, int T,
+                                const int64_t* cache_position, float scale,
+                                void* out, int out_dtype, int Hq, int Hkv, int n_split,
+                                void* stream);
+
 /* The same computation as two launches: partials only (o_part fp32
  * [Hq, n_split, 128], lse fp32 [Hq, n_split]), then the merge.  Replaces
  * decode_attn_v4_splitkv (cuda_decode_attention.py:226-302). */
