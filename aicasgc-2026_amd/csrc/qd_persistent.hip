@@ -42,23 +42,26 @@
 
 namespace qd {
 
-// Phase timestamps (library built with -DQD_TRACE only): wave 0 of every
-// workgroup records the 100 MHz real-time clock at fixed points of each layer
-// of the last launch; qd_persistent_trace_read copies them to the host.
-constexpr int kTraceLayers = 32, kTraceEvents = 16;
+// Phase timestamps (library built with -DQD_TRACE only): the first thread of
+// wave 0 (a poller, events 0..15) and of wave 4 (a streamer, events 16..31)
+// of every workgroup record the 100 MHz real-time clock at fixed points of
+// each layer of the last launch; qd_persistent_trace_read copies them out.
+constexpr int kTraceLayers = 32, kTraceEvents = 32;
 #ifdef QD_TRACE
 __device__ unsigned long long qd_trace_stamps[kPersistBlocks * kTraceLayers * kTraceEvents];
-#define QD_TRACE_AT(l, e)                                                                         \
+#define QD_TRACE_BY(tid0, l, e)                                                                   \
   do {                                                                                           \
-    if (!STREAM && threadIdx.x == 0)                                                             \
+    if (threadIdx.x == (tid0))                                                                   \
       qd_trace_stamps[((size_t)blockIdx.x * kTraceLayers + (l)) * kTraceEvents + (e)] =          \
           __builtin_amdgcn_s_memrealtime();                                                      \
   } while (0)
 #else
-#define QD_TRACE_AT(l, e) \
-  do {                    \
+#define QD_TRACE_BY(tid0, l, e) \
+  do {                          \
   } while (0)
 #endif
+#define QD_TRACE_AT(l, e) QD_TRACE_BY(0, l, e)                  // poller wave 0
+#define QD_TRACE_ST(l, e) QD_TRACE_BY(4 * kWave, l, 16 + (e))   // streamer wave 4
 
 namespace {
 
@@ -439,6 +442,7 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
 
     // ================================================================ QKV
     QD_TRACE_AT(l, 0);
+    QD_TRACE_ST(l, 0);
     QD_FRESH_LANE();
     if (l == 0) {
       long tok = a.token[0];
@@ -450,6 +454,7 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
     }
     __syncthreads();
     QD_TRACE_AT(l, 1);
+    QD_TRACE_ST(l, 1);
     QD_FRESH_LANE();
     {
       float y[2];
@@ -458,8 +463,10 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
       if (!streamer) puts_done();
     }
     QD_TRACE_AT(l, 2);
+    QD_TRACE_ST(l, 2);
     QD_FRESH_LANE();
     if (streamer) issue_gu(Lw, wgu);
+    QD_TRACE_ST(l, 3);
 
     // ================================================================ ATTN
     QD_FRESH_LANE();
@@ -475,6 +482,7 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
     }
     __syncthreads();
     QD_TRACE_AT(l, 3);
+    QD_TRACE_ST(l, 4);
     if (w < 4) {
       const int j = lane;
       const float x0 = s_raw[w][j], x1 = s_raw[w][j + 64];
@@ -503,6 +511,8 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
       }
     }
     __syncthreads();
+    QD_TRACE_AT(l, 15);
+    QD_TRACE_ST(l, 5);
     QD_FRESH_LANE();
     {
       const int row_off = lane >> 4;  // 16-lane row inside the wave
@@ -574,9 +584,12 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
       }
     }
     QD_TRACE_AT(l, 4);
+    QD_TRACE_ST(l, 6);
     QD_FRESH_LANE();
     if (streamer) issue_wd(Lw, wd);
+    QD_TRACE_ST(l, 7);
     __syncthreads();
+    QD_TRACE_ST(l, 8);
     if (tid < 2 * D) {
       const int g = tid / D;
       const int d = tid % D;
@@ -634,7 +647,9 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
     // waves 1-3 right after the partials, wave 0 after its two polls
     QD_FRESH_LANE();
     if (!streamer) issue_gu(Lw, wgu);
+    QD_TRACE_AT(l, 13);
     __syncthreads();
+    QD_TRACE_ST(l, 9);
 
     // ================================================================ O_PROJ
     QD_TRACE_AT(l, 7);
@@ -646,12 +661,14 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
       if (!streamer) puts_done();
     }
     QD_TRACE_AT(l, 8);
+    QD_TRACE_ST(l, 10);
 
     // ================================================================ GATE_UP
     QD_FRESH_LANE();
     if (!streamer) gather4<H / (4 * NA * kWave), NA * kWave>(r_r, s_r, (unsigned)tid, par, sp);
     __syncthreads();
     QD_TRACE_AT(l, 9);
+    QD_TRACE_ST(l, 11);
     QD_FRESH_LANE();
     u32x4 gi_next, gp_next;
     if (!streamer) {
@@ -659,6 +676,7 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
       gp_next = ld16(Ln.post_norm + tid * 8);
       issue_wd(Lw, wd);
     }
+    QD_TRACE_AT(l, 14);
     {
       float gu[6];
       rows_dot_norm<4, 6>(wgu, s_r, s_gpost, lds_rstd<4>(s_r, lane, a.eps), lane, gu);
@@ -672,17 +690,20 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
       if (!streamer) puts_done();
     }
     QD_TRACE_AT(l, 10);
+    QD_TRACE_ST(l, 12);
     QD_FRESH_LANE();
     if (streamer) {
       issue_qkv(Ln, rs_n);
       issue_kvwo(Ln, rs_n, tl_n);
     }
+    QD_TRACE_ST(l, 13);
 
     // ================================================================ DOWN
     QD_FRESH_LANE();
     if (!streamer) gather4<I / (4 * NA * kWave), NA * kWave>(r_hid, s_h, (unsigned)tid, par, sp);
     __syncthreads();
     QD_TRACE_AT(l, 11);
+    QD_TRACE_ST(l, 14);
     QD_FRESH_LANE();
     if (!streamer) {
       // every wave finished this layer's norms before the barrier above
@@ -698,6 +719,7 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
         put(a.x_t + gw, par, v);
         if (l + 1 == a.num_layers) a.x_out[gw] = v;
       }
+      QD_TRACE_ST(l, 15);
       if (!streamer) {
         puts_done();
         QD_TRACE_AT(l, 12);

@@ -29,6 +29,15 @@ import numpy as np
 EVENTS = ["layer start", "x gathered", "qkv rows stored", "qkv gathered", "attention loop done",
           "split partials stored", "merged output gathered", "o_proj start", "r rows stored", "r gathered",
           "hidden rows stored", "hidden gathered", "x rows stored"]
+# further points of the same poller wave (slots 13..15) and of a streamer wave (slots 16..31)
+EXTRA = {13: "poller: W_gate/up rows issued", 14: "poller: W_down rows issued (gate_up phase)",
+         15: "poller: q/k RoPE barrier passed",
+         16: "streamer: layer start", 17: "streamer: x gathered", 18: "streamer: qkv rows stored",
+         19: "streamer: W_gate/up rows issued", 20: "streamer: qkv gathered", 21: "streamer: q/k RoPE barrier passed",
+         22: "streamer: attention loop done", 23: "streamer: W_down rows issued", 24: "streamer: slot-merge barrier passed",
+         25: "streamer: merged output gathered", 26: "streamer: r rows stored", 27: "streamer: r gathered",
+         28: "streamer: hidden rows stored", 29: "streamer: next layer's W_qkv, K/V, W_o issued",
+         30: "streamer: hidden gathered", 31: "streamer: x rows stored"}
 LINKS = ["x hand-off", "QKV rows", "qkv hand-off", "q/k norm+RoPE, attention", "slot merge + partial store",
          "split merge + merged-output hand-off", "barrier", "o_proj rows", "r hand-off", "gate_up rows",
          "hidden hand-off", "down rows"]
@@ -72,8 +81,10 @@ def timeline(ctx: int, reps: int = 4, seed: int = 3) -> dict:
                "qd_persistent_trace_read")
     n_layers = len(w.layers)
     ev = len(EVENTS)
-    t = buf.reshape(nb, nl, ne)[:, :n_layers, :ev].astype(np.int64)
+    t_all = buf.reshape(nb, nl, ne)[:, :n_layers, :].astype(np.int64)
+    t = t_all[:, :, :ev]
     us = (t - t[:, 0, 0].min()) / CLOCK_HZ * 1e6
+    us_all = (t_all - t[:, 0, 0].min()) / CLOCK_HZ * 1e6
     last = us.max(axis=0)                       # [layer, event]: the last workgroup to pass each point
     inner = slice(1, n_layers - 1)
     links = {}
@@ -81,9 +92,23 @@ def timeline(ctx: int, reps: int = 4, seed: int = 3) -> dict:
         links[LINKS[e - 1]] = round(float(np.median(last[inner, e] - last[inner, e - 1])), 2)
     links["next layer start"] = round(float(np.median(last[2:n_layers, 0] - last[1:n_layers - 1, ev - 1])), 2)
     period = float(np.median(np.diff(last[:, ev - 1])))
+    # every recorded point as an offset from the layer's start (last workgroup
+    # through each), median over the inner layers
+    last_all = us_all.max(axis=0)
+    med_all = np.median(us_all, axis=0)
+    names = {i: f"poller: {n}" for i, n in enumerate(EVENTS)} | (EXTRA if ne > 16 else {})
+    timeline_pts = []
+    for e, name in names.items():
+        if e >= ne:
+            continue
+        off_last = float(np.median(last_all[inner, e] - last_all[inner, 0]))
+        off_med = float(np.median(med_all[inner, e] - med_all[inner, 0]))
+        timeline_pts.append((round(off_last, 2), round(off_med, 2), name))
+    timeline_pts.sort()
     return {"context_rows": ctx, "launch_us": [round(x, 1) for x in launch_us],
             "traced_span_us": round(float(last[n_layers - 1, ev - 1]), 1), "layer_period_us": round(period, 2),
             "links_us": links,
+            "timeline_us": [{"at_last_wg": a, "at_median_wg": b, "point": n} for a, b, n in timeline_pts],
             "method": "median over layers 1..L-2 of the time between consecutive points, each point taken "
                       "when the last workgroup passed it (s_memrealtime, 100 MHz), last of "
                       f"{reps} launches"}
@@ -101,6 +126,9 @@ def main(argv=None) -> int:
               f"{r['launch_us'][-1]} us (traced)", file=sys.stderr)
         for k, v in r["links_us"].items():
             print(f"  {k:40s} {v:6.2f} us", file=sys.stderr)
+        print("  timeline from layer start (last workgroup / median workgroup):", file=sys.stderr)
+        for p in r["timeline_us"]:
+            print(f"    {p['at_last_wg']:7.2f} {p['at_median_wg']:7.2f}  {p['point']}", file=sys.stderr)
     print(json.dumps(out), flush=True)
     if args.json:
         with open(args.json, "w") as f:

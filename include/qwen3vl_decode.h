@@ -343,11 +343,14 @@ int qd_decode_layers_persistent(const qd_model_desc* d, void* stream);
 
 /* Phase timeline of the persistent step, for profiling.  A library built with
  * -DQD_TRACE (libqwen3vl_decode_trace.so, made by the package's build step
- * next to the main library) has wave 0 of every workgroup record the 100 MHz
- * real-time clock at 13 points of every layer of each launch (events 0..12:
- * layer start, x gathered, qkv rows stored, qkv gathered, attention loop done,
- * split partials stored, merged output gathered, o_proj start, r rows stored, r
- * gathered, hidden rows stored, hidden gathered, x rows stored).  Writes
+ * next to the main library) has the first thread of wave 0 (a polling wave)
+ * and of wave 4 (a streaming wave) of every workgroup record the 100 MHz
+ * real-time clock at fixed points of every layer of each launch: events 0..12
+ * (wave 0) layer start, x gathered, qkv rows stored, qkv gathered, attention
+ * loop done, split partials stored, merged output gathered, o_proj start, r
+ * rows stored, r gathered, hidden rows stored, hidden gathered, x rows stored;
+ * 13..15 further wave-0 points; 16..31 wave 4's points (the names are listed
+ * in qwen3vl_hip/phase_trace.py).  Writes
  * dims[3] = {workgroups, layer slots, event slots} and copies
  * min(n, product of dims) stamps of the last launch, indexed
  * [(workgroup * layer slots + layer) * event slots + event], to host dst
