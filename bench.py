@@ -325,6 +325,133 @@ def bench_configs012(w, cpu: bool, reps: int = 5) -> dict:
     return out
 
 
+def dropin_text_model(w, device):
+    """transformers' Qwen3VLTextModel at the Qwen3-VL-2B text shape holding the
+    synthetic fp16 weights, every decoder layer swapped by
+    optimized_layer.replace_decoder_layers (reference optimized_layer.py:3848).
+    Built on the meta device and materialised on the GPU (the rotary buffers
+    are recomputed there, in fp32)."""
+    import torch
+    from transformers.models.qwen3_vl.configuration_qwen3_vl import Qwen3VLTextConfig
+    from transformers.models.qwen3_vl.modeling_qwen3_vl import Qwen3VLTextModel, Qwen3VLTextRotaryEmbedding
+
+    import optimized_layer
+
+    s = w.shape
+    cfg = Qwen3VLTextConfig(hidden_size=s.hidden, intermediate_size=s.intermediate, num_attention_heads=s.num_heads,
+                            num_key_value_heads=s.num_kv_heads, head_dim=s.head_dim, num_hidden_layers=s.num_layers,
+                            vocab_size=s.vocab, rms_norm_eps=s.rms_eps,
+                            rope_parameters={"rope_type": "default", "rope_theta": s.rope_theta,
+                                             "mrope_section": list(s.mrope_section)})
+    cfg._attn_implementation = "sdpa"
+    with torch.device("meta"):
+        m = Qwen3VLTextModel(cfg)
+    m = m.to_empty(device=device).half().eval()
+    with torch.device(device):
+        m.rotary_emb = Qwen3VLTextRotaryEmbedding(cfg)
+    q, kv, i = s.q_size, s.kv_size, s.intermediate
+    with torch.no_grad():
+        m.embed_tokens.weight.copy_(w.embed_tokens)
+        m.norm.weight.copy_(w.final_norm_weight)
+        for lw, L in zip(w.layers, m.layers):
+            a = L.self_attn
+            a.q_proj.weight.copy_(lw.qkv_weight[:q])
+            a.k_proj.weight.copy_(lw.qkv_weight[q:q + kv])
+            a.v_proj.weight.copy_(lw.qkv_weight[q + kv:])
+            a.o_proj.weight.copy_(lw.o_proj_weight)
+            a.q_norm.weight.copy_(lw.q_norm_weight)
+            a.k_norm.weight.copy_(lw.k_norm_weight)
+            L.mlp.gate_proj.weight.copy_(lw.gate_up_weight[:i])
+            L.mlp.up_proj.weight.copy_(lw.gate_up_weight[i:])
+            L.mlp.down_proj.weight.copy_(lw.down_proj_weight)
+            L.input_layernorm.weight.copy_(lw.input_layernorm_weight)
+            L.post_attention_layernorm.weight.copy_(lw.post_attn_layernorm_weight)
+    optimized_layer.replace_decoder_layers(m)
+    return m, cfg
+
+
+def bench_dropin(w, prompt, k_caches, v_caches, first: int, steps: int, warmup: int, golden) -> dict:
+    """The reference's own decode loop over the drop-in layers: one step of the
+    swapped transformers model (embedding, M-RoPE cos/sin, 28 swapped layers,
+    final norm, tied lm_head in fp16, argmax) captured in a HIP graph and
+    replayed with the static input buffers rewritten on the device between
+    replays (DecodeCudaGraphRunner, evaluation_wrapper.py:864-904, :941-960).
+    It continues from the native engine's prefilled K/V rows, so its tokens are
+    compared with the golden stream (reported, not required: this path keeps
+    fp16 activations between kernels, as the reference does)."""
+    import torch
+    from transformers.cache_utils import StaticCache
+
+    dev = k_caches[0].device
+    model, cfg = dropin_text_model(w, dev)
+    S = prompt.length
+    n = warmup + steps
+    max_len = S + n + 2
+    cache = StaticCache(config=cfg, max_cache_len=max_len)
+    like = torch.empty(1, w.shape.num_kv_heads, 1, w.shape.head_dim, dtype=torch.float16, device=dev)
+    for li, layer in enumerate(cache.layers):
+        if not layer.is_initialized:
+            layer.lazy_initialization(like, like)
+        layer.keys[:, :, :S].copy_(k_caches[li][:, :, :S])
+        layer.values[:, :, :S].copy_(v_caches[li][:, :, :S])
+    ids = torch.zeros(1, 1, dtype=torch.int64, device=dev)
+    cache_position = torch.zeros(1, dtype=torch.int64, device=dev)
+    position_ids = torch.zeros(3, 1, 1, dtype=torch.int64, device=dev)
+    mask = torch.zeros(1, max_len, dtype=torch.int64, device=dev)
+    mask[:, :S] = 1
+    next_token = torch.zeros(1, 1, dtype=torch.int64, device=dev)
+    out_tokens = torch.zeros(n, dtype=torch.int64, device=dev)
+    emb = w.embed_tokens
+
+    def run():
+        out = model(input_ids=ids, attention_mask=mask, position_ids=position_ids, past_key_values=cache,
+                    use_cache=True, cache_position=cache_position)
+        logits = out.last_hidden_state[:, -1] @ emb.T
+        next_token.copy_(torch.argmax(logits, dim=-1, keepdim=True))
+
+    def write_inputs(p):   # the runner's _write_inputs: device-side copies and fills, no host sync
+        ids.copy_(next_token)
+        cache_position.fill_(p)
+        position_ids.fill_(p + prompt.rope_delta)
+        mask[:, p] = 1
+
+    next_token.fill_(first)
+    write_inputs(S)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side), torch.no_grad():
+        run()                      # warm-up of lazy initialisation, outside the capture
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    next_token.fill_(first)
+    write_inputs(S)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph), torch.no_grad():
+        run()
+    next_token.fill_(first)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for i in range(n):
+        if i == warmup:
+            e0.record()
+        write_inputs(S + i)
+        graph.replay()
+        out_tokens[i].copy_(next_token[0, 0])
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    toks = out_tokens.tolist()
+    gold = golden["tokens"][1:1 + n]
+    match = next((i for i, (a, b) in enumerate(zip(toks, gold)) if a != b), min(len(toks), len(gold)))
+    del graph, model, cache
+    torch.cuda.empty_cache()
+    return {"method": "transformers Qwen3VLTextModel with every decoder layer swapped by "
+                      "optimized_layer.replace_decoder_layers, one step captured in a HIP graph, static input "
+                      "buffers rewritten on the device between replays (the reference's DecodeCudaGraphRunner); "
+                      "fp16 tied lm_head + torch.argmax in the graph; HIP events over the timed steps",
+            "ms_per_token": round(ms, 4), "tokens_per_s": round(1000.0 / ms, 1), "steps": steps, "warmup": warmup,
+            "context_start": S, "tokens_match_golden_prefix": match, "tokens_compared": min(len(toks), len(gold))}
+
+
 def phase_trace(contexts) -> list:
     """Per-link timeline of the persistent step (qwen3vl_hip.phase_trace) in a
     child process that loads the traced library, so this process's numbers come
@@ -416,6 +543,9 @@ def main() -> int:
                     help="timed steps of the batch-8 workload (config 4); 0 skips it")
     ap.add_argument("--no-configs012", action="store_true",
                     help="skip configs 0-2 (one layer, the GEMVs, attention) against their rooflines")
+    ap.add_argument("--dropin-steps", type=int, default=32,
+                    help="timed steps of the graph-captured drop-in path (transformers model + swapped layers); "
+                         "0 skips it")
     ap.add_argument("--phase-trace", type=int, action="append", metavar="CTX",
                     help="also report the persistent step's per-link timeline at this context (repeatable), from "
                          "the -DQD_TRACE library run in a child process (qwen3vl_hip.phase_trace)")
@@ -562,6 +692,13 @@ def main() -> int:
     head_bytes = 2 * shape.vocab * shape.hidden + 2 * shape.hidden + 4 * shape.hidden
     log(f"lm_head+argmax: {us_head:.2f} us, {head_bytes / (us_head * 1e-6) / 1e9:.1f} GB/s")
 
+    # ---- the drop-in path at config 3 (the reference user's own decode loop)
+    dropin = None
+    if args.dropin_steps > 0:
+        dropin = bench_dropin(w, prompt, eng.k_caches, eng.v_caches, first, args.dropin_steps, 4, gold)
+        log(f"drop-in (transformers model + swapped layers, HIP graph): {dropin['ms_per_token']:.4f} ms/token, "
+            f"golden prefix {dropin['tokens_match_golden_prefix']}/{dropin['tokens_compared']}")
+
     # ---- config 4: 8 sequences, ragged contexts L_i ~ U[2048, 4096]
     b8 = None
     if args.batch8_steps > 0:
@@ -661,6 +798,7 @@ def main() -> int:
         "batch8": b8,
         "configs012": c012,
         "phase_trace": traced,
+        "dropin": dropin,
     }
     print(json.dumps(out), flush=True)
     return 0
