@@ -332,10 +332,14 @@ int qd_add_f16(const void* a, const void* b, void* out, long n, void* stream) {
 size_t qd_attention_workspace_bytes(int Hq, int Hkv, int n_split) { return attn_ws_bytes(Hq, Hkv, n_split); }
 
 int qd_attention_default_splits(int T) {
-  // ~64 positions per workgroup, at least 4 and at most 64 splits per kv head
-  int s = (T + 63) / 64;
+  // ~128 positions per workgroup, at least 4 and at most 16 splits per kv head,
+  // so the merge always runs in the partial kernel (one launch).  Measured per
+  // call at T = L: 8 splits are fastest at 1024, 16 at 4096, and at 8192 16
+  // splits (one launch) are within 3% of 32 (partials + merge kernel); more
+  // splits only lengthen the merge.
+  int s = (T + 127) / 128;
   if (s < 4) s = 4;
-  if (s > 64) s = 64;
+  if (s > 16) s = 16;
   return s;
 }
 
@@ -534,9 +538,13 @@ bool step_layout(const qd_model_desc* d, int splits, StepBuffers* b, size_t* tot
 // sequence-heads to spread over the CUs, so it takes 1/B as many (at least 4).
 int splits_of(const qd_model_desc* d) {
   if (d->attn_splits > 0) return d->attn_splits;
-  const int s = qd_attention_default_splits(d->capacity);
   const int B = batch_of(d);
-  return B > 1 ? std::max(4, s / B) : s;
+  if (B > 1) {
+    // batch: ~64 positions per workgroup over the B sequences, 4..64 / B splits
+    const int s = std::min(64, std::max(4, (d->capacity + 63) / 64));
+    return std::max(4, s / B);
+  }
+  return qd_attention_default_splits(d->capacity);
 }
 
 }  // namespace

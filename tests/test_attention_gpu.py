@@ -51,7 +51,7 @@ def test_attention_split_count_invariance(cuda, split_k):
     assert_close_rel(out, ref, what=f"split_k={split_k}")
 
 
-@pytest.mark.parametrize("L", [1024, 4096])   # 16 splits: one launch; 64: partials + merge kernel
+@pytest.mark.parametrize("L", [1024, 4096, 8192])   # 8 / 16 / 16 default splits
 def test_attention_partial_merge_matches_fused(cuda, L):
     import cuda_decode_attention as A
     from qwen3vl_hip import synthetic as syn
@@ -86,8 +86,8 @@ def test_attention_equal_keys_give_mean_of_values(cuda):
     assert_close_rel(out, expect, what="equal keys")
 
 
-@pytest.mark.parametrize("T", [1024, 2048])   # one launch with arrival counters; two launches
-def test_attention_graph_replay_self_resets(cuda, T):
+@pytest.mark.parametrize("T,split_k", [(1024, 4), (2048, 32)])   # one launch (arrival counters); two launches
+def test_attention_graph_replay_self_resets(cuda, T, split_k):
     """Capture once, replay at several cache positions: the arrival counters
     reset themselves, so every replay matches the eager result and the oracle."""
     import cuda_decode_attention as A
@@ -97,17 +97,18 @@ def test_attention_graph_replay_self_resets(cuda, T):
     qd, kd, vd = q.to(cuda), kc.to(cuda), vc.to(cuda)
     cp = torch.tensor([100], dtype=torch.int64, device=cuda)
     ws: dict = {}
-    A.decode_attn_v4_cta_qhead_splitkv_fused(qd, kd, vd, SCALE, 2, cp, workspace=ws)  # warm-up
+    A.decode_attn_v4_cta_qhead_splitkv_fused(qd, kd, vd, SCALE, 2, cp, split_k=split_k, workspace=ws)  # warm-up
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        out = A.decode_attn_v4_cta_qhead_splitkv_fused(qd, kd, vd, SCALE, 2, cp, workspace=ws)
+        out = A.decode_attn_v4_cta_qhead_splitkv_fused(qd, kd, vd, SCALE, 2, cp, split_k=split_k, workspace=ws)
     for pos in (100, T - 1, 5, T // 2 - 1, T + 100):
         cp.fill_(pos)
         g.replay()
         torch.cuda.synchronize()
         got = out.reshape(16, 128).clone()
-        eager = A.decode_attn_v4_cta_qhead_splitkv_fused(qd, kd, vd, SCALE, 2, cp, workspace={})
+        eager = A.decode_attn_v4_cta_qhead_splitkv_fused(qd, kd, vd, SCALE, 2, cp, split_k=split_k,
+                                                         workspace={})
         torch.cuda.synchronize()
         assert torch.equal(got, eager.reshape(16, 128))
         assert_close_rel(got, O.decode_attention(q.reshape(16, 128), kc, vc, pos, SCALE), what=f"replay pos={pos}")

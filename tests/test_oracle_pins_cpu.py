@@ -185,13 +185,22 @@ def test_post_attn_mlp_matches_transformers_modules():
     norm = Qwen3VLTextRMSNorm(256, eps=1e-6).double()
     g = torch.Generator().manual_seed(11)
     with torch.no_grad():
+        # every parameter set explicitly: module construction may leave them
+        # uninitialised when an earlier test disabled transformers' weight init
+        for lin in (mlp.gate_proj, mlp.up_proj, mlp.down_proj):
+            lin.weight.copy_(0.05 * torch.randn(lin.weight.shape, generator=g, dtype=D64))
         norm.weight.copy_(1 + 0.02 * torch.randn(256, generator=g))
     res, att = torch.randn(256, generator=g, dtype=D64), torch.randn(256, generator=g, dtype=D64)
     gu = torch.cat([mlp.gate_proj.weight, mlp.up_proj.weight], 0).detach()
     hid, out, r = O.post_attn_mlp(res, att, norm.weight.detach(), gu, mlp.down_proj.weight.detach(), None, 1e-6, D64)
     with torch.no_grad():
-        ref = (res + att) + mlp(norm(res + att))
-    assert torch.allclose(out, ref, atol=1e-12) and torch.allclose(r, res + att)
+        # transformers' MLP module on an fp64 RMSNorm: exact to fp64 rounding
+        ref = (res + att) + mlp(F.rms_norm(res + att, (256,), norm.weight, eps=1e-6))
+        # transformers' own RMSNorm module normalises in fp32 (relative error ~6e-8)
+        ref_hf = (res + att) + mlp(norm(res + att))
+    assert torch.allclose(out, ref, rtol=1e-12, atol=1e-12) and torch.equal(r, res + att)
+    assert torch.allclose(out, ref_hf, rtol=0, atol=1e-6 * float(ref_hf.abs().max()))
+    assert float((out - (res + att)).abs().max()) > 0.1   # the MLP term is present, not zero
 
 
 def test_lm_head_argmax_takes_first_maximum():
