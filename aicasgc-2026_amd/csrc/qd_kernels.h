@@ -163,7 +163,8 @@ struct PersistArgs {
   const int64_t* cache_position;  // int64 [1]
   const int64_t* rope_position;   // int64 [3]
   const float* inv_freq;          // fp32 [64]
-  // hand-off buffers: fp32 words whose mantissa LSB carries the write parity
+  // hand-off buffers (the per-device uncached hand-off area): fp32 words
+  // whose mantissa LSB carries the write parity
   unsigned* x_t;                  // [H]
   unsigned* qkv_t;                // [Hq*D + 2*Hkv*D]
   unsigned* opart_t;              // [Hq, splits, D]
@@ -173,8 +174,11 @@ struct PersistArgs {
   unsigned* hid_t;                // [I]
   float* x_out;                   // fp32 [H]: last layer's output (lm_head input)
   unsigned* status;               // bit 0: a hand-off wait ran out of its spin budget
-  unsigned* epoch;                // step counter that makes the tags unique
-  unsigned* done;                 // workgroups finished (self-resetting)
+  // per-device state shared by every persistent launch on the device, like the
+  // hand-off words: the layer generation (layers run so far; the words' write
+  // parity follows it) and the workgroups finished in this launch (self-resetting)
+  unsigned* generation;
+  unsigned* done;
 };
 
 // Model shape the persistent kernel is specialised for, and its grid.

@@ -27,7 +27,9 @@
 // seen the previous write, can only see that write (wrong parity) or the one
 // it waits for: one bit is a complete tag.  A wave waits for its own stores to
 // complete before it polls; polling with a store in flight is several times
-// slower on this part.
+// slower on this part.  The words live in one uncached area per device, shared
+// by every persistent launch on it; the parity follows a per-device layer
+// generation, so launches of different layer counts keep the sequence.
 //
 // Every wait is bounded: a thread polls at most kSpinLimit times per launch,
 // then records an error in the status word and continues, so the grid always
@@ -82,11 +84,13 @@ static_assert(H == NTH, "o_proj / down: one row per wave");
 static_assert(I == 3 * NTH, "gate_up: three row pairs per wave");
 static_assert(MERGE_DIMS == 8, "merge: 8 dims per workgroup");
 
-// Parity of the words written at layer l of the launch with epoch ep.  It
-// alternates from layer to layer and across launches (the epoch advances once
-// per launch); the +1 makes the first write differ from a zeroed workspace.
-__device__ __forceinline__ unsigned parity_of(unsigned ep, int num_layers, int l) {
-  return (ep * (unsigned)num_layers + (unsigned)l + 1u) & 1u;
+// Parity of the words written at layer l of the launch that starts at layer
+// generation gen.  It alternates from layer to layer and across launches of
+// any layer count (the generation advances by the launch's layer count, and
+// its wrap at 2^32 keeps the low bit's sequence); the +1 makes the first write
+// differ from the zeroed hand-off area.
+__device__ __forceinline__ unsigned parity_of(unsigned gen, int l) {
+  return (gen + (unsigned)l + 1u) & 1u;
 }
 
 __device__ __forceinline__ unsigned word_of(float v, unsigned par) {
@@ -317,7 +321,7 @@ struct __align__(16) Smem {
 struct Ctx {
   int w, gw, kvh, split, t0, t1, mh, md0;
   long pos;
-  unsigned ep;
+  unsigned gen;
   float rc, rs;               // M-RoPE cos / sin of rotary pair `lane`
 };
 
@@ -331,7 +335,7 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
   const int w = cx.w, gw = cx.gw, kvh = cx.kvh, split = cx.split, t0 = cx.t0, t1 = cx.t1, mh = cx.mh,
             md0 = cx.md0;
   const long pos = cx.pos;
-  const unsigned ep = cx.ep;
+  const unsigned gen = cx.gen;
   const float rc = cx.rc, rs = cx.rs;
   constexpr bool streamer = STREAM;
   const bool poller = (w == 0);     // polls the split partials (MERGE) and the merged output
@@ -428,7 +432,7 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
 
   for (int l = 0; l < a.num_layers; ++l) {
     const PersistLayer& Lw = a.layers[l];
-    const unsigned par = parity_of(ep, a.num_layers, l);
+    const unsigned par = parity_of(gen, l);
     // The next layer's weights are issued unconditionally (a conditional issue
     // would leave the previous values live to the end of the iteration on the
     // path that skips it); after the last layer the loads are made cheap
@@ -745,7 +749,7 @@ __global__ __launch_bounds__(512) void decode_persistent_kernel(const PersistArg
   Ctx cx;
   cx.w = w;
   cx.gw = b * NW + w;
-  cx.ep = a.epoch[0];
+  cx.gen = a.generation[0];
   cx.pos = a.cache_position[0];
   long Ll = cx.pos + 1 < (long)a.T ? cx.pos + 1 : (long)a.T;
   if (Ll < 0) Ll = 0;
@@ -768,15 +772,15 @@ __global__ __launch_bounds__(512) void decode_persistent_kernel(const PersistArg
   if (w >= NA) persist_layers<true>(a, cx, sm, sp);
   else persist_layers<false>(a, cx, sm, sp);
 
-  // The last workgroup to finish advances the epoch for the next launch.  Every
-  // workgroup read the epoch before it produced anything, so none can read the
-  // new value in this launch.
+  // The last workgroup to finish advances the generation by this launch's
+  // layer count.  Every workgroup read the generation before it produced
+  // anything, so none can read the new value in this launch.
   __syncthreads();
   if (tid == 0) {
     const unsigned n = __hip_atomic_fetch_add(a.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (n == NB - 1) {
       __hip_atomic_store(a.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(a.epoch, cx.ep + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(a.generation, cx.gen + (unsigned)a.num_layers, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }

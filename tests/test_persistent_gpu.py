@@ -132,6 +132,41 @@ def test_persistent_long_generation_is_deterministic(cuda, two_layer_weights):
     assert len(set(runs[0])) > 100   # a real token stream, not a fixed point
 
 
+def test_persistent_engines_of_different_depths_interleaved(cuda):
+    """Persistent engines of 2 and 3 layers stepping in turn on one device share
+    its hand-off area; the per-device layer generation keeps the word parities
+    consistent (a 3-layer launch shifts the parity of the next 2-layer one), so
+    each engine's tokens match its kernel-chain twin step for step."""
+    from qwen3vl_hip import synthetic as syn
+    from qwen3vl_hip.config import Qwen3VLTextShape
+    from qwen3vl_hip.engine import DecodeEngine
+
+    pos0, cap, n = 300, 512, 12
+    pairs = []
+    for depth in (2, 3):
+        w = syn.model_weights(30 + depth, shape=Qwen3VLTextShape(num_layers=depth, vocab=VOCAB))
+        twin = {}
+        for m in ("persistent", "chain"):
+            eng = DecodeEngine(w, capacity=cap, step_mode=m)
+            g = torch.Generator(device=cuda).manual_seed(depth)
+            for k, v in zip(eng.k_caches, eng.v_caches):
+                k.normal_(generator=g)
+                v.normal_(generator=g)
+            twin[m] = eng
+        assert twin["persistent"].step_mode == "persistent"
+        pairs.append(twin)
+    toks = [{"persistent": [100 + i], "chain": [100 + i]} for i in range(len(pairs))]
+    for step in range(n):
+        for i, twin in enumerate(pairs):
+            for m, eng in twin.items():
+                use_graph = m == "persistent" and step % 2 == 1
+                toks[i][m] += eng.decode(toks[i][m][-1], pos0 + step, 0, 1, use_graph=use_graph)
+    for i, twin in enumerate(pairs):
+        assert twin["persistent"].status() == 0
+        print(f"depth {2 + i}: persistent {toks[i]['persistent']}\n         chain {toks[i]['chain']}", flush=True)
+        assert toks[i]["persistent"] == toks[i]["chain"]
+
+
 def test_persistent_mode_rejected_for_other_shapes(cuda):
     from qwen3vl_hip import _lib
     from qwen3vl_hip import synthetic as syn
