@@ -945,9 +945,18 @@ static int step_phases(const qd_model_desc* d, int first_layer, int n_layers, un
     aa.rope_pos = d->rope_position; aa.inv_freq = d->inv_freq; aa.sec_h = d->sec_h; aa.sec_w = d->sec_w;
     aa.q_rot_out = b.q_rot;
     attn_ws(b.attn_ws, aa);
-    if ((phase_mask & QD_PHASE_ATTN) && (st = qd::attention_partial_launch<float>(aa, s))) return st;
-    // 3. merge of the splits -> attention output [Hq*D]
-    if ((phase_mask & QD_PHASE_ATTN_MERGE) && (st = qd::attention_merge_launch<float>(aa, s))) return st;
+    // 3. merge of the splits -> attention output [Hq*D]: with both phases and
+    //    at most 16 splits in the partial kernel (the last split of each kv
+    //    head merges; arrival counters in the workspace header), else the merge
+    //    kernel (one phase on its own, e.g. when timing the phases)
+    const unsigned attn_both = QD_PHASE_ATTN | QD_PHASE_ATTN_MERGE;
+    if ((phase_mask & attn_both) == attn_both && splits <= 16 && Hkv <= 64) {
+      aa.done = reinterpret_cast<unsigned*>(b.attn_ws);
+      if ((st = qd::attention_partial_launch<float>(aa, s))) return st;
+    } else {
+      if ((phase_mask & QD_PHASE_ATTN) && (st = qd::attention_partial_launch<float>(aa, s))) return st;
+      if ((phase_mask & QD_PHASE_ATTN_MERGE) && (st = qd::attention_merge_launch<float>(aa, s))) return st;
+    }
     // 4. o_proj + residual: r = x + W_o attn
     GemvArgs g4;
     g4.x = b.attn; g4.W = (const u16*)w.o_proj; g4.residual = b.x; g4.y = b.r; g4.N = H; g4.K = qs; g4.ldw = qs;
