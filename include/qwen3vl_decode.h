@@ -222,7 +222,9 @@ int qd_attention_partial(const void* q, int q_dtype, long q_stride,
 int qd_attention_merge(const float* o_part, const float* lse, void* out, int out_dtype,
                        int Hq, int n_split, void* stream);
 
-/* Default split count for a cache of capacity T (fixed per captured graph). */
+/* Default split count for a cache of capacity T (fixed per captured graph):
+ * about 128 rows per split, 4..16 splits, so the merge stays in the partial
+ * kernel. */
 int qd_attention_default_splits(int T);
 
 /* ------------------------------------------------------------------ decode step */
@@ -301,7 +303,9 @@ int qd_decode_workspace_layout(const qd_model_desc* d, size_t* offsets, int n);
 
 /* Enqueue one full batch-1 decode step: embedding row of *token, 28 layers,
  * final norm, lm_head, argmax -> *token.  The K/V of the new token are written
- * at *cache_position.  Capturable into a hipGraph.  Replaces the captured step
+ * at *cache_position.  Capturable into a hipGraph (in persistent mode after a
+ * first step on the device outside capture: see qd_decode_layers_persistent).
+ * Replaces the captured step
  * DecodeCudaGraphRunner._run_step (evaluation_wrapper.py:941-952) driving
  * OptimizedDecoderLayer.forward (optimized_layer.py:108-469) x 28 and
  * FastLmHead (evaluation_wrapper.py:1227-1238). */
@@ -332,8 +336,14 @@ int qd_decode_step_phases(const qd_model_desc* d, int first_layer, int n_layers,
 int qd_decode_step_mode(const qd_model_desc* d);
 
 /* Embedding + all layers as ONE persistent launch: 256 workgroups stay
- * resident and hand activations to each other through tagged words in the
- * workspace (no grid barrier, no kernel boundary between layers).  Leaves the
+ * resident and hand activations to each other through parity-tagged words (no
+ * grid barrier, no kernel boundary between layers).  The words live in one
+ * area per device that the library allocates (uncached device memory, about
+ * 330 KB, plus a 256-byte counter block), zeroes at the first persistent step
+ * on the device and keeps until the process ends; that first step must run
+ * outside stream capture (QD_ERR_ARG otherwise).  Every persistent step on the
+ * device shares the area, so persistent steps on one device are serialised
+ * (each occupies every CU in any case).  Leaves the
  * final hidden state (before the final norm) in the workspace's residual vector
  * x (first offset of qd_decode_workspace_layout); the lm_head phase of
  * qd_decode_step_phases continues from there.  Replaces the same span of the
