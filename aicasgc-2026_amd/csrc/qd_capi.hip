@@ -174,9 +174,9 @@ int qd_rmsnorm_matvec_f16(const void* x, const void* gamma, const void* W, const
   return qd::gemv_store<qd::PRO_RMSNORM, u16, u16>(a, S(stream));
 }
 
-int qd_post_attn_mlp_f16(const void* residual, const void* attn, const void* gamma, const void* W_gu,
+static int post_attn_mlp(const void* residual, const void* attn, const void* gamma, const void* W_gu,
                          const void* W_d, const void* bias, void* hidden_out, void* out, int H, int I, float eps,
-                         void* stream) {
+                         const int64_t* position, int64_t* next_position, void* stream) {
   QD_REQUIRE(residual && attn && gamma && W_gu && W_d && hidden_out && out, QD_ERR_ARG, "null pointer");
   QD_REQUIRE(a16(residual) && a16(attn) && a16(gamma) && a16(W_gu) && a16(W_d) && a16(hidden_out) && a16(out),
              QD_ERR_ARG, "pointers must be 16-byte aligned");
@@ -192,8 +192,24 @@ int qd_post_attn_mlp_f16(const void* residual, const void* attn, const void* gam
   GemvArgs d;
   d.x = hidden_out; d.W = (const u16*)W_d; d.bias = bias; d.residual = out; d.y = out;
   d.N = H; d.K = I; d.ldw = I;
+  d.next_src = position; d.next_dst = next_position;
   st = qd::gemv_store<qd::PRO_PLAIN, u16, u16>(d, S(stream));
   return st;
+}
+
+int qd_post_attn_mlp_f16(const void* residual, const void* attn, const void* gamma, const void* W_gu,
+                         const void* W_d, const void* bias, void* hidden_out, void* out, int H, int I, float eps,
+                         void* stream) {
+  return post_attn_mlp(residual, attn, gamma, W_gu, W_d, bias, hidden_out, out, H, I, eps, nullptr, nullptr,
+                       stream);
+}
+
+int qd_post_attn_mlp_next_f16(const void* residual, const void* attn, const void* gamma, const void* W_gu,
+                              const void* W_d, const void* bias, void* hidden_out, void* out, int H, int I,
+                              float eps, const int64_t* position, int64_t* next_position, void* stream) {
+  QD_REQUIRE(position && next_position, QD_ERR_ARG, "null position pointer");
+  return post_attn_mlp(residual, attn, gamma, W_gu, W_d, bias, hidden_out, out, H, I, eps, position, next_position,
+                       stream);
 }
 
 int qd_gateup_silu_down_f16(const void* x, const void* W_gu, const void* W_d, const void* bias, void* hidden_out,

@@ -101,6 +101,12 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
   const long gw = (long)blockIdx.x * wpb + wib;
   const long nw = (long)gridDim.x * wpb;
   const long stride = nw * RO;
+  if constexpr (EPI == EPI_STORE) {
+    // read and written by this one thread only, and no other thread of the
+    // launch touches either word, so next_src may equal next_dst
+    if (a.next_dst != nullptr && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0)
+      a.next_dst[0] = a.next_src[0] + 1;
+  }
 
   // The weights do not depend on the activation: issue the first row group's
   // loads before the activation prologue so the two latencies overlap.

@@ -41,6 +41,10 @@ struct GemvArgs {
   // logits + torch.argmax: among logits equal in fp16 the first index wins)
   // instead of the fp32 accumulators
   int argmax_f16 = 0;
+  // EPI_STORE: one thread also writes next_dst[0] = next_src[0] + 1 (a decoder
+  // layer's last kernel advancing its cache's running length); null = none
+  const int64_t* next_src = nullptr;
+  int64_t* next_dst = nullptr;
 };
 
 template <int PRO, typename TX, typename TY>

@@ -130,7 +130,9 @@ def fused_gateup_silu_downproj_mega_partial_half(x, gate_up_weight, down_proj_we
 
 
 def _post_attn_mlp(name, residual, attn_output, norm_weight, gate_up_weight, down_proj_weight, bias, eps, workspace,
-                   kind):
+                   kind, next_position=None):
+    """next_position: optional (position, length) int64 device words; the last
+    kernel then also writes length = position + 1."""
     _require_decode_half(name, residual, attn_output, norm_weight, gate_up_weight, down_proj_weight, x=residual)
     if residual.shape != attn_output.shape:
         raise RuntimeError(f"{name} expects fp16 CUDA single-token decode tensors")
@@ -146,8 +148,16 @@ def _post_attn_mlp(name, residual, attn_output, norm_weight, gate_up_weight, dow
     out = _reuse(workspace, kind, "out", (n,), residual.dtype, residual.device)
     b = _vec(bias) if bias is not None else None
     rv, av, gv = _vec(residual), _vec(attn_output), _vec(norm_weight)   # held until the launch is enqueued
-    _check(_load_ext().qd_post_attn_mlp_f16(_p(rv), _p(av), _p(gv), _p(wgu), _p(wd), _p(b), _p(hidden), _p(out), h,
-                                            i, float(eps), _stream(residual)), name)
+    if next_position is None:
+        _check(_load_ext().qd_post_attn_mlp_f16(_p(rv), _p(av), _p(gv), _p(wgu), _p(wd), _p(b), _p(hidden), _p(out),
+                                                h, i, float(eps), _stream(residual)), name)
+    else:
+        pos, length = next_position
+        if not all(t.device == residual.device and t.dtype == torch.int64 and t.numel() == 1 for t in (pos, length)):
+            raise RuntimeError(f"{name}: position and length must be single int64 words on the GPU")
+        _check(_load_ext().qd_post_attn_mlp_next_f16(_p(rv), _p(av), _p(gv), _p(wgu), _p(wd), _p(b), _p(hidden),
+                                                     _p(out), h, i, float(eps), _p(pos), _p(length),
+                                                     _stream(residual)), name)
     return hidden.view(*residual.shape[:-1], i), out.view(*residual.shape[:-1], n)
 
 

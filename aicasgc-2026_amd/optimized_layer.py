@@ -31,6 +31,7 @@ import torch.nn.functional as F
 import cuda_decode_attention
 import cuda_decode_gemv
 import cuda_decode_small_ops
+from cuda_decode_gemv_ops import fused as fused_ops
 
 
 @dataclass(slots=True)
@@ -128,6 +129,16 @@ class OptimizedDecoderLayer(nn.Module):
         return None
 
     @staticmethod
+    def _length_word(layer, pos: torch.Tensor):
+        """The StaticLayer's running length when it is one int64 word beside
+        ``pos`` on the device: the layer's last kernel then advances it."""
+        cl = getattr(layer, "cumulative_length", None)
+        if torch.is_tensor(cl) and cl.device == pos.device and cl.dtype == torch.int64 and cl.numel() == 1 \
+                and cl.is_contiguous():
+            return cl
+        return None
+
+    @staticmethod
     def _advance_length(layer, pos: torch.Tensor) -> None:
         """Keep the StaticLayer's running length at pos + 1 after the HIP step
         wrote row ``pos``, as StaticLayer.update would: transformers reads it
@@ -158,14 +169,18 @@ class OptimizedDecoderLayer(nn.Module):
                                        hidden_states.new_empty(1, self.num_kv_heads, 1, self.head_dim))
             pos = self._decode_position(layer, cache_position, hidden_states.device) if layer is not None else None
             if pos is not None:
-                out = self._decode_step(hidden_states, position_embeddings, (layer.keys, layer.values), pos)
-                self._advance_length(layer, pos)
+                length = self._length_word(layer, pos)
+                out = self._decode_step(hidden_states, position_embeddings, (layer.keys, layer.values), pos, length)
+                if length is None:
+                    self._advance_length(layer, pos)
                 return out
         return self._general_forward(hidden_states, position_embeddings, attention_mask, position_ids,
                                      past_key_values, use_cache, cache_position, **kwargs)
 
     # ------------------------------------------------------------ HIP decode chain
-    def _decode_step(self, hidden_states, position_embeddings, kv, cache_position):
+    def _decode_step(self, hidden_states, position_embeddings, kv, cache_position, length=None):
+        """The HIP decode chain of one layer; with ``length`` (the cache's
+        running-length word) its last kernel also sets length = position + 1."""
         cos, sin = position_embeddings
         k_cache, v_cache = kv
         eps = self.rms_norm_eps
@@ -184,9 +199,11 @@ class OptimizedDecoderLayer(nn.Module):
         attn = attn.reshape(1, 1, self.q_size)
         o = cuda_decode_gemv.nosplit_matvec_half(attn, self.o_proj_weight, self.o_proj_bias,
                                                  workspace=self._o_proj_workspace)
-        _hidden, out = cuda_decode_gemv.fused_post_attn_mlp_softsync_half(
-            hidden_states, o, self.post_attn_layernorm_weight, self.gate_up_weight, self.down_proj_weight,
-            self.down_proj_bias, eps, workspace=self._post_attn_mlp_workspace)
+        _hidden, out = fused_ops._post_attn_mlp(
+            "fused_post_attn_mlp_softsync_half", hidden_states, o, self.post_attn_layernorm_weight,
+            self.gate_up_weight, self.down_proj_weight, self.down_proj_bias, eps, self._post_attn_mlp_workspace,
+            "fused_post_attn_mlp_softsync",
+            next_position=None if length is None else (cache_position, length))
         return out
 
     # ------------------------------------------------------------ general (prefill) path

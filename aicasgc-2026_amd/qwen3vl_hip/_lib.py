@@ -39,6 +39,7 @@ _SIGS = {
     "qd_splitk_matvec_f16": (c_int, [P, P, P, P, P, c_int, c_int, c_int, P]),
     "qd_rmsnorm_matvec_f16": (c_int, [P, P, P, P, P, c_int, c_int, c_float, P]),
     "qd_post_attn_mlp_f16": (c_int, [P, P, P, P, P, P, P, P, c_int, c_int, c_float, P]),
+    "qd_post_attn_mlp_next_f16": (c_int, [P, P, P, P, P, P, P, P, c_int, c_int, c_float, P, P, P]),
     "qd_gateup_silu_down_f16": (c_int, [P, P, P, P, P, P, c_int, c_int, P]),
     "qd_add_rmsnorm_matvec_f16": (c_int, [P, P, P, P, P, P, P, c_int, c_int, c_float, P]),
     "qd_silu_matvec_f16": (c_int, [P, P, P, P, c_int, c_int, P]),

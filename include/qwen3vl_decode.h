@@ -82,6 +82,20 @@ int qd_post_attn_mlp_f16(const void* residual, const void* attn, const void* gam
                          void* hidden_out, void* out, int H, int I, float eps,
                          void* stream);
 
+/* qd_post_attn_mlp_f16 that also sets next_position[0] = position[0] + 1
+ * (int64 device words; they may be the same word) from its last kernel, after
+ * every earlier launch of the layer has read the position.  For a decoder
+ * layer that is the last user of its cache's write row: the swapped
+ * OptimizedDecoderLayer advances its StaticLayer's cumulative_length this way,
+ * as transformers' StaticLayer.update (cache_utils.py) does on the reference
+ * path (OptimizedDecoderLayer.forward, optimized_layer.py:108-469, then the
+ * cache update), without two extra launches per layer. */
+int qd_post_attn_mlp_next_f16(const void* residual, const void* attn, const void* gamma,
+                              const void* W_gu, const void* W_d, const void* bias,
+                              void* hidden_out, void* out, int H, int I, float eps,
+                              const int64_t* position, int64_t* next_position,
+                              void* stream);
+
 /* hidden = silu(W_gu[:I] x) * (W_gu[I:] x); out = W_d hidden (+ bias).  fp16
  * I/O, bias may be NULL.  Replaces fused_gateup_silu_downproj_half and its
  * persistent / softsync / gridsync / mega variants

@@ -111,6 +111,27 @@ def test_fused_post_attn_mlp(cuda):
         assert_close_rel(out.reshape(-1), ro, what=f"{fn.__name__} out")
 
 
+def test_post_attn_mlp_advances_the_running_length(cuda):
+    """qd_post_attn_mlp_next_f16: the same outputs as qd_post_attn_mlp_f16
+    (bit for bit) plus length = position + 1, also when both are one word (the
+    StaticLayer's cumulative_length read and advanced in place)."""
+    from cuda_decode_gemv_ops import fused
+    from qwen3vl_hip import synthetic as syn
+
+    lw = syn.layer_weights(0, 0)
+    args = (syn.normal(0, ("residual",), (1, 1, 2048)).to(cuda), syn.normal(0, ("attn",), (1, 1, 2048)).to(cuda),
+            lw.post_attn_layernorm_weight.to(cuda), lw.gate_up_weight.to(cuda), lw.down_proj_weight.to(cuda), None,
+            1e-6)
+    hid0, out0 = fused._post_attn_mlp("post_attn_mlp", *args, None, "plain")
+    pos = torch.tensor([777], dtype=torch.int64, device=cuda)
+    length = torch.tensor(-5, dtype=torch.int64, device=cuda)
+    hid1, out1 = fused._post_attn_mlp("post_attn_mlp", *args, None, "next", next_position=(pos, length))
+    assert torch.equal(hid0, hid1) and torch.equal(out0, out1)
+    assert int(length) == 778 and int(pos) == 777
+    _, out2 = fused._post_attn_mlp("post_attn_mlp", *args, None, "same", next_position=(length, length))
+    assert torch.equal(out0, out2) and int(length) == 779
+
+
 def test_fused_post_attn_mlp_bias_and_workspace_reuse(cuda):
     import cuda_decode_gemv as g
     from qwen3vl_hip import synthetic as syn
