@@ -183,9 +183,15 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
   // rotary pair j is a per-lane vector load: a scalar load is waited for with
   // every other outstanding scalar load, and the K/V addressing has some.)
   long rpj = 0;
+  float cs_c = 0.f, cs_s = 0.f;   // given cos / sin of slot j (a.cos set)
   if constexpr (FUSED_ROPE) {
-    ifq = a.inv_freq[j];
-    rpj = rope_pos[mrope_stream(j, a.sec_h, a.sec_w)];
+    if (a.cos != nullptr) {
+      cs_c = h2f(a.cos[(long)bq * kD + j]);
+      cs_s = h2f(a.sin[(long)bq * kD + j]);
+    } else {
+      ifq = a.inv_freq[j];
+      rpj = rope_pos[mrope_stream(j, a.sec_h, a.sec_w)];
+    }
 #pragma unroll
     for (int i = 0; i < kPre; ++i) {
       const int item = w + 4 * i;
@@ -216,8 +222,8 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
   __shared__ float s_q[G][kD];
   __shared__ __align__(16) uint16_t s_kv[2][kD];   // new token's K_rot and V, fp16 as cached
   if constexpr (FUSED_ROPE) {
-    float c, s;
-    sincosf((float)rpj * ifq, &s, &c);
+    float c = cs_c, s = cs_s;
+    if (a.cos == nullptr) sincosf((float)rpj * ifq, &s, &c);
 #pragma unroll
     for (int i = 0; i < kPre; ++i) {
       const int item = w + 4 * i;

@@ -403,6 +403,30 @@ int qd_attention_decode(const void* q, int q_dtype, long q_stride, const void* k
                              : qd::attention_merge_launch<float>(a, S(stream));
 }
 
+int qd_attention_qkv_decode_f16(const void* qkv, const void* q_weight, const void* k_weight, float eps,
+                                const void* cos, const void* sin, void* k_cache, void* v_cache, long cache_stride_h,
+                                long cache_stride_s, int T, const int64_t* cache_position, float scale, void* out,
+                                int Hq, int Hkv, int n_split, void* workspace, void* stream) {
+  qd::AttnArgs a;
+  int st = attn_common(a, qkv, QD_F16, 128, k_cache, v_cache, cache_stride_h, cache_stride_s, T, cache_position,
+                       scale, Hq, Hkv, n_split);
+  if (st) return st;
+  QD_REQUIRE(q_weight && k_weight && cos && sin && out && workspace, QD_ERR_ARG, "null pointer");
+  QD_REQUIRE(Hq / Hkv == 2, QD_ERR_SHAPE, "the fused prologue serves 2 q heads per kv head (got %d)", Hq / Hkv);
+  QD_REQUIRE(a16(out), QD_ERR_ARG, "out must be 16-byte aligned");
+  a.qkv = qkv; a.q_weight = (const u16*)q_weight; a.k_weight = (const u16*)k_weight; a.eps = eps;
+  a.cos = (const u16*)cos; a.sin = (const u16*)sin;
+  a.k_w = (u16*)k_cache; a.v_w = (u16*)v_cache;
+  a.out = out;
+  attn_ws(workspace, a);
+  if (n_split <= 16 && Hkv <= 64) {
+    a.done = reinterpret_cast<unsigned*>(workspace);
+    return qd::attention_partial_launch<u16>(a, S(stream));
+  }
+  if ((st = qd::attention_partial_launch<u16>(a, S(stream)))) return st;
+  return qd::attention_merge_launch<u16>(a, S(stream));
+}
+
 int qd_attention_decode_noalloc(const void* q, int q_dtype, long q_stride, const void* k_cache,
                                 const void* v_cache, long cache_stride_h, long cache_stride_s, int T,
                                 const int64_t* cache_position, float scale, void* out, int out_dtype, int Hq, int Hkv,

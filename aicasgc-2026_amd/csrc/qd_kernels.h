@@ -78,6 +78,10 @@ struct AttnArgs {
   float eps = 1e-6f;
   const int64_t* rope_pos = nullptr;  // int64 [3]
   const float* inv_freq = nullptr;    // fp32 [64]
+  // instead of rope_pos / inv_freq: the rotation's cos / sin (fp16 [batch][128],
+  // slot j at j; the caller's rotary embedding, e.g. transformers')
+  const uint16_t* cos = nullptr;
+  const uint16_t* sin = nullptr;
   int sec_h = 20, sec_w = 20;
   uint16_t* k_w = nullptr;            // writable aliases of k / v for the new row
   uint16_t* v_w = nullptr;

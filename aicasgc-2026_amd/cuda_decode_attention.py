@@ -88,6 +88,46 @@ def _run_fused(q, k, v, scaling, num_key_value_groups, cache_position, split_k, 
     return out.unsqueeze(2).transpose(1, 2)
 
 
+def _qkv_rope_attention(qkv, q_weight, k_weight, eps: float, cos, sin, k_cache, v_cache, scaling, cache_position,
+                        split_k: int = 4, workspace: dict | None = None):
+    """q/k head RMSNorm + RoPE (the caller's cos / sin), the new K/V row written
+    to the caches at ``cache_position`` and split-KV attention, in one launch
+    (qd_attention_qkv_decode_f16): the pair fused_q_rope_kv_cache_update +
+    decode_attn_v4_cta_qhead_splitkv_fused that the decoder layer calls back to
+    back.  qkv [1, 1, (Hq + 2 Hkv) * 128] fp16; returns [1, 1, Hq, 128], or
+    None when the inputs are outside what the kernel supports."""
+    if qkv.device.type != "cuda" or qkv.dtype != torch.float16 or not qkv.is_contiguous():
+        return None
+    if k_cache.ndim != 4 or k_cache.shape[0] != 1 or k_cache.shape[-1] != 128 or k_cache.shape != v_cache.shape:
+        return None
+    hkv, T = k_cache.shape[1], k_cache.shape[2]
+    hq = qkv.shape[-1] // 128 - 2 * hkv
+    if (hq != 2 * hkv or qkv.numel() != (hq + 2 * hkv) * 128 or k_cache.dtype != torch.float16
+            or v_cache.dtype != torch.float16 or k_cache.stride(-1) != 1 or k_cache.stride() != v_cache.stride()
+            or k_cache.stride(1) % 8 or k_cache.stride(2) % 8 or k_cache.data_ptr() % 16 or v_cache.data_ptr() % 16
+            or qkv.data_ptr() % 16):
+        return None
+    if not (cache_position.device.type == "cuda" and cache_position.dtype == torch.long
+            and cache_position.numel() == 1):
+        return None
+    norms = (q_weight, k_weight)
+    if any(t.dtype != torch.float16 or t.numel() != 128 or t.device != qkv.device for t in norms):
+        return None
+    if any(t.dtype != torch.float16 or t.numel() != 128 or t.device != qkv.device for t in (cos, sin)):
+        return None
+    lib = _load_ext()
+    n_split = _splits(T, split_k)
+    out = _out_buffer(workspace, qkv.view(1, hq + 2 * hkv, 1, 128)[:, :hq])
+    ws = _ws_buffer(workspace, qkv, int(lib.qd_attention_workspace_bytes(hq, hkv, n_split)))
+    qw, kw = q_weight.contiguous(), k_weight.contiguous()   # held until the launch is enqueued
+    cs, sn, cp = cos.contiguous(), sin.contiguous(), cache_position.contiguous()
+    _lib.check(lib.qd_attention_qkv_decode_f16(
+        _lib.ptr(qkv), _lib.ptr(qw), _lib.ptr(kw), float(eps), _lib.ptr(cs), _lib.ptr(sn), _lib.ptr(k_cache),
+        _lib.ptr(v_cache), k_cache.stride(1), k_cache.stride(2), T, _lib.ptr(cp), float(scaling), _lib.ptr(out),
+        hq, hkv, n_split, _lib.ptr(ws), _lib.stream(qkv.device)), "qd_attention_qkv_decode_f16")
+    return out.unsqueeze(2).transpose(1, 2)
+
+
 def decode_attn_v4_cta_qhead_splitkv_fused(q, k, v, scaling, num_key_value_groups, cache_position, split_k: int = 4,
                                            workspace: dict | None = None):
     """Reference cuda_decode_attention.py:489-558 (default decode attention)."""

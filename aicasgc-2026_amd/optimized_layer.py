@@ -186,14 +186,20 @@ class OptimizedDecoderLayer(nn.Module):
         eps = self.rms_norm_eps
         qkv = cuda_decode_gemv.fused_rmsnorm_qkv_half(hidden_states, self.input_layernorm_weight, self.qkv_weight,
                                                       None, eps)
-        q, k, v = qkv.split([self.q_size, self.kv_size, self.kv_size], dim=-1)
-        q_rot = cuda_decode_small_ops.fused_q_rope_kv_cache_update(
-            q.view(1, 1, self.num_heads, self.head_dim), k.view(1, 1, self.num_kv_heads, self.head_dim),
-            v.view(1, 1, self.num_kv_heads, self.head_dim), self.q_norm_weight, self.k_norm_weight, eps,
-            cos.reshape(1, 1, 128), sin.reshape(1, 1, 128), k_cache, v_cache, cache_position)
-        attn = cuda_decode_attention.decode_attn_v4_cta_qhead_splitkv_fused(
-            q_rot.transpose(1, 2), k_cache, v_cache, self.scaling, self.num_key_value_groups, cache_position,
-            split_k=4, workspace=self._attention_workspace)
+        # q/k norm + RoPE + K/V write + attention in one launch; the two-call
+        # form (the reference's own sequence) where that kernel does not apply
+        attn = cuda_decode_attention._qkv_rope_attention(
+            qkv, self.q_norm_weight, self.k_norm_weight, eps, cos.reshape(128), sin.reshape(128), k_cache, v_cache,
+            self.scaling, cache_position, split_k=4, workspace=self._attention_workspace)
+        if attn is None:
+            q, k, v = qkv.split([self.q_size, self.kv_size, self.kv_size], dim=-1)
+            q_rot = cuda_decode_small_ops.fused_q_rope_kv_cache_update(
+                q.view(1, 1, self.num_heads, self.head_dim), k.view(1, 1, self.num_kv_heads, self.head_dim),
+                v.view(1, 1, self.num_kv_heads, self.head_dim), self.q_norm_weight, self.k_norm_weight, eps,
+                cos.reshape(1, 1, 128), sin.reshape(1, 1, 128), k_cache, v_cache, cache_position)
+            attn = cuda_decode_attention.decode_attn_v4_cta_qhead_splitkv_fused(
+                q_rot.transpose(1, 2), k_cache, v_cache, self.scaling, self.num_key_value_groups, cache_position,
+                split_k=4, workspace=self._attention_workspace)
         if attn is None:
             raise RuntimeError("decode attention inputs unsupported by the HIP kernel")
         attn = attn.reshape(1, 1, self.q_size)

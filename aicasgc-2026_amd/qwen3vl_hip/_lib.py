@@ -56,6 +56,8 @@ _SIGS = {
     "qd_attention_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
     "qd_attention_decode": (c_int, [P, c_int, c_long, P, P, c_long, c_long, c_int, P, c_float, P, c_int,
                                     c_int, c_int, c_int, P, P]),
+    "qd_attention_qkv_decode_f16": (c_int, [P, P, P, c_float, P, P, P, P, c_long, c_long, c_int, P, c_float, P,
+                                            c_int, c_int, c_int, P, P]),
     "qd_attention_decode_noalloc": (c_int, [P, c_int, c_long, P, P, c_long, c_long, c_int, P, c_float, P,
                                             c_int, c_int, c_int, c_int, P]),
     "qd_attention_partial": (c_int, [P, c_int, c_long, P, P, c_long, c_long, c_int, P, c_float, P, P,

@@ -204,6 +204,25 @@ int qd_attention_decode(const void* q, int q_dtype, long q_stride,
                         void* out, int out_dtype, int Hq, int Hkv, int n_split,
                         void* workspace, void* stream);
 
+/* One decoder layer's attention from its raw qkv projection, in one launch
+ * (two when n_split > 16): per-head RMSNorm of q and k (q_weight / k_weight,
+ * 128 fp16 each, eps) and rotate-half RoPE with the caller's cos / sin (fp16
+ * [128]: transformers' rotary embedding for the new token), the new K_rot and
+ * V row written to the fp16 caches at cache_position[0], then qd_attention_decode
+ * with the rotated q kept in fp32 (the new row comes from registers, not from
+ * the cache).  qkv: fp16 [Hq*128 | Hkv*128 | Hkv*128]; Hq = 2 Hkv; out fp16
+ * [Hq,128]; workspace as for qd_attention_decode.  Replaces the pair
+ * fused_q_rope_kv_cache_update (cuda_decode_small_ops.py:136-225) +
+ * decode_attn_v4_cta_qhead_splitkv_fused (cuda_decode_attention.py:489-558)
+ * that OptimizedDecoderLayer.forward calls back to back
+ * (optimized_layer.py:108-469). */
+int qd_attention_qkv_decode_f16(const void* qkv, const void* q_weight, const void* k_weight,
+                                float eps, const void* cos, const void* sin,
+                                void* k_cache, void* v_cache,
+                                long cache_stride_h, long cache_stride_s, int T,
+                                const int64_t* cache_position, float scale, void* out,
+                                int Hq, int Hkv, int n_split, void* workspace, void* stream);
+
 /* qd_attention_decode without a workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  No counterpart in the reference, which

@@ -114,6 +114,46 @@ def test_attention_graph_replay_self_resets(cuda, T, split_k):
         assert_close_rel(got, O.decode_attention(q.reshape(16, 128), kc, vc, pos, SCALE), what=f"replay pos={pos}")
 
 
+@pytest.mark.parametrize("pos,cap", [(0, 64), (700, 1024), (4095, 4096)])
+def test_qkv_rope_attention_matches_the_two_call_sequence(cuda, pos, cap):
+    """The one-launch q/k norm + RoPE + K/V write + attention of the drop-in
+    layer against the reference's two calls (fused_q_rope_kv_cache_update,
+    then decode attention) on the same inputs: identical cache rows (V exact,
+    K within one fp16 step), attention within the bar (the one-launch form
+    keeps the rotated q in fp32), and against the oracle."""
+    import cuda_decode_attention as A
+    import cuda_decode_small_ops as S
+    from qwen3vl_hip import synthetic as syn
+
+    print(f"case qkv attention pos={pos} cap={cap}", flush=True)
+    lw = syn.layer_weights(4, 0)
+    qkv = syn.normal(4, ("x", pos), (1, 1, 4096)).to(cuda)
+    cos, sin = O.mrope_cos_sin(torch.tensor([[pos + 9], [pos + 3], [pos + 5]]))
+    cos16, sin16 = cos.half().reshape(128).to(cuda), sin.half().reshape(128).to(cuda)
+    kc = syn.normal(4, ("k", pos), (1, 8, cap, 128))
+    vc = syn.normal(4, ("v", pos), (1, 8, cap, 128))
+    kc[:, :, pos:] = 7.0   # stale rows at and after the new position
+    vc[:, :, pos:] = -7.0
+    cp = torch.tensor([pos], dtype=torch.int64, device=cuda)
+    qn, kn = lw.q_norm_weight.to(cuda), lw.k_norm_weight.to(cuda)
+    k1, v1 = kc.to(cuda), vc.to(cuda)
+    one = A._qkv_rope_attention(qkv, qn, kn, 1e-6, cos16, sin16, k1, v1, SCALE, cp, workspace={})
+    assert one is not None and one.shape == (1, 1, 16, 128)
+    k2, v2 = kc.to(cuda), vc.to(cuda)
+    q, k, v = qkv.split([2048, 1024, 1024], dim=-1)
+    q_rot = S.fused_q_rope_kv_cache_update(q.view(1, 1, 16, 128), k.view(1, 1, 8, 128), v.view(1, 1, 8, 128),
+                                           qn, kn, 1e-6, cos16.view(1, 1, 128), sin16.view(1, 1, 128), k2, v2, cp)
+    two = A.decode_attn_v4_cta_qhead_splitkv_fused(q_rot.transpose(1, 2), k2, v2, SCALE, 2, cp, workspace={})
+    torch.cuda.synchronize()
+    assert torch.equal(v1.cpu(), v2.cpu())
+    assert torch.equal(k1[:, :, :pos].cpu(), k2[:, :, :pos].cpu()) and torch.equal(k1[:, :, pos + 1:].cpu(),
+                                                                                  k2[:, :, pos + 1:].cpu())
+    assert_close_rel(k1[0, :, pos].float().cpu(), k2[0, :, pos].float().cpu(), rel=2.0 ** -10, what="new K row")
+    assert_close_rel(one.reshape(16, 128).float().cpu(), two.reshape(16, 128).float().cpu(), what="one vs two calls")
+    ref = O.decode_attention(q_rot.reshape(16, 128).float().cpu(), k2.cpu(), v2.cpu(), pos, SCALE)
+    assert_close_rel(one.reshape(16, 128).float().cpu(), ref, what="one launch vs oracle")
+
+
 def test_attention_unsupported_returns_none(cuda):
     import cuda_decode_attention as A
     from qwen3vl_hip import synthetic as syn
