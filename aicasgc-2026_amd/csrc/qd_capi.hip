@@ -606,6 +606,8 @@ int qd_decode_workspace_layout(const qd_model_desc* d, size_t* offsets, int n) {
 
 namespace {
 
+bool persistent_device_unsupported(char* why, size_t n);
+
 // Why the persistent step cannot serve this descriptor on the current device
 // (empty when it can).
 bool persistent_unsupported(const qd_model_desc* d, char* why, size_t n) {
@@ -624,6 +626,13 @@ bool persistent_unsupported(const qd_model_desc* d, char* why, size_t n) {
     snprintf(why, n, "persistent step supports 1..%d layers", qd::kPersistMaxLayers);
     return true;
   }
+  return persistent_device_unsupported(why, n);
+}
+
+// Why the current device cannot keep the persistent grid resident (empty when
+// it can); the occupancy query runs once per device.
+bool persistent_device_unsupported(char* why, size_t n) {
+  why[0] = 0;
   static std::mutex mu;
   static std::vector<int> verdict;  // per device: 0 unknown, 1 ok, 2 unsupported
   static std::vector<std::string> reason;
@@ -700,6 +709,17 @@ int persist_area(hipStream_t s, unsigned** out, unsigned** out_ctrl) {
   return QD_OK;
 }
 
+// The hand-off buffers of a launch, carved from the per-device area.
+void set_handoff_words(qd::PersistArgs& p, unsigned* t) {
+  p.x_t = t; t += qd::kPersistHidden;
+  p.qkv_t = t; t += (qd::kPersistHeads + 2 * qd::kPersistKvHeads) * qd::kPersistHeadDim;
+  p.opart_t = t; t += (size_t)qd::kPersistHeads * qd::kPersistSplits * qd::kPersistHeadDim;
+  p.lse_t = t; t += qd::kPersistHeads * qd::kPersistSplits;
+  p.att_t = t; t += qd::kPersistHeads * qd::kPersistHeadDim;
+  p.r_t = t; t += qd::kPersistHidden;
+  p.hid_t = t;
+}
+
 int launch_persistent(const qd_model_desc* d, const StepBuffers& b, hipStream_t s) {
   qd::PersistArgs p;
   memset(&p, 0, sizeof(p));
@@ -725,13 +745,7 @@ int launch_persistent(const qd_model_desc* d, const StepBuffers& b, hipStream_t 
   unsigned *t = nullptr, *ctrl = nullptr;
   int st = persist_area(s, &t, &ctrl);
   if (st) return st;
-  p.x_t = t; t += qd::kPersistHidden;
-  p.qkv_t = t; t += (qd::kPersistHeads + 2 * qd::kPersistKvHeads) * qd::kPersistHeadDim;
-  p.opart_t = t; t += (size_t)qd::kPersistHeads * qd::kPersistSplits * qd::kPersistHeadDim;
-  p.lse_t = t; t += qd::kPersistHeads * qd::kPersistSplits;
-  p.att_t = t; t += qd::kPersistHeads * qd::kPersistHeadDim;
-  p.r_t = t; t += qd::kPersistHidden;
-  p.hid_t = t;
+  set_handoff_words(p, t);
   p.x_out = b.x;
   p.status = b.control;
   p.generation = ctrl;
@@ -921,6 +935,50 @@ int qd_decode_layers_persistent(const qd_model_desc* d, void* stream) {
   size_t total = 0;
   step_layout(d, splits_of(d), &b, &total);
   return launch_persistent(d, b, S(stream));
+}
+
+int qd_persistent_prepare(void* stream) {
+  char why[256];
+  QD_REQUIRE(!persistent_device_unsupported(why, sizeof(why)), QD_ERR_SHAPE, "%s", why);
+  unsigned *t = nullptr, *ctrl = nullptr;
+  return persist_area(S(stream), &t, &ctrl);
+}
+
+int qd_decoder_layer_persistent_f16(const void* hidden_in, const qd_layer_weights* w, int capacity,
+                                    const int64_t* cache_position, const void* cos, const void* sin, float eps,
+                                    float scale, void* hidden_out, int64_t* length_out, unsigned* status,
+                                    void* stream) {
+  QD_REQUIRE(hidden_in && w && cache_position && cos && sin && hidden_out && status, QD_ERR_ARG, "null pointer");
+  QD_REQUIRE(w->qkv && w->o_proj && w->gate_up && w->down && w->input_norm && w->post_norm && w->q_norm &&
+                 w->k_norm && w->k_cache && w->v_cache,
+             QD_ERR_ARG, "null layer weight or cache pointer");
+  QD_REQUIRE(capacity >= 1, QD_ERR_SHAPE, "cache capacity %d", capacity);
+  char why[256];
+  QD_REQUIRE(!persistent_device_unsupported(why, sizeof(why)), QD_ERR_SHAPE, "%s", why);
+  qd::PersistArgs p;
+  memset(&p, 0, sizeof(p));
+  p.layers[0] = qd::PersistLayer{(const u16*)w->qkv,        (const u16*)w->o_proj,    (const u16*)w->gate_up,
+                                 (const u16*)w->down,       (const u16*)w->input_norm, (const u16*)w->post_norm,
+                                 (const u16*)w->q_norm,     (const u16*)w->k_norm,    (u16*)w->k_cache,
+                                 (u16*)w->v_cache};
+  p.num_layers = 1;
+  p.T = capacity;
+  p.eps = eps;
+  p.scale = scale;
+  p.cache_position = cache_position;
+  p.x_in = (const u16*)hidden_in;
+  p.rope_cos = (const u16*)cos;
+  p.rope_sin = (const u16*)sin;
+  p.x_out16 = (u16*)hidden_out;
+  p.length_out = length_out;
+  unsigned *t = nullptr, *ctrl = nullptr;
+  int st = persist_area(S(stream), &t, &ctrl);
+  if (st) return st;
+  set_handoff_words(p, t);
+  p.status = status;
+  p.generation = ctrl;
+  p.done = ctrl + 1;
+  return qd::decode_persistent_layer_launch(p, S(stream));
 }
 
 int qd_decode_status(const qd_model_desc* d, unsigned* status, int reset) {

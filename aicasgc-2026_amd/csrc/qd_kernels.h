@@ -187,6 +187,15 @@ struct PersistArgs {
   // parity follows it) and the workgroups finished in this launch (self-resetting)
   unsigned* generation;
   unsigned* done;
+  // one-layer launch of the drop-in decoder layer (the kernel's LAYER
+  // instance): the layer input instead of the embedding row, transformers'
+  // cos / sin instead of the M-RoPE positions, the output in fp16, and the
+  // cache's running length set to cache_position + 1 after the layer
+  const uint16_t* x_in;           // fp16 [H]
+  const uint16_t* rope_cos;       // fp16 [D] (two equal halves)
+  const uint16_t* rope_sin;       // fp16 [D]
+  uint16_t* x_out16;              // fp16 [H]
+  int64_t* length_out;            // int64 [1] or null
 };
 
 // Model shape the persistent kernel is specialised for, and its grid.
@@ -200,6 +209,9 @@ constexpr size_t kPersistTaggedWords = kPersistHidden                           
                                        + kPersistHidden + kPersistInter;                              // r, hid
 
 int decode_persistent_launch(const PersistArgs& a, hipStream_t s);
+// The same kernel's one-layer instance for the drop-in decoder layer (x_in,
+// rope_cos / rope_sin, x_out16 and length_out set; num_layers 1).
+int decode_persistent_layer_launch(const PersistArgs& a, hipStream_t s);
 
 // ---------------------------------------------------------------- batch step
 

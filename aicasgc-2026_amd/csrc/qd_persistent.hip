@@ -18,8 +18,10 @@
 //
 // Hand-off between workgroups is fence-free.  Every produced value is one
 // 32-bit word: the fp32 value with its mantissa LSB replaced by the parity of
-// the write (a change of at most one ulp), stored with a relaxed agent-scope
-// atomic store.  Consumers read 16 bytes per lane with device-coherent (sc1)
+// the write, stored with a relaxed agent-scope atomic store; readers clear
+// that bit again, so every reader uses the value with its LSB cleared (a
+// change of at most one ulp, the same in every launch).  Consumers read 16
+// bytes per lane with device-coherent (sc1)
 // buffer loads and poll until every word shows the parity they expect; no
 // release/acquire (L2 write-back / invalidate) is ever issued.  Each buffer is
 // written once per layer and every reader reads the same words at every layer,
@@ -34,6 +36,12 @@
 // Every wait is bounded: a thread polls at most kSpinLimit times per launch,
 // then records an error in the status word and continues, so the grid always
 // drains.
+//
+// A second instance of the kernel (LAYER) runs one decoder layer for the
+// drop-in layer's forward: its input is the caller's fp16 hidden state
+// instead of an embedding row, the rotation uses the caller's cos / sin
+// (transformers' rotary embedding), its output is fp16, and the last
+// workgroup sets the cache's running length to cache_position + 1.
 
 #include <float.h>
 #include <math.h>
@@ -125,9 +133,11 @@ __device__ __forceinline__ unsigned peek1(Rsrc r, unsigned off) {
 __device__ __forceinline__ bool parity_ok(u32x4 v, unsigned par) {
   return (((v.x ^ par) | (v.y ^ par) | (v.z ^ par) | (v.w ^ par)) & 1u) == 0u;
 }
-// Whole-vector cast: casting the elements one by one (bit_cast of v.y, ...)
-// is folded to v.x by this compiler.
-__device__ __forceinline__ f32x4 values_of(u32x4 v) { return __builtin_bit_cast(f32x4, v); }
+// The values of four words, their tag bit cleared: every reader then uses the
+// same value whichever parity the write carried, so a launch's results do not
+// depend on the launches before it.  Whole-vector cast: casting the elements
+// one by one (bit_cast of v.y, ...) is folded to v.x by this compiler.
+__device__ __forceinline__ f32x4 values_of(u32x4 v) { return __builtin_bit_cast(f32x4, v & ~1u); }
 
 // A per-lane value the compiler must treat as new at this point: keeps it from
 // hoisting per-lane address arithmetic out of the layer loop (where it would
@@ -192,7 +202,7 @@ __device__ __forceinline__ float take1(Rsrc r, unsigned i, unsigned par, Spin& s
     __builtin_amdgcn_s_sleep(1);
     v = peek1(r, i * 4u);
   }
-  return __builtin_bit_cast(float, v);
+  return __builtin_bit_cast(float, v & ~1u);
 }
 
 // THREADS threads (ids t = 0..THREADS-1) gather N * THREADS * 4 words into
@@ -330,7 +340,7 @@ struct Ctx {
 // and in one shared loop the compiler would have to keep each group's
 // loop-carried weight registers live on the other group's path as well.
 // Both instances execute the same sequence of workgroup barriers.
-template <bool STREAM>
+template <bool STREAM, bool LAYER>
 __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& cx, Smem& sm, Spin& sp) {
   const int w = cx.w, gw = cx.gw, kvh = cx.kvh, split = cx.split, t0 = cx.t0, t1 = cx.t1, mh = cx.mh,
             md0 = cx.md0;
@@ -449,10 +459,14 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
     QD_TRACE_ST(l, 0);
     QD_FRESH_LANE();
     if (l == 0) {
-      long tok = a.token[0];
-      if (tok < 0 || tok >= a.vocab) tok = 0;
-      const uint16_t* row = a.embed + tok * (long)H;
-      for (int i = tid; i < H; i += NW * kWave) s_x[i] = h2f(row[i]);
+      if constexpr (LAYER) {
+        for (int i = tid; i < H; i += NW * kWave) s_x[i] = h2f(a.x_in[i]);
+      } else {
+        long tok = a.token[0];
+        if (tok < 0 || tok >= a.vocab) tok = 0;
+        const uint16_t* row = a.embed + tok * (long)H;
+        for (int i = tid; i < H; i += NW * kWave) s_x[i] = h2f(row[i]);
+      }
     } else if (!streamer) {
       gather4<H / (4 * NA * kWave), NA * kWave>(r_x, s_x, (unsigned)tid, par ^ 1u, sp);
     }
@@ -721,7 +735,10 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
       if (lane == 0) {
         const float v = y[0] + s_r[gw];
         put(a.x_t + gw, par, v);
-        if (l + 1 == a.num_layers) a.x_out[gw] = v;
+        if (l + 1 == a.num_layers) {
+          if constexpr (LAYER) a.x_out16[gw] = f2h(v);
+          else a.x_out[gw] = v;
+        }
       }
       QD_TRACE_ST(l, 15);
       if (!streamer) {
@@ -738,6 +755,7 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
 
 }  // namespace
 
+template <bool LAYER>
 __global__ __launch_bounds__(512) void decode_persistent_kernel(const PersistArgs a) {
   const int b = blockIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform: branches on it are scalar
@@ -761,7 +779,11 @@ __global__ __launch_bounds__(512) void decode_persistent_kernel(const PersistArg
   cx.t1 = min(cx.t0 + chunk, L);
   cx.mh = b / (D / MERGE_DIMS);               // merged q head of this workgroup
   cx.md0 = (b % (D / MERGE_DIMS)) * MERGE_DIMS;
-  {
+  if constexpr (LAYER) {
+    // the caller's rotation of pair `lane` (cos / sin repeat over the two halves)
+    cx.rc = h2f(a.rope_cos[lane]);
+    cx.rs = h2f(a.rope_sin[lane]);
+  } else {
     // M-RoPE angle of rotary pair `lane` (the same for every layer of the step)
     int stream = 0;
     if (lane % 3 == 1 && lane < 3 * a.sec_h) stream = 1;
@@ -769,25 +791,34 @@ __global__ __launch_bounds__(512) void decode_persistent_kernel(const PersistArg
     sincosf((float)a.rope_position[stream] * a.inv_freq[lane], &cx.rs, &cx.rc);
   }
 
-  if (w >= NA) persist_layers<true>(a, cx, sm, sp);
-  else persist_layers<false>(a, cx, sm, sp);
+  if (w >= NA) persist_layers<true, LAYER>(a, cx, sm, sp);
+  else persist_layers<false, LAYER>(a, cx, sm, sp);
 
   // The last workgroup to finish advances the generation by this launch's
   // layer count.  Every workgroup read the generation before it produced
-  // anything, so none can read the new value in this launch.
+  // anything, so none can read the new value in this launch.  The same holds
+  // for the cache position, which the LAYER instance then advances.
   __syncthreads();
   if (tid == 0) {
     const unsigned n = __hip_atomic_fetch_add(a.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (n == NB - 1) {
       __hip_atomic_store(a.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(a.generation, cx.gen + (unsigned)a.num_layers, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if constexpr (LAYER) {
+        if (a.length_out != nullptr) *a.length_out = cx.pos + 1;
+      }
     }
   }
 }
 
 int decode_persistent_launch(const PersistArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(decode_persistent_kernel, dim3(NB), dim3(NW * kWave), 0, s, a);
+  hipLaunchKernelGGL(decode_persistent_kernel<false>, dim3(NB), dim3(NW * kWave), 0, s, a);
   return qd_host::launch_status("decode_persistent_kernel");
+}
+
+int decode_persistent_layer_launch(const PersistArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL(decode_persistent_kernel<true>, dim3(NB), dim3(NW * kWave), 0, s, a);
+  return qd_host::launch_status("decode_persistent_kernel<LAYER>");
 }
 
 extern "C" int qd_persistent_trace_read(uint64_t* dst, size_t n, int* dims) {
@@ -819,8 +850,12 @@ int decode_persistent_check_device(char* why, size_t why_len) {
   int dev = 0, cus = 0, per_cu = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  int per_cu_layer = 0;
   if (e == hipSuccess)
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_persistent_kernel, NW * kWave, 0);
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_persistent_kernel<false>, NW * kWave, 0);
+  if (e == hipSuccess)
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_layer, decode_persistent_kernel<true>, NW * kWave, 0);
+  if (per_cu_layer < per_cu) per_cu = per_cu_layer;
   if (e != hipSuccess) {
     snprintf(why, why_len, "device query failed: %s", hipGetErrorString(e));
     return 1;

@@ -9,7 +9,11 @@ get identical results.
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
+
+from qwen3vl_hip import _lib
 
 from .matvec import nosplit_matvec_half
 from .runtime import _check, _contig_weight, _load_ext, _p, _require_decode_half, _reuse, _stream
@@ -203,18 +207,100 @@ def fused_o_proj_post_attn_mlp_softsync_half(residual, attn_input, o_proj_weight
                                  workspace)
 
 
+_FULL_LAYER_KIND = "fused_decode_full_layer_softsync"
+_PERSISTENT_DEVICE_OK: dict = {}   # device index -> the one-layer persistent launch runs there
+
+
+def _persistent_layer_device_ok(device: torch.device) -> bool:
+    """Whether the one-layer persistent launch runs on ``device``.  The first
+    call per device (outside stream capture) allocates the device's persistent
+    hand-off area (qd_persistent_prepare); under capture before that, False."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    ok = _PERSISTENT_DEVICE_OK.get(idx)
+    if ok is None:
+        if torch.cuda.is_current_stream_capturing():
+            return False
+        st = _load_ext().qd_persistent_prepare(_lib.stream(device))
+        if st not in (0, _lib.QD_ERR_SHAPE):
+            _check(st, "qd_persistent_prepare")
+        ok = _PERSISTENT_DEVICE_OK[idx] = st == 0
+    return ok
+
+
+def _full_layer_persistent(hidden_states, qkv_weight, input_layernorm_weight, q_norm_weight, k_norm_weight, cos,
+                           sin, k_cache, v_cache, cache_position, o_proj_weight, o_proj_bias, post_attn_norm_weight,
+                           gate_up_weight, down_proj_weight, down_proj_bias, eps, attn_scale, workspace=None,
+                           length=None):
+    """One Qwen3-VL-2B decoder layer as one persistent launch
+    (qd_decoder_layer_persistent_f16), or None where it does not apply: the
+    reference's eligibility of its one-launch layer (optimized_layer.py:1511-1600:
+    fp16 GPU tensors at the 2B shapes, contiguous last dims, static [1, 8, T, 128]
+    caches, one cache position) with no biases, contiguous caches and a device
+    that keeps the grid resident.  ``length``: the cache's running-length word,
+    set to position + 1 by the launch.  The output and the status word live in
+    ``workspace`` (stable addresses for graph capture)."""
+    h = hidden_states
+    if not (h.device.type == "cuda" and h.dtype == torch.float16 and h.numel() == 2048 and h.shape[-1] == 2048
+            and o_proj_bias is None and down_proj_bias is None):
+        return None
+    mats = ((qkv_weight, (4096, 2048)), (o_proj_weight, (2048, 2048)), (gate_up_weight, (12288, 2048)),
+            (down_proj_weight, (2048, 6144)))
+    vecs = ((input_layernorm_weight, 2048), (post_attn_norm_weight, 2048), (q_norm_weight, 128),
+            (k_norm_weight, 128), (cos, 128), (sin, 128))
+    if not all(t.device == h.device and t.dtype == torch.float16 and tuple(t.shape) == shp and t.is_contiguous()
+               for t, shp in mats):
+        return None
+    if not all(t.device == h.device and t.dtype == torch.float16 and t.numel() == n and t.is_contiguous()
+               for t, n in vecs):
+        return None
+    if not all(c.device == h.device and c.dtype == torch.float16 and c.ndim == 4 and c.shape[0] == 1
+               and c.shape[1] == 8 and c.shape[3] == 128 and c.is_contiguous() for c in (k_cache, v_cache)):
+        return None
+    if k_cache.shape != v_cache.shape or not (cache_position.device == h.device and cache_position.numel() == 1
+                                              and cache_position.dtype == torch.int64):
+        return None
+    if length is not None and not (length.device == h.device and length.dtype == torch.int64
+                                   and length.numel() == 1):
+        return None
+    if not _persistent_layer_device_ok(h.device):
+        return None
+    ws = workspace if workspace is not None else {}
+    if not (ws.get("type") == _FULL_LAYER_KIND and "out" in ws and "status" in ws and ws["out"].device == h.device):
+        ws.clear()
+        ws.update(type=_FULL_LAYER_KIND, out=torch.empty(2048, dtype=torch.float16, device=h.device),
+                  status=torch.zeros(1, dtype=torch.int32, device=h.device))
+    out = ws["out"]
+    x = h.reshape(-1)
+    w = _lib.LayerDesc(qkv=qkv_weight.data_ptr(), o_proj=o_proj_weight.data_ptr(), gate_up=gate_up_weight.data_ptr(),
+                       down=down_proj_weight.data_ptr(), input_norm=input_layernorm_weight.data_ptr(),
+                       post_norm=post_attn_norm_weight.data_ptr(), q_norm=q_norm_weight.data_ptr(),
+                       k_norm=k_norm_weight.data_ptr(), k_cache=k_cache.data_ptr(), v_cache=v_cache.data_ptr())
+    _check(_load_ext().qd_decoder_layer_persistent_f16(
+        _p(x), ctypes.byref(w), int(k_cache.shape[2]), _p(cache_position), _p(cos), _p(sin), float(eps),
+        float(attn_scale), _p(out), _p(length), _p(ws["status"]), _stream(h)), "fused_decode_full_layer_softsync_half")
+    return out.view(*h.shape[:-1], 2048)
+
+
 def fused_decode_full_layer_softsync_half(hidden_states, qkv_weight, input_layernorm_weight, q_norm_weight,
                                           k_norm_weight, cos, sin, k_cache, v_cache, cache_position, o_proj_weight,
                                           o_proj_bias, post_attn_norm_weight, gate_up_weight, down_proj_weight,
                                           down_proj_bias, eps, attn_scale, workspace=None, launch_blocks=None):
-    """One full decoder layer for one token (reference fused.py:498-665): the
-    layer chain of QKV, q/k norm + RoPE + KV write, attention, o_proj and MLP."""
+    """One full decoder layer for one token (reference fused.py:498-665): QKV,
+    q/k norm + RoPE + KV write, attention, o_proj and MLP.  At the Qwen3-VL-2B
+    shapes this is one persistent launch (the reference's one-launch soft-sync
+    layer); elsewhere the layer chain of the separate kernels."""
     import cuda_decode_attention
     import cuda_decode_small_ops
 
     del launch_blocks
     name = "fused_decode_full_layer_softsync_half"
     _require_decode_half(name, hidden_states, qkv_weight, x=hidden_states)
+    out = _full_layer_persistent(hidden_states, qkv_weight, input_layernorm_weight, q_norm_weight, k_norm_weight,
+                                 cos, sin, k_cache, v_cache, cache_position, o_proj_weight, o_proj_bias,
+                                 post_attn_norm_weight, gate_up_weight, down_proj_weight, down_proj_bias, eps,
+                                 attn_scale, workspace)
+    if out is not None:
+        return out
     hkv, d = k_cache.shape[1], k_cache.shape[3]
     hq = (qkv_weight.shape[0] - 2 * hkv * d) // d
     qkv = fused_rmsnorm_qkv_half(hidden_states, input_layernorm_weight, qkv_weight, None, eps).reshape(-1)

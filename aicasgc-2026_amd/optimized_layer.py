@@ -5,8 +5,11 @@ wraps an HF ``Qwen3VLTextDecoderLayer`` (same constructor, same forward
 signature, fused qkv / gate_up weights as at optimized_layer.py:60-84), and
 ``replace_decoder_layers`` swaps it into a model.
 
-Decode step (one token, batch 1, fp16, GPU, static KV cache; the chain of
-optimized_layer.py:108-469):
+Decode step (one token, batch 1, fp16, GPU, static KV cache; optimized_layer.py:108-469).
+At the Qwen3-VL-2B shapes the whole layer is one persistent launch, the
+reference's one-launch layer fused_decode_full_layer_softsync_half (tried
+first, :127-154); otherwise, or with the ``full_layer_softsync`` fusion flag
+off, the chain:
 
     fused_rmsnorm_qkv_half            RMSNorm + QKV GEMV        (HIP)
     fused_q_rope_kv_cache_update      q/k norm + RoPE + KV write (HIP)
@@ -93,6 +96,7 @@ class OptimizedDecoderLayer(nn.Module):
         self._attention_workspace: dict = {}
         self._post_attn_mlp_workspace: dict = {"type": "fused_post_attn_mlp_softsync"}
         self._o_proj_workspace: dict = {"type": "nosplit"}
+        self._full_layer_workspace: dict = {}
 
     # ------------------------------------------------------------ dispatch
     def _static_layer(self, past_key_values, k_like: torch.Tensor):
@@ -179,11 +183,19 @@ class OptimizedDecoderLayer(nn.Module):
 
     # ------------------------------------------------------------ HIP decode chain
     def _decode_step(self, hidden_states, position_embeddings, kv, cache_position, length=None):
-        """The HIP decode chain of one layer; with ``length`` (the cache's
+        """The HIP decode step of one layer; with ``length`` (the cache's
         running-length word) its last kernel also sets length = position + 1."""
         cos, sin = position_embeddings
         k_cache, v_cache = kv
         eps = self.rms_norm_eps
+        if _FUSION_FLAGS["full_layer_softsync"]:
+            out = fused_ops._full_layer_persistent(
+                hidden_states, self.qkv_weight, self.input_layernorm_weight, self.q_norm_weight, self.k_norm_weight,
+                cos, sin, k_cache, v_cache, cache_position, self.o_proj_weight, self.o_proj_bias,
+                self.post_attn_layernorm_weight, self.gate_up_weight, self.down_proj_weight, self.down_proj_bias,
+                eps, self.scaling, self._full_layer_workspace, length=length)
+            if out is not None:
+                return out
         qkv = cuda_decode_gemv.fused_rmsnorm_qkv_half(hidden_states, self.input_layernorm_weight, self.qkv_weight,
                                                       None, eps)
         # q/k norm + RoPE + K/V write + attention in one launch; the two-call
@@ -289,7 +301,10 @@ def set_small_decode_triton_enabled(model, enabled: bool) -> bool:
 _FUSION_FLAG_NAMES = ("add_rmsnorm_gateup", "full_layer_softsync", "post_attn_mlp_persistent",
                       "o_proj_post_attn_mlp_persistent", "o_proj_post_attn_mlp_softsync", "silu_downproj",
                       "gateup_silu_downproj", "gateup_silu_downproj_mega")
-_FUSION_FLAGS = {n: n == "post_attn_mlp_persistent" for n in _FUSION_FLAG_NAMES}
+# full_layer_softsync: the swapped layer's decode step is one persistent launch
+# where the shapes allow (on by default here: on MI355X it is faster than the
+# kernel chain; the reference's A800 default was off)
+_FUSION_FLAGS = {n: n in ("post_attn_mlp_persistent", "full_layer_softsync") for n in _FUSION_FLAG_NAMES}
 
 
 def set_cuda_mlp_fusion_flags(*, add_rmsnorm_gateup: bool | None = None, full_layer_softsync: bool | None = None,
@@ -299,9 +314,10 @@ def set_cuda_mlp_fusion_flags(*, add_rmsnorm_gateup: bool | None = None, full_la
                               gateup_silu_downproj: bool | None = None,
                               gateup_silu_downproj_mega: bool | None = None) -> tuple:
     """Reference optimized_layer.py:3876-3921: sets the MLP fusion choices and
-    returns the previous 8-tuple.  Every choice computes the same math on
-    gfx950 (the decode chain above); the flags are recorded for callers that
-    read them back."""
+    returns the previous 8-tuple.  ``full_layer_softsync`` selects the
+    one-launch layer (on by default) or the kernel chain; the other choices
+    compute the same math on gfx950 and are recorded for callers that read
+    them back."""
     prev = tuple(_FUSION_FLAGS[n] for n in _FUSION_FLAG_NAMES)
     new = dict(add_rmsnorm_gateup=add_rmsnorm_gateup, full_layer_softsync=full_layer_softsync,
                post_attn_mlp_persistent=post_attn_mlp_persistent,

@@ -27,6 +27,7 @@ PHASE = {"embed": 0x01, "qkv": 0x02, "attn": 0x04, "attn_merge": 0x08, "o_proj":
          "down": 0x40, "lm_head": 0x80}
 PHASE_ALL = 0xFF
 STEP_AUTO, STEP_CHAIN, STEP_PERSISTENT = 0, 1, 2
+QD_ERR_ARG, QD_ERR_SHAPE = -1, -2
 
 P = c_void_p
 
@@ -71,6 +72,8 @@ _SIGS = {
     "qd_decode_advance": (c_int, [P, P, P, P, P, c_int, P]),
     "qd_decode_step_mode": (c_int, [P]),
     "qd_decode_layers_persistent": (c_int, [P, P]),
+    "qd_decoder_layer_persistent_f16": (c_int, [P, P, c_int, P, P, P, c_float, c_float, P, P, P, P]),
+    "qd_persistent_prepare": (c_int, [P]),
     "qd_decode_status": (c_int, [P, POINTER(ctypes.c_uint), c_int]),
     "qd_persistent_trace_read": (c_int, [P, c_size_t, POINTER(c_int)]),
     "qd_batch_gemv_workspace_bytes": (ctypes.c_size_t, [c_long, c_long]),

@@ -373,7 +373,8 @@ def dropin_text_model(w, device):
 def bench_dropin(w, prompt, k_caches, v_caches, first: int, steps: int, warmup: int, golden) -> dict:
     """The reference's own decode loop over the drop-in layers: one step of the
     swapped transformers model (embedding, M-RoPE cos/sin, 28 swapped layers,
-    final norm, tied lm_head in fp16, argmax) captured in a HIP graph and
+    final norm, the tied lm_head through the drop-in nosplit_matvec_half as the
+    reference's FastLmHead does, argmax) captured in a HIP graph and
     replayed with the static input buffers rewritten on the device between
     replays (DecodeCudaGraphRunner, evaluation_wrapper.py:864-904, :941-960).
     It continues from the native engine's prefilled K/V rows, so its tokens are
@@ -381,6 +382,8 @@ def bench_dropin(w, prompt, k_caches, v_caches, first: int, steps: int, warmup: 
     fp16 activations between kernels, as the reference does)."""
     import torch
     from transformers.cache_utils import StaticCache
+
+    import cuda_decode_gemv
 
     dev = k_caches[0].device
     model, cfg = dropin_text_model(w, dev)
@@ -402,12 +405,15 @@ def bench_dropin(w, prompt, k_caches, v_caches, first: int, steps: int, warmup: 
     next_token = torch.zeros(1, 1, dtype=torch.int64, device=dev)
     out_tokens = torch.zeros(n, dtype=torch.int64, device=dev)
     emb = w.embed_tokens
+    lm_head_ws = {"type": "nosplit", "out": torch.empty(emb.shape[0], dtype=emb.dtype, device=dev)}
 
     def run():
         out = model(input_ids=ids, attention_mask=mask, position_ids=position_ids, past_key_values=cache,
                     use_cache=True, cache_position=cache_position)
-        logits = out.last_hidden_state[:, -1] @ emb.T
-        next_token.copy_(torch.argmax(logits, dim=-1, keepdim=True))
+        # the reference's FastLmHead (evaluation_wrapper.py:1210-1238): the tied lm_head as one
+        # cuda_decode_gemv.nosplit_matvec_half into a workspace output, then torch.argmax (:952)
+        logits = cuda_decode_gemv.nosplit_matvec_half(out.last_hidden_state, emb, None, workspace=lm_head_ws)
+        next_token.copy_(torch.argmax(logits[:, -1, :], dim=-1, keepdim=True))
 
     def write_inputs(p):   # the runner's _write_inputs: device-side copies and fills, no host sync
         ids.copy_(next_token)
@@ -415,41 +421,64 @@ def bench_dropin(w, prompt, k_caches, v_caches, first: int, steps: int, warmup: 
         position_ids.fill_(p + prompt.rope_delta)
         mask[:, p] = 1
 
-    next_token.fill_(first)
-    write_inputs(S)
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side), torch.no_grad():
-        run()                      # warm-up of lazy initialisation, outside the capture
-    torch.cuda.current_stream().wait_stream(side)
-    torch.cuda.synchronize()
-    next_token.fill_(first)
-    write_inputs(S)
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph), torch.no_grad():
-        run()
-    next_token.fill_(first)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    for i in range(n):
-        if i == warmup:
-            e0.record()
-        write_inputs(S + i)
-        graph.replay()
-        out_tokens[i].copy_(next_token[0, 0])
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / steps
-    toks = out_tokens.tolist()
+    def timed(one_launch: bool):
+        """Capture the step with the swapped layers on one decode path (the
+        one-launch persistent layer, or the kernel chain) and time its replays
+        from the prompt's end; returns (ms per token, tokens)."""
+        import optimized_layer
+
+        prev = optimized_layer.set_cuda_mlp_fusion_flags(full_layer_softsync=one_launch)
+        try:
+            next_token.fill_(first)
+            write_inputs(S)
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side), torch.no_grad():
+                run()                      # warm-up of lazy initialisation, outside the capture
+            torch.cuda.current_stream().wait_stream(side)
+            torch.cuda.synchronize()
+            next_token.fill_(first)
+            write_inputs(S)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph), torch.no_grad():
+                run()
+        finally:
+            optimized_layer.set_cuda_mlp_fusion_flags(full_layer_softsync=prev[1])
+        next_token.fill_(first)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        for i in range(n):
+            if i == warmup:
+                e0.record()
+            write_inputs(S + i)
+            graph.replay()
+            out_tokens[i].copy_(next_token[0, 0])
+        e1.record()
+        torch.cuda.synchronize()
+        del graph
+        return e0.elapsed_time(e1) / steps, out_tokens.tolist()
+
     gold = golden["tokens"][1:1 + n]
-    match = next((i for i, (a, b) in enumerate(zip(toks, gold)) if a != b), min(len(toks), len(gold)))
-    del graph, model, cache
+    res = {}
+    for label, one_launch in (("one_launch", True), ("chain", False)):
+        ms, toks = timed(one_launch)
+        match = next((i for i, (a, b) in enumerate(zip(toks, gold)) if a != b), min(len(toks), len(gold)))
+        res[label] = (ms, match, min(len(toks), len(gold)))
+    fused_layers = sum(1 for L in model.layers if L._full_layer_workspace.get("out") is not None)
+    del model, cache
     torch.cuda.empty_cache()
+    ms, match, n_cmp = res["one_launch"]
     return {"method": "transformers Qwen3VLTextModel with every decoder layer swapped by "
                       "optimized_layer.replace_decoder_layers, one step captured in a HIP graph, static input "
                       "buffers rewritten on the device between replays (the reference's DecodeCudaGraphRunner); "
-                      "fp16 tied lm_head + torch.argmax in the graph; HIP events over the timed steps",
+                      "tied lm_head through cuda_decode_gemv.nosplit_matvec_half (the reference's FastLmHead) + "
+                      "torch.argmax in the graph; HIP events over the timed steps",
+            "layer_path": "one persistent launch per swapped layer (fused_decode_full_layer_softsync_half)",
+            "layers_on_one_launch_path": fused_layers,
             "ms_per_token": round(ms, 4), "tokens_per_s": round(1000.0 / ms, 1), "steps": steps, "warmup": warmup,
-            "context_start": S, "tokens_match_golden_prefix": match, "tokens_compared": min(len(toks), len(gold))}
+            "context_start": S, "tokens_match_golden_prefix": match, "tokens_compared": n_cmp,
+            "chain": {"layer_path": "kernel chain per swapped layer (full_layer_softsync fusion flag off)",
+                      "ms_per_token": round(res["chain"][0], 4),
+                      "tokens_match_golden_prefix": res["chain"][1], "tokens_compared": res["chain"][2]}}
 
 
 def phase_trace(contexts) -> list:
@@ -696,8 +725,11 @@ def main() -> int:
     dropin = None
     if args.dropin_steps > 0:
         dropin = bench_dropin(w, prompt, eng.k_caches, eng.v_caches, first, args.dropin_steps, 4, gold)
-        log(f"drop-in (transformers model + swapped layers, HIP graph): {dropin['ms_per_token']:.4f} ms/token, "
-            f"golden prefix {dropin['tokens_match_golden_prefix']}/{dropin['tokens_compared']}")
+        log(f"drop-in (transformers model + swapped layers, HIP graph): {dropin['ms_per_token']:.4f} ms/token "
+            f"one launch per layer ({dropin['layers_on_one_launch_path']} layers), "
+            f"{dropin['chain']['ms_per_token']:.4f} ms/token kernel chain; golden prefix "
+            f"{dropin['tokens_match_golden_prefix']} / {dropin['chain']['tokens_match_golden_prefix']} of "
+            f"{dropin['tokens_compared']}")
 
     # ---- config 4: 8 sequences, ragged contexts L_i ~ U[2048, 4096]
     b8 = None

@@ -384,6 +384,38 @@ int qd_decode_step_mode(const qd_model_desc* d);
  * 28, optimized_layer.py:108-469). */
 int qd_decode_layers_persistent(const qd_model_desc* d, void* stream);
 
+/* One Qwen3-VL-2B decoder layer for one token as one persistent launch (the
+ * kernel of qd_decode_layers_persistent, one layer): hidden_in fp16 [2048] ->
+ * hidden_out fp16 [2048], with RMSNorm + QKV, q/k head RMSNorm + RoPE by the
+ * caller's cos / sin (fp16 [128] each, two equal halves as transformers'
+ * rotary embedding makes them), the new K/V row written into w->k_cache /
+ * w->v_cache ([8, capacity, 128]) at *cache_position, attention over rows
+ * 0..min(*cache_position, capacity - 1) scaled by `scale`, o_proj + residual,
+ * RMSNorm + gate_up + SiLU*up, down + residual; activations stay fp32 between
+ * the phases.  length_out (nullable): set to *cache_position + 1 after every
+ * workgroup has read *cache_position (a static cache's running length; it may
+ * be the same word as cache_position).  status: a device word the caller
+ * zeroes; bit 0 is set when a hand-off wait ran out of its polling budget
+ * (the output is then invalid).  Shares the per-device hand-off area and its
+ * rules with qd_decode_layers_persistent (the first persistent launch on a
+ * device must not be under stream capture: qd_persistent_prepare).
+ * QD_ERR_SHAPE when the device cannot keep the grid resident.  Replaces
+ * cuda_decode_gemv.fused_decode_full_layer_softsync_half
+ * (cuda_decode_gemv_ops/fused.py:498-665), the one-launch decoder layer that
+ * OptimizedDecoderLayer.forward tries first (optimized_layer.py:127-154,
+ * :1490-1610). */
+int qd_decoder_layer_persistent_f16(const void* hidden_in, const qd_layer_weights* w, int capacity,
+                                    const int64_t* cache_position, const void* cos, const void* sin, float eps,
+                                    float scale, void* hidden_out, int64_t* length_out, unsigned* status,
+                                    void* stream);
+
+/* Allocates and zeroes the current device's persistent hand-off area if it is
+ * not there yet (outside stream capture; synchronous the first time), so that
+ * later persistent launches may be captured.  QD_ERR_SHAPE when the device
+ * cannot keep the persistent grid resident.  No counterpart in the reference
+ * (its soft-sync kernels take their counters from the caller's workspace). */
+int qd_persistent_prepare(void* stream);
+
 /* Phase timeline of the persistent step, for profiling.  A library built with
  * -DQD_TRACE (libqwen3vl_decode_trace.so, made by the package's build step
  * next to the main library) has the first thread of wave 0 (a polling wave)

@@ -46,7 +46,18 @@ def _hf_layer(lw):
     return layer
 
 
-def test_optimized_decoder_layer_config0(cuda):
+@pytest.fixture(params=[True, False], ids=["one_launch", "chain"])
+def layer_path(request):
+    """The swapped layer's two decode paths: the one-launch persistent layer
+    (default) and the kernel chain (full_layer_softsync fusion flag off)."""
+    import optimized_layer
+
+    prev = optimized_layer.set_cuda_mlp_fusion_flags(full_layer_softsync=request.param)
+    yield request.param
+    optimized_layer.set_cuda_mlp_fusion_flags(full_layer_softsync=prev[1])
+
+
+def test_optimized_decoder_layer_config0(cuda, layer_path):
     import optimized_layer
     from qwen3vl_hip import synthetic as syn
 
@@ -69,7 +80,7 @@ def test_optimized_decoder_layer_config0(cuda):
     assert torch.equal(kc[0, :, :512].cpu(), inp.k_cache[0, :, :512])
 
 
-def test_optimized_decoder_layer_with_transformers_static_cache(cuda):
+def test_optimized_decoder_layer_with_transformers_static_cache(cuda, layer_path):
     """The drop-in layer on transformers' own StaticCache (lazily initialised by
     the layer on its first call): three consecutive decode steps, each reading
     the K/V rows the previous ones wrote, against the oracle step by step."""
