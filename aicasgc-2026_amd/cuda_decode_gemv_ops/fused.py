@@ -262,6 +262,15 @@ def _full_layer_persistent(hidden_states, qkv_weight, input_layernorm_weight, q_
     if length is not None and not (length.device == h.device and length.dtype == torch.int64
                                    and length.numel() == 1):
         return None
+    with torch.cuda.device(h.device):   # the persistent hand-off area is per device: the current one
+        return _full_layer_launch(h, qkv_weight, input_layernorm_weight, q_norm_weight, k_norm_weight, cos, sin,
+                                  k_cache, v_cache, cache_position, o_proj_weight, post_attn_norm_weight,
+                                  gate_up_weight, down_proj_weight, eps, attn_scale, workspace, length)
+
+
+def _full_layer_launch(h, qkv_weight, input_layernorm_weight, q_norm_weight, k_norm_weight, cos, sin, k_cache,
+                       v_cache, cache_position, o_proj_weight, post_attn_norm_weight, gate_up_weight,
+                       down_proj_weight, eps, attn_scale, workspace, length):
     if not _persistent_layer_device_ok(h.device):
         return None
     ws = workspace if workspace is not None else {}

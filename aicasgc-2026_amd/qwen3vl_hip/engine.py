@@ -161,7 +161,8 @@ class DecodeEngine(_CapturedSteps):
     @property
     def step_mode(self) -> str:
         """The mode qd_decode_step runs in on this device ("chain" or "persistent")."""
-        m = _lib.lib().qd_decode_step_mode(ctypes.byref(self.desc))
+        with torch.cuda.device(self.device):   # the library's per-device state follows the current device
+            m = _lib.lib().qd_decode_step_mode(ctypes.byref(self.desc))
         if m < 0:
             _lib.check(m, "qd_decode_step_mode")
         return "persistent" if m == _lib.STEP_PERSISTENT else "chain"
@@ -176,8 +177,9 @@ class DecodeEngine(_CapturedSteps):
     def layers_persistent(self) -> None:
         """Enqueue embedding + all layers as one persistent launch (x left in buffers()["x"])."""
         st = torch.cuda.current_stream(self.device).cuda_stream
-        _lib.check(_lib.lib().qd_decode_layers_persistent(ctypes.byref(self.desc), ctypes.c_void_p(st)),
-                   "qd_decode_layers_persistent")
+        with torch.cuda.device(self.device):
+            _lib.check(_lib.lib().qd_decode_layers_persistent(ctypes.byref(self.desc), ctypes.c_void_p(st)),
+                       "qd_decode_layers_persistent")
 
     # ------------------------------------------------------------ state
     def set_state(self, token: int, cache_position: int, rope_position: int) -> None:
@@ -203,7 +205,8 @@ class DecodeEngine(_CapturedSteps):
     def step_eager(self) -> None:
         """Enqueue one decode step + advance on the current stream."""
         st = torch.cuda.current_stream(self.device).cuda_stream
-        _lib.check(_lib.lib().qd_decode_step(ctypes.byref(self.desc), ctypes.c_void_p(st)), "qd_decode_step")
+        with torch.cuda.device(self.device):
+            _lib.check(_lib.lib().qd_decode_step(ctypes.byref(self.desc), ctypes.c_void_p(st)), "qd_decode_step")
         if self.desc.advance_counter:
             return
         _lib.check(_lib.lib().qd_decode_advance(
