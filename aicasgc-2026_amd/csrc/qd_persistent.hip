@@ -89,6 +89,7 @@ constexpr unsigned kSpinLimit = 1u << 16;  // polls per thread and launch (tens 
 
 static_assert(NQKV == 2 * NTH, "QKV: two rows per wave");
 static_assert(H == NTH, "o_proj / down: one row per wave");
+static_assert(H == 4 * NW * kWave, "one-layer launch: 4 input values per thread");
 static_assert(I == 3 * NTH, "gate_up: three row pairs per wave");
 static_assert(MERGE_DIMS == 8, "merge: 8 dims per workgroup");
 
@@ -327,6 +328,17 @@ struct __align__(16) Smem {
   uint16_t gpost[H];          // post-attention RMSNorm weight of the current layer
 };
 
+// Rows [t0, t1) of the attended length min(pos + 1, T) that split `split`
+// (of NS) of a kv head covers.
+__device__ __forceinline__ void split_window(const PersistArgs& a, long pos, int split, int& t0, int& t1) {
+  long Ll = pos + 1 < (long)a.T ? pos + 1 : (long)a.T;
+  if (Ll < 0) Ll = 0;
+  const int L = (int)Ll;
+  const int chunk = (L + NS - 1) / NS;
+  t0 = split * chunk;
+  t1 = min(t0 + chunk, L);
+}
+
 // Per-workgroup constants of a launch.
 struct Ctx {
   int w, gw, kvh, split, t0, t1, mh, md0;
@@ -341,11 +353,13 @@ struct Ctx {
 // loop-carried weight registers live on the other group's path as well.
 // Both instances execute the same sequence of workgroup barriers.
 template <bool STREAM, bool LAYER>
-__device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& cx, Smem& sm, Spin& sp) {
-  const int w = cx.w, gw = cx.gw, kvh = cx.kvh, split = cx.split, t0 = cx.t0, t1 = cx.t1, mh = cx.mh,
-            md0 = cx.md0;
-  const long pos = cx.pos;
-  const unsigned gen = cx.gen;
+__device__ __forceinline__ void persist_layers(const PersistArgs& a, Ctx& cx, Smem& sm, Spin& sp,
+                                               uint2 x_first) {
+  const int w = cx.w, gw = cx.gw, kvh = cx.kvh, split = cx.split, mh = cx.mh, md0 = cx.md0;
+  // (LAYER: read below, once the first weight rows are in flight)
+  int t0 = cx.t0, t1 = cx.t1;
+  long pos = cx.pos;
+  unsigned gen = cx.gen;
   const float rc = cx.rc, rs = cx.rs;
   constexpr bool streamer = STREAM;
   const bool poller = (w == 0);     // polls the split partials (MERGE) and the merged output
@@ -431,14 +445,41 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
   // RMSNorm weights of a layer are staged in LDS by the polling waves: 16 bytes
   // of each vector per thread, loaded together with their W_down rows of the
   // previous layer and written after the DOWN hand-off.
+  // (LAYER: stored after the first weight rows are issued, so no wave waits for
+  // them before its W_qkv rows are in flight)
+  u32x4 gi0 = {0u, 0u, 0u, 0u}, gp0 = {0u, 0u, 0u, 0u};
   if (!streamer) {
-    const u32x4 gi = ld16(a.layers[0].input_norm + tid * 8);
-    const u32x4 gp = ld16(a.layers[0].post_norm + tid * 8);
-    *reinterpret_cast<u32x4*>(s_gin + tid * 8) = gi;
-    *reinterpret_cast<u32x4*>(s_gpost + tid * 8) = gp;
+    gi0 = ld16(a.layers[0].input_norm + tid * 8);
+    gp0 = ld16(a.layers[0].post_norm + tid * 8);
+    if constexpr (!LAYER) {
+      *reinterpret_cast<u32x4*>(s_gin + tid * 8) = gi0;
+      *reinterpret_cast<u32x4*>(s_gpost + tid * 8) = gp0;
+    }
   }
   issue_qkv(a.layers[0], H);
+  if constexpr (LAYER) {
+    // the layer generation and the cache position, by vector loads issued
+    // behind the W_qkv rows: only the K/V addressing below waits for them (a
+    // scalar load would put a wait for every outstanding scalar load, which
+    // return out of order, in front of the first weight rows)
+    const Rsrc rg = rsrc_of(a.generation, 1);
+    const Rsrc rp = rsrc_of(reinterpret_cast<const unsigned*>(a.cache_position), 2);
+    const unsigned g = __builtin_amdgcn_raw_buffer_load_b32(rg, 0u, 0, 0);
+    const unsigned p0 = __builtin_amdgcn_raw_buffer_load_b32(rp, 0u, 0, 0);
+    const unsigned p1 = __builtin_amdgcn_raw_buffer_load_b32(rp, 4u, 0, 0);
+    gen = __builtin_amdgcn_readfirstlane(g);
+    pos = (long)(((unsigned long)__builtin_amdgcn_readfirstlane(p1) << 32) | __builtin_amdgcn_readfirstlane(p0));
+    split_window(a, pos, split, t0, t1);
+    cx.gen = gen;
+    cx.pos = pos;
+  }
   issue_kvwo(a.layers[0], H, t1);
+  if constexpr (LAYER) {
+    if (!streamer) {
+      *reinterpret_cast<u32x4*>(s_gin + tid * 8) = gi0;
+      *reinterpret_cast<u32x4*>(s_gpost + tid * 8) = gp0;
+    }
+  }
 
   for (int l = 0; l < a.num_layers; ++l) {
     const PersistLayer& Lw = a.layers[l];
@@ -460,7 +501,11 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, const Ctx& 
     QD_FRESH_LANE();
     if (l == 0) {
       if constexpr (LAYER) {
-        for (int i = tid; i < H; i += NW * kWave) s_x[i] = h2f(a.x_in[i]);
+        // loaded at kernel start: 4 values per thread
+        s_x[tid * 4 + 0] = h2f((uint16_t)(x_first.x & 0xffffu));
+        s_x[tid * 4 + 1] = h2f((uint16_t)(x_first.x >> 16));
+        s_x[tid * 4 + 2] = h2f((uint16_t)(x_first.y & 0xffffu));
+        s_x[tid * 4 + 3] = h2f((uint16_t)(x_first.y >> 16));
       } else {
         long tok = a.token[0];
         if (tok < 0 || tok >= a.vocab) tok = 0;
@@ -763,20 +808,30 @@ __global__ __launch_bounds__(512) void decode_persistent_kernel(const PersistArg
   const int tid = threadIdx.x;
   Spin sp{kSpinLimit, a.status};
   __shared__ Smem sm;
+  // LAYER: the layer input is every thread's first vector load (4 fp16 values),
+  // issued before the scalar reads below: loads complete in issue order, so the
+  // QKV phase waits for it and not for the weight rows issued later
+  uint2 x_first = {0u, 0u};
+  if constexpr (LAYER) {
+    x_first = *reinterpret_cast<const uint2*>(a.x_in + tid * 4);
+    __builtin_amdgcn_sched_barrier(0);
+  }
 
   Ctx cx;
   cx.w = w;
   cx.gw = b * NW + w;
-  cx.gen = a.generation[0];
-  cx.pos = a.cache_position[0];
-  long Ll = cx.pos + 1 < (long)a.T ? cx.pos + 1 : (long)a.T;
-  if (Ll < 0) Ll = 0;
-  const int L = (int)Ll;
   cx.kvh = b % HKV;
   cx.split = b / HKV;
-  const int chunk = (L + NS - 1) / NS;
-  cx.t0 = cx.split * chunk;
-  cx.t1 = min(cx.t0 + chunk, L);
+  if constexpr (LAYER) {
+    // read inside the layer loop's set-up, behind the first weight rows
+    cx.gen = 0u;
+    cx.pos = 0;
+    cx.t0 = cx.t1 = 0;
+  } else {
+    cx.gen = a.generation[0];
+    cx.pos = a.cache_position[0];
+    split_window(a, cx.pos, cx.split, cx.t0, cx.t1);
+  }
   cx.mh = b / (D / MERGE_DIMS);               // merged q head of this workgroup
   cx.md0 = (b % (D / MERGE_DIMS)) * MERGE_DIMS;
   if constexpr (LAYER) {
@@ -791,8 +846,8 @@ __global__ __launch_bounds__(512) void decode_persistent_kernel(const PersistArg
     sincosf((float)a.rope_position[stream] * a.inv_freq[lane], &cx.rs, &cx.rc);
   }
 
-  if (w >= NA) persist_layers<true, LAYER>(a, cx, sm, sp);
-  else persist_layers<false, LAYER>(a, cx, sm, sp);
+  if (w >= NA) persist_layers<true, LAYER>(a, cx, sm, sp, x_first);
+  else persist_layers<false, LAYER>(a, cx, sm, sp, x_first);
 
   // The last workgroup to finish advances the generation by this launch's
   // layer count.  Every workgroup read the generation before it produced
