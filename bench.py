@@ -249,6 +249,29 @@ def bench_configs012(w, cpu: bool, reps: int = 5) -> dict:
             raise RuntimeError("persistent one-layer step reported a failed hand-off")
     chain = ["qkv", "attn", "attn_merge", "o_proj", "gate_up", "down"]
     c0["chain_us"] = round(_graph_us([lambda e=e: e.run_phases(chain, 0, 1) for e in engines], reps), 2)
+    # the drop-in layer's one launch (cuda_decode_gemv.fused_decode_full_layer_softsync_half) on
+    # config 0's own input: a hidden state x ~ N(0, 1) and the rotation of position 512
+    from cuda_decode_gemv_ops import fused as fused_ops
+
+    f = engines[0].inv_freq * 512.0
+    cos = torch.cat([f, f]).cos().half()
+    sin = torch.cat([f, f]).sin().half()
+    cp = torch.full((1,), 512, dtype=torch.int64, device=dev)
+    xs = [torch.randn(1, 1, shape.hidden, generator=gen, device=dev).half() for _ in engines]
+    wss = [{} for _ in engines]
+
+    def one_launch(i):
+        lw, e = w.layers[i], engines[i]
+        if fused_ops._full_layer_persistent(
+                xs[i], lw.qkv_weight, lw.input_layernorm_weight, lw.q_norm_weight, lw.k_norm_weight, cos, sin,
+                e.k_caches[0], e.v_caches[0], cp, lw.o_proj_weight, None, lw.post_attn_layernorm_weight,
+                lw.gate_up_weight, lw.down_proj_weight, None, shape.rms_eps, shape.head_dim ** -0.5, wss[i]) is None:
+            raise RuntimeError("the one-launch decoder layer does not apply here")
+
+    if engines[0].step_mode == "persistent":
+        c0["dropin_one_launch_us"] = round(_graph_us([lambda i=i: one_launch(i) for i in range(len(engines))], reps), 2)
+        if any(int(ws["status"].item()) for ws in wss):
+            raise RuntimeError("one-launch decoder layer reported a failed hand-off")
     best = min(v for k, v in c0.items() if k.endswith("_us"))
     c0.update(roofline_us=round(c0["bytes"] / (PEAK_HBM_GBPS * 1e3), 2), frac=round(c0["bytes"] / (best * 1e-6) /
                                                                                         1e9 / PEAK_HBM_GBPS, 4))
