@@ -156,3 +156,40 @@ def test_full_layer_graph_replay(cuda):
                              sin16.float())
         assert_close_rel(got.reshape(-1).float().cpu(), ref, what=f"replay pos={pos}")
     assert int(ws["status"].item()) == 0
+
+
+def test_full_layer_declines_inputs_it_does_not_take(cuda):
+    """The one-launch layer returns None (the caller then runs the kernel
+    chain, as the reference's optimized_layer.py:1511-1600 falls back) for a
+    projection bias, non-contiguous cos / sin, a non-contiguous cache or a
+    non-int64 position; on its own inputs it runs."""
+    import cuda_decode_gemv_ops.fused as F
+
+    inp, cos16, sin16 = _inputs(9, 40, 64)
+    lw = inp.weights.to(cuda)
+    h = inp.hidden.to(cuda)
+    kc, vc = inp.k_cache.to(cuda), inp.v_cache.to(cuda)
+    cp = torch.tensor([40], dtype=torch.int64, device=cuda)
+    cos_d, sin_d = cos16.to(cuda), sin16.to(cuda)
+
+    def call(**kw):
+        args = dict(o_proj_bias=None, down_proj_bias=None, cos=cos_d, sin=sin_d, k_cache=kc, v_cache=vc,
+                    cache_position=cp)
+        args.update(kw)
+        return F._full_layer_persistent(h, lw.qkv_weight, lw.input_layernorm_weight, lw.q_norm_weight,
+                                        lw.k_norm_weight, args["cos"], args["sin"], args["k_cache"],
+                                        args["v_cache"], args["cache_position"], lw.o_proj_weight,
+                                        args["o_proj_bias"], lw.post_attn_layernorm_weight, lw.gate_up_weight,
+                                        lw.down_proj_weight, args["down_proj_bias"], 1e-6, SCALE, {})
+
+    bias = torch.zeros(2048, dtype=torch.float16, device=cuda)
+    assert call(o_proj_bias=bias) is None
+    assert call(down_proj_bias=bias) is None
+    strided = torch.stack([cos_d, cos_d], dim=1)[:, 0]          # 128 values, stride 2
+    assert not strided.is_contiguous() and call(cos=strided) is None
+    wide = torch.zeros(1, 8, 64, 256, dtype=torch.float16, device=cuda)[..., :128]
+    assert call(k_cache=wide) is None
+    assert call(cache_position=cp.to(torch.int32)) is None
+    out = call()
+    torch.cuda.synchronize()
+    assert out is not None and out.shape == (1, 1, 2048)
