@@ -6,6 +6,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -709,6 +710,11 @@ int persist_area(hipStream_t s, unsigned** out, unsigned** out_ctrl) {
   return QD_OK;
 }
 
+// Polls per thread and launch before a persistent wait gives up (0: the
+// kernel's default); set by qd_persistent_set_spin_limit for tests of the
+// failure path, read when a launch's arguments are built.
+std::atomic<unsigned> g_spin_limit{0};
+
 // The hand-off buffers of a launch, carved from the per-device area.
 void set_handoff_words(qd::PersistArgs& p, unsigned* t) {
   p.x_t = t; t += qd::kPersistHidden;
@@ -750,6 +756,7 @@ int launch_persistent(const qd_model_desc* d, const StepBuffers& b, hipStream_t 
   p.status = b.control;
   p.generation = ctrl;
   p.done = ctrl + 1;
+  p.spin_limit = g_spin_limit.load();
   return qd::decode_persistent_launch(p, s);
 }
 
@@ -978,7 +985,13 @@ int qd_decoder_layer_persistent_f16(const void* hidden_in, const qd_layer_weight
   p.status = status;
   p.generation = ctrl;
   p.done = ctrl + 1;
+  p.spin_limit = g_spin_limit.load();
   return qd::decode_persistent_layer_launch(p, S(stream));
+}
+
+int qd_persistent_set_spin_limit(unsigned polls) {
+  g_spin_limit.store(polls);
+  return QD_OK;
 }
 
 int qd_decode_status(const qd_model_desc* d, unsigned* status, int reset) {

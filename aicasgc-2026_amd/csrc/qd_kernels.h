@@ -196,6 +196,7 @@ struct PersistArgs {
   const uint16_t* rope_sin;       // fp16 [D]
   uint16_t* x_out16;              // fp16 [H]
   int64_t* length_out;            // int64 [1] or null
+  unsigned spin_limit;            // polls per thread and launch before a wait gives up (0: the default)
 };
 
 // Model shape the persistent kernel is specialised for, and its grid.

@@ -85,7 +85,7 @@ constexpr int NS = kPersistSplits;      // attention splits per kv head
 constexpr int SLOTS = NW * 4;           // position slots per workgroup (4 rows of 16 lanes per wave)
 constexpr int KU = 4;                   // K/V rows per slot per batch
 constexpr int MERGE_DIMS = HQ * D / NB; // dims of one head merged per workgroup
-constexpr unsigned kSpinLimit = 1u << 16;  // polls per thread and launch (tens of ms)
+constexpr unsigned kSpinLimit = 1u << 16;  // default polls per thread and launch (tens of ms)
 
 static_assert(NQKV == 2 * NTH, "QKV: two rows per wave");
 static_assert(H == NTH, "o_proj / down: one row per wave");
@@ -806,7 +806,7 @@ __global__ __launch_bounds__(512) void decode_persistent_kernel(const PersistArg
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform: branches on it are scalar
   const int lane = lane_id();
   const int tid = threadIdx.x;
-  Spin sp{kSpinLimit, a.status};
+  Spin sp{a.spin_limit != 0u ? a.spin_limit : kSpinLimit, a.status};
   __shared__ Smem sm;
   // LAYER: the layer input is every thread's first vector load (4 fp16 values),
   // issued before the scalar reads below: loads complete in issue order, so the

@@ -74,6 +74,7 @@ _SIGS = {
     "qd_decode_layers_persistent": (c_int, [P, P]),
     "qd_decoder_layer_persistent_f16": (c_int, [P, P, c_int, P, P, P, c_float, c_float, P, P, P, P]),
     "qd_persistent_prepare": (c_int, [P]),
+    "qd_persistent_set_spin_limit": (c_int, [ctypes.c_uint]),
     "qd_decode_status": (c_int, [P, POINTER(ctypes.c_uint), c_int]),
     "qd_persistent_trace_read": (c_int, [P, c_size_t, POINTER(c_int)]),
     "qd_batch_gemv_workspace_bytes": (ctypes.c_size_t, [c_long, c_long]),

@@ -193,3 +193,32 @@ def test_full_layer_declines_inputs_it_does_not_take(cuda):
     out = call()
     torch.cuda.synchronize()
     assert out is not None and out.shape == (1, 1, 2048)
+
+
+def test_full_layer_exhausted_polling_budget_is_reported(cuda):
+    """The one-launch layer with a one-poll budget (forced from the host)
+    finishes and sets bit 0 of its status word; with the default budget again
+    the next launch reports nothing and equals the oracle's layer."""
+    from qwen3vl_hip import _lib
+
+    inp, cos16, sin16 = _inputs(10, 300, 512)
+    lw = inp.weights.to(cuda)
+    h = inp.hidden.to(cuda)
+    cp = torch.tensor([300], dtype=torch.int64, device=cuda)
+    lib = _lib.lib()
+    print("case one-launch layer with a one-poll budget", flush=True)
+    _lib.check(lib.qd_persistent_set_spin_limit(1), "qd_persistent_set_spin_limit")
+    try:
+        ws: dict = {}
+        _call(lw, h, cos16.to(cuda), sin16.to(cuda), inp.k_cache.to(cuda), inp.v_cache.to(cuda), cp, ws)
+        torch.cuda.synchronize()
+    finally:
+        _lib.check(lib.qd_persistent_set_spin_limit(0), "qd_persistent_set_spin_limit")
+    assert int(ws["status"].item()) & 1, "a launch with a one-poll budget reported no exhausted wait"
+    ws = {}
+    out = _call(lw, h, cos16.to(cuda), sin16.to(cuda), inp.k_cache.to(cuda), inp.v_cache.to(cuda), cp, ws)
+    torch.cuda.synchronize()
+    assert int(ws["status"].item()) == 0
+    ref = O.decode_layer(inp.weights.tensors(), inp.hidden.reshape(-1), inp.k_cache.clone(), inp.v_cache.clone(), 300,
+                         cos16.float(), sin16.float())
+    assert_close_rel(out.reshape(-1).float().cpu(), ref, what="one-launch layer after an exhausted budget")

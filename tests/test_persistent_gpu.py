@@ -224,3 +224,42 @@ def test_generate_stops_at_eos(cuda, two_layer_weights):
         assert eng.generate(prompt, n, use_graph=False, eos_token_ids=[full[j]]) == full[:j + 1]
         assert eng.generate(prompt, n, eos_token_ids=[full[0]]) == full[:1]
         assert eng.generate(prompt, n, eos_token_ids=[-1]) == full
+
+
+def test_exhausted_polling_budget_is_reported_and_drains(cuda, two_layer_weights):
+    """A launch whose hand-off waits run out of polling budget (forced from
+    the host: one poll per thread and launch) still finishes every wave and
+    sets bit 0 of the status word; the per-device hand-off words and layer
+    generation stay consistent, so the next launch with the default budget
+    reports nothing and reproduces the earlier result bit for bit."""
+    from qwen3vl_hip import _lib
+    from qwen3vl_hip import synthetic as syn
+    from qwen3vl_hip.engine import DecodeEngine
+
+    w = two_layer_weights
+    pos, cap = 200, 256
+    eng = DecodeEngine(w, capacity=cap, step_mode="persistent")
+    assert eng.step_mode == "persistent"
+    for li in range(2):
+        eng.k_caches[li][:, :, :pos].copy_(syn.normal(13, ("k", li), (1, 8, pos, 128)))
+        eng.v_caches[li][:, :, :pos].copy_(syn.normal(13, ("v", li), (1, 8, pos, 128)))
+
+    def run():
+        eng.set_state(4321, pos, pos)
+        eng.layers_persistent()
+        torch.cuda.synchronize()
+        return eng.buffers()["x"].clone(), eng.status()
+
+    ref, st = run()
+    assert st == 0
+    lib = _lib.lib()
+    print("case persistent launch with a one-poll budget", flush=True)
+    _lib.check(lib.qd_persistent_set_spin_limit(1), "qd_persistent_set_spin_limit")
+    try:
+        _, st_bad = run()
+    finally:
+        _lib.check(lib.qd_persistent_set_spin_limit(0), "qd_persistent_set_spin_limit")
+    assert st_bad & 1, "a launch with a one-poll budget reported no exhausted wait"
+    again, st = run()
+    assert st == 0
+    assert torch.equal(again, ref)
