@@ -38,7 +38,7 @@ def _call(lw, hidden, cos16, sin16, kc, vc, cp, workspace=None):
         1e-6, SCALE, workspace=workspace)
 
 
-@pytest.mark.parametrize("pos,cap", [(0, 64), (512, 640), (4095, 4096), (8000, 8192)])
+@pytest.mark.parametrize("pos,cap", [(0, 64), (512, 640), (4095, 4096), (8000, 8192), (30000, 32768)])
 def test_full_layer_matches_oracle(cuda, pos, cap):
     """The layer output, the K/V row written at the position and the rest of
     the cache against the oracle's decoder layer on the same fp16 inputs."""

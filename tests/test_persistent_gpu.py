@@ -5,7 +5,8 @@ kernel-chain step on the same inputs.
 Cases cover the attention split edge cases of the persistent kernel (32
 splits per kv head): a context of one row (cache_position 0), fewer rows than
 splits, a context that is not a multiple of the split size, a full 4096-row
-cache and an 8000-row context (several K/V batches per split).  The lm_head's
+cache, an 8000-row context (several K/V batches per split) and a 30000-row
+context in a 32768-row cache (eight batches per split).  The lm_head's
 argmax reduction (with the fused position advance) is checked on ties, and a
 3000-step generation repeated from the same state must give identical tokens.
 """
@@ -40,7 +41,8 @@ def _oracle_step(w, token, kc, vc, pos, rope_pos):
     return h, logits, tok
 
 
-@pytest.mark.parametrize("pos,cap", [(0, 64), (5, 64), (45, 64), (1000, 1030), (4095, 4096), (8000, 8192)])
+@pytest.mark.parametrize("pos,cap", [(0, 64), (5, 64), (45, 64), (1000, 1030), (4095, 4096), (8000, 8192),
+                                     (30000, 32768)])
 def test_persistent_step_matches_oracle_and_chain(cuda, two_layer_weights, pos, cap):
     from qwen3vl_hip import synthetic as syn
     from qwen3vl_hip.engine import DecodeEngine
