@@ -26,7 +26,7 @@ def _run(fn, q, kc, vc, pos, cuda, **kw):
     return out.reshape(16, 128)
 
 
-@pytest.mark.parametrize("L", [256, 1024, 4096, 8192])
+@pytest.mark.parametrize("L", [256, 1024, 4096, 8192, 32768])   # config 2, and a 32K context
 @pytest.mark.parametrize("stale", [False, True])
 def test_attention_config2(cuda, L, stale):
     import cuda_decode_attention as A
