@@ -334,14 +334,14 @@ constexpr int kWavesPerBlock = kThreads / kWave;
 
 long ceil_div(long a, long b) { return (a + b - 1) / b; }
 
-template <int KCH, int R, int PRO, int EPI, typename TX, typename TY>
+template <int KCH, int R, int PRO, int EPI, typename TX, typename TY, bool PIPE = (EPI == EPI_ARGMAX)>
 int launch_fixed(const GemvArgs& a, int splits, long max_blocks, hipStream_t s, long* blocks_out) {
   constexpr int RO = (EPI == EPI_SILU) ? R / 2 : R;
   long blocks = ceil_div(ceil_div(a.N, RO), kWavesPerBlock);
   if (max_blocks > 0 && blocks > max_blocks) blocks = max_blocks;
   if (blocks < 1) blocks = 1;
   if (blocks_out != nullptr) *blocks_out = blocks;
-  hipLaunchKernelGGL((gemv_kernel<KCH, R, PRO, EPI, TX, TY>), dim3((unsigned)blocks, (unsigned)splits),
+  hipLaunchKernelGGL((gemv_kernel<KCH, R, PRO, EPI, TX, TY, PIPE>), dim3((unsigned)blocks, (unsigned)splits),
                      dim3(kThreads), 0, s, a);
   return qd_host::launch_status("gemv_kernel");
 }
@@ -371,6 +371,9 @@ bool has_fixed_k(int k) {
 // N = 4096: 4.9 us with 2 rows per wave, 5.0 with 4; larger N keeps 4).
 static int rows_for(long n_out) { return n_out <= 4096 ? 2 : 4; }
 
+// (A looping launch for the lm_head-sized plain GEMV, one 4-wave workgroup per
+// CU over row pairs with the next pair in flight as gemv_argmax runs, took
+// 104.6 us against 97.4 for this one-workgroup-per-row-group launch.)
 template <int PRO, typename TX, typename TY>
 int gemv_store(const GemvArgs& a, hipStream_t s) {
   if (has_fixed_k(a.K)) {
@@ -395,11 +398,14 @@ int gemv_silu(const GemvArgs& a, hipStream_t s) {
 template <int PRO, typename TX, typename TY>
 int gemv_argmax(const GemvArgs& a, hipStream_t s) {
   if (!has_fixed_k(a.K)) return QD_ERR_SHAPE;
-  // 4 blocks of 4 waves per CU, each wave looping over pairs of rows with the
-  // next pair in flight: 94.8-95.3 us for the 151936 x 2048 lm_head, against
-  // 95.6-95.9 with 6 or 8 blocks and 96.4 with 4 rows per wave at 2 blocks
-  // (same-box sweeps; 4 rows at 4 blocks: 100-102 us)
-  long max_blocks = (long)qd_host::cu_count() * 4;
+  // One block of 4 waves per CU, each wave looping over pairs of rows with the
+  // next pair in flight: 92.2-92.6 us for the 151936 x 2048 lm_head with its
+  // argmax reduction, against 95.1-95.5 with 4 blocks per CU and 96.0-96.9 with
+  // 2 or 3 (same-box sweep; 4 rows per wave: 101-102 us at 1 block, 97 at 2).
+  // A pure 16-byte streaming read of the same 622 MB peaks at 7.0-7.1 TB/s
+  // with ~32 KB in flight per CU (one 4-wave workgroup, 8 loads per lane) and
+  // drops to 5.3-6.3 TB/s with 4-16x as many workgroups.
+  long max_blocks = (long)qd_host::cu_count();
   if (max_blocks > kMaxArgmaxBlocks) max_blocks = kMaxArgmaxBlocks;
   long blocks = 0;
   int st = launch_k<2, PRO, EPI_ARGMAX, TX, TY>(a, a.K, 1, max_blocks, s, &blocks);
