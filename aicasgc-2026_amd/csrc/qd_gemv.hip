@@ -367,20 +367,15 @@ bool has_fixed_k(int k) {
 
 }  // namespace
 
-// Rows per wave chosen so that small N still spreads over every SIMD (qkv,
-// N = 4096: 4.9 us with 2 rows per wave, 5.0 with 4; larger N keeps 4).
-static int rows_for(long n_out) { return n_out <= 4096 ? 2 : 4; }
-
-// (A looping launch for the lm_head-sized plain GEMV, one 4-wave workgroup per
-// CU over row pairs with the next pair in flight as gemv_argmax runs, took
-// 104.6 us against 97.4 for this one-workgroup-per-row-group launch.)
+// Two rows per wave (8 KB of weights in flight per wave) at every N: the
+// 151936 x 2048 lm_head takes 88.9-90.2 us (6.9-7.0 TB/s, the part's streaming
+// read ceiling) against 94.7-97.2 with 4 rows and 96-98 with 8; qkv (N = 4096)
+// 4.9 us against 5.0; 12288 rows within run-to-run spread.  (A looping launch
+// for the lm_head-sized GEMV, one 4-wave workgroup per CU over row pairs with
+// the next pair in flight as gemv_argmax runs, took 104.6 us.)
 template <int PRO, typename TX, typename TY>
 int gemv_store(const GemvArgs& a, hipStream_t s) {
-  if (has_fixed_k(a.K)) {
-    const int r = rows_for(a.N);
-    return r == 2 ? launch_k<2, PRO, EPI_STORE, TX, TY>(a, a.K, 1, 0, s)
-                  : launch_k<4, PRO, EPI_STORE, TX, TY>(a, a.K, 1, 0, s);
-  }
+  if (has_fixed_k(a.K)) return launch_k<2, PRO, EPI_STORE, TX, TY>(a, a.K, 1, 0, s);
   if constexpr (PRO == PRO_ADD_RMSNORM || PRO == PRO_SILU) return QD_ERR_SHAPE;
   long blocks = ceil_div(a.N, kWavesPerBlock);
   const long cap = (long)qd_host::cu_count() * 8;
