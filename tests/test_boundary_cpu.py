@@ -46,7 +46,7 @@ def test_library_host_only_calls():
     assert lib.qd_matvec_f16(None, None, None, None, 8, 8, None) == -1
     assert b"null" in lib.qd_last_error()
     assert lib.qd_attention_merge(None, None, None, 0, 16, 4, None) == -1
-    assert lib.qd_decoder_layer_persistent_f16(None, None, None, 64, None, None, None, 1e-6, 0.088, None, None, None,
+    assert lib.qd_decoder_layer_persistent_f16(None, None, 64, None, None, None, 1e-6, 0.088, None, None, None,
                                                None) == -1
     # the persistent launches' polling budget is host state only
     assert lib.qd_persistent_set_spin_limit(0) == 0
