@@ -635,7 +635,7 @@ bool persistent_unsupported(const qd_model_desc* d, char* why, size_t n) {
 bool persistent_device_unsupported(char* why, size_t n) {
   why[0] = 0;
   static std::mutex mu;
-  static std::vector<int> verdict;  // per device: 0 unknown, 1 ok, 2 unsupported
+  static std::vector<int> support;  // per device: 0 unknown, 1 ok, 2 unsupported
   static std::vector<std::string> reason;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) {
@@ -643,17 +643,17 @@ bool persistent_device_unsupported(char* why, size_t n) {
     return true;
   }
   std::lock_guard<std::mutex> lk(mu);
-  if ((int)verdict.size() <= dev) {
-    verdict.resize(dev + 1, 0);
+  if ((int)support.size() <= dev) {
+    support.resize(dev + 1, 0);
     reason.resize(dev + 1);
   }
-  if (verdict[dev] == 0) {
+  if (support[dev] == 0) {
     char buf[256] = "";
-    verdict[dev] = qd::decode_persistent_check_device(buf, sizeof(buf)) ? 2 : 1;
+    support[dev] = qd::decode_persistent_check_device(buf, sizeof(buf)) ? 2 : 1;
     reason[dev] = buf;
   }
-  if (verdict[dev] == 2) snprintf(why, n, "%s", reason[dev].c_str());
-  return verdict[dev] == 2;
+  if (support[dev] == 2) snprintf(why, n, "%s", reason[dev].c_str());
+  return support[dev] == 2;
 }
 
 // The persistent step's hand-off words live in one area per device, in
