@@ -61,13 +61,15 @@ using u16 = uint16_t;
 inline hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
 inline bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Workspace layout of the lm_head argmax: [reserved (256 B)] [vals] [idx].
+// Workspace layout of the lm_head argmax: [header (256 B): the blocks' arrival
+// counter] [vals] [idx].
 constexpr size_t kArgmaxHeader = 256;
 size_t argmax_ws_bytes() {
   return kArgmaxHeader + (size_t)qd::kMaxArgmaxBlocks * (sizeof(float) + sizeof(long));
 }
 void argmax_ws(void* ws, GemvArgs& a) {
   char* b = reinterpret_cast<char*>(ws);
+  a.argmax_count = reinterpret_cast<unsigned*>(b);
   a.part_idx = reinterpret_cast<long*>(b + kArgmaxHeader);
   a.part_val = reinterpret_cast<float*>(b + kArgmaxHeader + (size_t)qd::kMaxArgmaxBlocks * sizeof(long));
 }

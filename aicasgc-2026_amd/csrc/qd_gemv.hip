@@ -42,17 +42,18 @@ __device__ __forceinline__ void load_rows(const GemvArgs& a, long o0, long kofs,
   }
 }
 
-// First maximal index over n per-block partials (whole block, 256 threads).
+// First maximal index over the n per-block partials that the other blocks of
+// this launch published (agent-coherent loads; whole block, 256 threads).
 // Writes a.token[0] and, when a.adv_counter is set, advances the decode state
-// as decode_advance_kernel does.
+// as decode_advance_kernel does (one launch less per decode step).
 __device__ __forceinline__ void argmax_finish(const GemvArgs& a, int n) {
   __shared__ float r_v[256];
   __shared__ long r_i[256];
   float bv = -INFINITY;
   long bi = 0x7fffffffffffL;
   for (int b = threadIdx.x; b < n; b += blockDim.x) {
-    const float v = a.part_val[b];
-    const long i = a.part_idx[b];
+    const float v = load_coherent(a.part_val + b);
+    const long i = load_coherent(a.part_idx + b);
     if (v > bv || (v == bv && i < bi)) {
       bv = v;
       bi = i;
@@ -240,9 +241,11 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
   }
 
   if constexpr (EPI == EPI_ARGMAX) {
-    // per-block (max, first index); reduced by argmax_reduce_kernel in the next launch
+    // per-block (max, first index), published with coherent stores and
+    // reduced by the last block to arrive (a.argmax_count, self-resetting)
     __shared__ float s_v[16];
     __shared__ long s_i[16];
+    __shared__ int s_last;
     if (lane == 0) {
       s_v[wib] = best_v;
       s_i[wib] = best_i;
@@ -257,17 +260,14 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
           bi = s_i[w];
         }
       }
-      a.part_val[blockIdx.x] = bv;
-      a.part_idx[blockIdx.x] = bi;
+      store_coherent(a.part_val + blockIdx.x, bv);
+      store_coherent(a.part_idx + blockIdx.x, bi);
+      stores_done();
+      s_last = arrive_last(a.argmax_count, gridDim.x);
     }
+    __syncthreads();
+    if (s_last) argmax_finish(a, (int)gridDim.x);
   }
-}
-
-// One block: the first index of the maximum over n per-block partials -> a.token[0];
-// when a.adv_counter is set it also advances the decode state as
-// decode_advance_kernel does (one launch less per decode step).
-__global__ __launch_bounds__(256) void argmax_reduce_kernel(const GemvArgs a, int n) {
-  argmax_finish(a, n);
 }
 
 // Generic fallback: any K % 8 == 0; one wave per output row, x streamed from
@@ -335,12 +335,11 @@ constexpr int kWavesPerBlock = kThreads / kWave;
 long ceil_div(long a, long b) { return (a + b - 1) / b; }
 
 template <int KCH, int R, int PRO, int EPI, typename TX, typename TY, bool PIPE = (EPI == EPI_ARGMAX)>
-int launch_fixed(const GemvArgs& a, int splits, long max_blocks, hipStream_t s, long* blocks_out) {
+int launch_fixed(const GemvArgs& a, int splits, long max_blocks, hipStream_t s) {
   constexpr int RO = (EPI == EPI_SILU) ? R / 2 : R;
   long blocks = ceil_div(ceil_div(a.N, RO), kWavesPerBlock);
   if (max_blocks > 0 && blocks > max_blocks) blocks = max_blocks;
   if (blocks < 1) blocks = 1;
-  if (blocks_out != nullptr) *blocks_out = blocks;
   hipLaunchKernelGGL((gemv_kernel<KCH, R, PRO, EPI, TX, TY, PIPE>), dim3((unsigned)blocks, (unsigned)splits),
                      dim3(kThreads), 0, s, a);
   return qd_host::launch_status("gemv_kernel");
@@ -348,15 +347,14 @@ int launch_fixed(const GemvArgs& a, int splits, long max_blocks, hipStream_t s, 
 
 // Dispatch on K (per split slice) to a register-resident kernel; R rows per wave.
 template <int R, int PRO, int EPI, typename TX, typename TY>
-int launch_k(const GemvArgs& a, int k_slice, int splits, long max_blocks, hipStream_t s,
-             long* blocks_out = nullptr) {
+int launch_k(const GemvArgs& a, int k_slice, int splits, long max_blocks, hipStream_t s) {
   switch (k_slice) {
-    case 512: return launch_fixed<1, R, PRO, EPI, TX, TY>(a, splits, max_blocks, s, blocks_out);
-    case 1024: return launch_fixed<2, R, PRO, EPI, TX, TY>(a, splits, max_blocks, s, blocks_out);
-    case 2048: return launch_fixed<4, R, PRO, EPI, TX, TY>(a, splits, max_blocks, s, blocks_out);
-    case 3072: return launch_fixed<6, (R > 2 ? 2 : R), PRO, EPI, TX, TY>(a, splits, max_blocks, s, blocks_out);
-    case 4096: return launch_fixed<8, (R > 2 ? 2 : R), PRO, EPI, TX, TY>(a, splits, max_blocks, s, blocks_out);
-    case 6144: return launch_fixed<12, (R > 2 ? 2 : R), PRO, EPI, TX, TY>(a, splits, max_blocks, s, blocks_out);
+    case 512: return launch_fixed<1, R, PRO, EPI, TX, TY>(a, splits, max_blocks, s);
+    case 1024: return launch_fixed<2, R, PRO, EPI, TX, TY>(a, splits, max_blocks, s);
+    case 2048: return launch_fixed<4, R, PRO, EPI, TX, TY>(a, splits, max_blocks, s);
+    case 3072: return launch_fixed<6, (R > 2 ? 2 : R), PRO, EPI, TX, TY>(a, splits, max_blocks, s);
+    case 4096: return launch_fixed<8, (R > 2 ? 2 : R), PRO, EPI, TX, TY>(a, splits, max_blocks, s);
+    case 6144: return launch_fixed<12, (R > 2 ? 2 : R), PRO, EPI, TX, TY>(a, splits, max_blocks, s);
     default: return 1;  // caller falls back
   }
 }
@@ -393,20 +391,19 @@ int gemv_silu(const GemvArgs& a, hipStream_t s) {
 template <int PRO, typename TX, typename TY>
 int gemv_argmax(const GemvArgs& a, hipStream_t s) {
   if (!has_fixed_k(a.K)) return QD_ERR_SHAPE;
+  if (a.argmax_count == nullptr) return QD_ERR_ARG;
   // One block of 4 waves per CU, each wave looping over pairs of rows with the
   // next pair in flight: 92.2-92.6 us for the 151936 x 2048 lm_head with its
-  // argmax reduction, against 95.1-95.5 with 4 blocks per CU and 96.0-96.9 with
-  // 2 or 3 (same-box sweep; 4 rows per wave: 101-102 us at 1 block, 97 at 2).
+  // argmax reduction in a second launch, against 95.1-95.5 with 4 blocks per CU
+  // and 96.0-96.9 with 2 or 3 (same-box sweep; 4 rows per wave: 101-102 us at
+  // 1 block, 97 at 2).  With one round of blocks none waits for another, so the
+  // last block to finish reduces the partials: 90.1-90.6 us, one launch.
   // A pure 16-byte streaming read of the same 622 MB peaks at 7.0-7.1 TB/s
   // with ~32 KB in flight per CU (one 4-wave workgroup, 8 loads per lane) and
   // drops to 5.3-6.3 TB/s with 4-16x as many workgroups.
   long max_blocks = (long)qd_host::cu_count();
   if (max_blocks > kMaxArgmaxBlocks) max_blocks = kMaxArgmaxBlocks;
-  long blocks = 0;
-  int st = launch_k<2, PRO, EPI_ARGMAX, TX, TY>(a, a.K, 1, max_blocks, s, &blocks);
-  if (st != QD_OK) return st;
-  hipLaunchKernelGGL(argmax_reduce_kernel, dim3(1), dim3(kThreads), 0, s, a, (int)blocks);
-  return qd_host::launch_status("argmax_reduce_kernel");
+  return launch_k<2, PRO, EPI_ARGMAX, TX, TY>(a, a.K, 1, max_blocks, s);
 }
 
 template <typename TX, typename TY>

@@ -29,6 +29,8 @@ struct GemvArgs {
   float eps = 1e-6f;
   float* part_val = nullptr;       // EPI_ARGMAX per-block max / EPI_PARTIAL [splits, N]
   long* part_idx = nullptr;        // EPI_ARGMAX per-block argmax
+  unsigned* argmax_count = nullptr; // EPI_ARGMAX (required): arrival counter, zeroed once and
+                                    // self-resetting; the last block to arrive reduces the partials
   int64_t* token = nullptr;        // EPI_ARGMAX result
   // EPI_ARGMAX: the argmax reduction also advances the decode state
   // (qd_decode_advance semantics) when adv_counter is set
