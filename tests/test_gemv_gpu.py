@@ -187,6 +187,7 @@ def test_lm_head_argmax_config1(cuda):
     lib = _lib.lib()
     wsp = torch.zeros(int(lib.qd_lm_head_workspace_bytes(w.shape[0])), dtype=torch.uint8, device=cuda)
     for _ in range(3):  # the arrival counter must self-reset between launches
+        tok.fill_(-1)   # a launch whose last block never reduces would leave this
         _lib.check(lib.qd_lm_head_argmax(_lib.ptr(xs), _lib.QD_F16, _lib.ptr(gs), 1e-6, _lib.ptr(ws_), w.shape[0],
                                          2048, _lib.ptr(logits), _lib.ptr(tok), _lib.ptr(wsp), _lib.stream()),
                    "lm_head")
