@@ -121,7 +121,9 @@ int qd_silu_matvec_f16(const void* gate_up, const void* W, const void* bias, voi
  *   token  = first index of max(logits)      (fp32 logits, torch.argmax order)
  * h dtype h_dtype; logits_out (fp16, may be NULL); token_out int64[1].
  * partial: workspace of qd_lm_head_workspace_bytes(V) bytes; its counter is
- * self-resetting (zero it once at allocation).  Replaces FastLmHead.forward +
+ * self-resetting (zero it once at allocation).  The last workgroup to finish
+ * reduces the partials in the same launch, so calls that share a workspace
+ * must not overlap (order them on one stream).  Replaces FastLmHead.forward +
  * torch.argmax (evaluation_wrapper.py:1227-1238, :952). */
 size_t qd_lm_head_workspace_bytes(int V);
 int qd_lm_head_argmax(const void* h, int h_dtype, const void* gamma, float eps,
