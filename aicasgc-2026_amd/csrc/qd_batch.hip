@@ -84,6 +84,52 @@ __device__ __forceinline__ float group_sum(float v) {
   }
 }
 
+// First maximal index per sequence over the nblk workgroup partials that the
+// other workgroups of this launch published (agent-coherent loads): the whole
+// 512-thread workgroup, wave b for sequence b; the result is the sequence's
+// next token.  With a.adv_counter set the workgroup then advances the decode
+// state as advance8_kernel does (one launch less per step).
+__device__ __forceinline__ void argmax8_finish(const Gemv8Args& a, int nblk) {
+  const int seq = threadIdx.x / kWave;
+  const int lane = lane_id();
+  const int64_t c = a.adv_counter != nullptr ? a.adv_counter[0] : 0;
+  if (seq < a.nseq) {
+    float bv = -INFINITY;
+    long bi = 0x7fffffffffffL;
+    for (int b = lane; b < nblk; b += kWave) {
+      const float v = load_coherent(a.part_val + (long)b * kB + seq);
+      const long i = load_coherent(a.part_idx + (long)b * kB + seq);
+      if (v > bv || (v == bv && i < bi)) {
+        bv = v;
+        bi = i;
+      }
+    }
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const float ov = __shfl_xor(bv, off);
+      const long oi = __shfl_xor(bi, off);
+      if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    if (lane == 0) {
+      // no finite maximum anywhere (all partials -inf / NaN): token 0
+      const int64_t tok = bi >= 0x7fffffffL ? 0 : bi;
+      a.token[seq] = tok;
+      if (a.adv_counter != nullptr) {
+        if (a.adv_out != nullptr && c < a.adv_max_tokens) a.adv_out[c * a.nseq + seq] = tok;
+        a.adv_cache_position[seq] += 1;
+        a.adv_rope_position[3 * seq + 0] += 1;
+        a.adv_rope_position[3 * seq + 1] += 1;
+        a.adv_rope_position[3 * seq + 2] += 1;
+      }
+    }
+  }
+  __syncthreads();   // every wave read the counter before it moves
+  if (threadIdx.x == 0 && a.adv_counter != nullptr) a.adv_counter[0] = c + 1;
+}
+
 // RG: rows per workgroup, 16 (the MFMA M dimension) or 8 (rows 8..15 of the
 // A operand are zero: twice the workgroups for the same rows, so a shape with
 // few row groups fills the CUs without splitting K).
@@ -344,10 +390,18 @@ __global__ __launch_bounds__(512) void gemv8_kernel(const Gemv8Args a) {
     }
   }
   if constexpr (ARGMAX) {
+    // per-workgroup (max, first index) of each sequence, published with
+    // coherent stores; the last workgroup to arrive reduces them (one round
+    // of workgroups: none waits for another)
     if (t < OUT && rl == 0) {
-      a.part_val[(long)blockIdx.x * kB + seq] = best;
-      a.part_idx[(long)blockIdx.x * kB + seq] = best_i;
+      store_coherent(a.part_val + (long)blockIdx.x * kB + seq, best);
+      store_coherent(a.part_idx + (long)blockIdx.x * kB + seq, (long)best_i);
+      stores_done();
     }
+    __syncthreads();
+    if (t == 0) s_last = arrive_last(a.argmax_count, gridDim.x);
+    __syncthreads();
+    if (s_last) argmax8_finish(a, (int)gridDim.x);
   }
 }
 
@@ -422,54 +476,6 @@ __global__ __launch_bounds__(256) void bimage8_kernel(const TX* x, long ldx, con
   }
 }
 
-// First maximal index per sequence over the workgroup partials: one block,
-// wave b reduces sequence b; the result is the sequence's next token.  With
-// adv_counter set the block then advances the decode state as advance8_kernel
-// does (one launch less per step).
-__global__ __launch_bounds__(512) void argmax8_reduce_kernel(const float* part_val, const long* part_idx, int nblk,
-                                                             int64_t* token, int nseq, int64_t* adv_out,
-                                                             int64_t* adv_counter, int64_t* adv_cache_position,
-                                                             int64_t* adv_rope_position, int adv_max_tokens) {
-  const int seq = threadIdx.x / kWave;
-  const int lane = lane_id();
-  const int64_t c = adv_counter != nullptr ? adv_counter[0] : 0;
-  if (seq < nseq) {
-    float bv = -INFINITY;
-    long bi = 0x7fffffffffffL;
-    for (int b = lane; b < nblk; b += kWave) {
-      const float v = part_val[(long)b * kB + seq];
-      const long i = part_idx[(long)b * kB + seq];
-      if (v > bv || (v == bv && i < bi)) {
-        bv = v;
-        bi = i;
-      }
-    }
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-      const float ov = __shfl_xor(bv, off);
-      const long oi = __shfl_xor(bi, off);
-      if (ov > bv || (ov == bv && oi < bi)) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-    if (lane == 0) {
-      // no finite maximum anywhere (all partials -inf / NaN): token 0
-      const int64_t tok = bi >= 0x7fffffffL ? 0 : bi;
-      token[seq] = tok;
-      if (adv_counter != nullptr) {
-        if (adv_out != nullptr && c < adv_max_tokens) adv_out[c * nseq + seq] = tok;
-        adv_cache_position[seq] += 1;
-        adv_rope_position[3 * seq + 0] += 1;
-        adv_rope_position[3 * seq + 1] += 1;
-        adv_rope_position[3 * seq + 2] += 1;
-      }
-    }
-  }
-  __syncthreads();   // every wave read the counter before it moves
-  if (threadIdx.x == 0 && adv_counter != nullptr) adv_counter[0] = c + 1;
-}
-
 // Per sequence: out_tokens[counter][b] = token[b] (while counter < max_tokens),
 // ++cache_position[b], ++rope_position[b][0..2]; then ++counter.
 __global__ void advance8_kernel(const int64_t* token, int64_t* out_tokens, int64_t* counter,
@@ -511,6 +517,7 @@ int gemv8_launch(const Gemv8Args& a, int epi, hipStream_t s) {
   if (a.ksplit > 1 && (epi == EPI_ARGMAX || a.kpart == nullptr || a.kcount == nullptr)) return QD_ERR_SHAPE;
   if (epi == EPI_ARGMAX) {
     if (KW != 2048 || rg != 16 || a.part_val == nullptr || a.part_idx == nullptr) return QD_ERR_SHAPE;
+    if (a.argmax_count == nullptr || a.token == nullptr) return QD_ERR_ARG;
     const unsigned gx = (a.grid > 0 && (unsigned)a.grid < nrg) ? (unsigned)a.grid : nrg;
     return launch8<2048, EPI_ARGMAX, 16>(a, gx, s);
   }
@@ -550,15 +557,6 @@ int embed8_launch(const uint16_t* table, const int64_t* token, float* out, int H
   hipLaunchKernelGGL((bimage8_kernel<uint16_t>), dim3(kB), dim3(256), 0, s, table, 0L, token, V, gamma, true, eps,
                      H, nseq, out, img, ss, scale);
   return qd_host::launch_status("embed8_kernel");
-}
-
-int argmax8_reduce_launch(const float* part_val, const long* part_idx, int nblk, int64_t* token, int nseq,
-                          hipStream_t s, int64_t* adv_out, int64_t* adv_counter, int64_t* adv_cache_position,
-                          int64_t* adv_rope_position, int adv_max_tokens) {
-  if (nseq < 1 || nseq > kB) return QD_ERR_SHAPE;
-  hipLaunchKernelGGL(argmax8_reduce_kernel, dim3(1), dim3(kB * kWave), 0, s, part_val, part_idx, nblk, token, nseq,
-                     adv_out, adv_counter, adv_cache_position, adv_rope_position, adv_max_tokens);
-  return qd_host::launch_status("argmax8_reduce_kernel");
 }
 
 int advance8_launch(const int64_t* token, int64_t* out_tokens, int64_t* counter, int64_t* cache_position,

@@ -902,12 +902,18 @@ int batch_step(const qd_model_desc* d, hipStream_t s) {
   gl.part_idx = b.part_idx;
   const int groups = qd::gemv8_row_groups(d->vocab);
   gl.grid = std::min(groups, qd_host::cu_count());   // one looping workgroup per CU (two buffers of weights in flight)
-  if ((st = qd::gemv8_launch(gl, qd::EPI_ARGMAX, s))) return st;
-  if (d->advance_counter != nullptr)
-    return qd::argmax8_reduce_launch(b.part_val, b.part_idx, gl.grid, d->token, B, s, d->advance_out_tokens,
-                                     d->advance_counter, const_cast<int64_t*>(d->cache_position),
-                                     const_cast<int64_t*>(d->rope_position), d->advance_max_tokens);
-  return qd::argmax8_reduce_launch(b.part_val, b.part_idx, gl.grid, d->token, B, s);
+  // the last workgroup reduces the per-sequence argmax (arrival counter: the
+  // header of the batch-1 argmax workspace, which a batch step does not use)
+  gl.argmax_count = reinterpret_cast<unsigned*>(b.argmax_ws);
+  gl.token = d->token;
+  if (d->advance_counter != nullptr) {
+    gl.adv_out = d->advance_out_tokens;
+    gl.adv_counter = d->advance_counter;
+    gl.adv_cache_position = const_cast<int64_t*>(d->cache_position);
+    gl.adv_rope_position = const_cast<int64_t*>(d->rope_position);
+    gl.adv_max_tokens = d->advance_max_tokens;
+  }
+  return qd::gemv8_launch(gl, qd::EPI_ARGMAX, s);
 }
 
 }  // namespace

@@ -258,6 +258,16 @@ struct Gemv8Args {
   int grid = 0;                    // EPI_ARGMAX: workgroups (each loops over row groups); 0: one per group
   float* part_val = nullptr;       // EPI_ARGMAX: [grid][8]
   long* part_idx = nullptr;
+  // EPI_ARGMAX: the last workgroup to arrive (argmax_count: zeroed once,
+  // self-resetting) reduces the partials to token[nseq] and, with adv_counter
+  // set, advances the decode state as advance8_launch does
+  unsigned* argmax_count = nullptr;
+  int64_t* token = nullptr;
+  int64_t* adv_out = nullptr;
+  int64_t* adv_counter = nullptr;
+  int64_t* adv_cache_position = nullptr;
+  int64_t* adv_rope_position = nullptr;
+  int adv_max_tokens = 0;
 };
 
 int gemv8_launch(const Gemv8Args& a, int epi, hipStream_t s);
@@ -266,11 +276,6 @@ int gemv8_row_groups(long N, int rows_per_group = 16);
 // sum of squares of x as one partial ss[8], s to scale[8].
 int bimage8_launch(const float* x, long ldx, const uint16_t* gamma, bool norm, float eps, int K, int nseq,
                    uint16_t* img, float* ss, float* scale, hipStream_t s);
-// (with adv_counter: also the advance of advance8_launch)
-int argmax8_reduce_launch(const float* part_val, const long* part_idx, int nblk, int64_t* token, int nseq,
-                          hipStream_t s, int64_t* adv_out = nullptr, int64_t* adv_counter = nullptr,
-                          int64_t* adv_cache_position = nullptr, int64_t* adv_rope_position = nullptr,
-                          int adv_max_tokens = 0);
 // x[b] = embed[token[b]] and its image (gamma, scale rstd(x)), ss, scale.
 int embed8_launch(const uint16_t* table, const int64_t* token, float* out, int H, long V, int nseq,
                   const uint16_t* gamma, float eps, uint16_t* img, float* ss, float* scale, hipStream_t s);
