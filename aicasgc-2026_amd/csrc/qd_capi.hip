@@ -60,6 +60,7 @@ using u16 = uint16_t;
 
 inline hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
 inline bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline bool aligned(const void* p, uintptr_t n) { return (reinterpret_cast<uintptr_t>(p) & (n - 1)) == 0; }
 
 // Workspace layout of the lm_head argmax: [header (256 B): the blocks' arrival
 // counter] [vals] [idx].
@@ -968,6 +969,15 @@ int qd_decoder_layer_persistent_f16(const void* hidden_in, const qd_layer_weight
                  w->k_norm && w->k_cache && w->v_cache,
              QD_ERR_ARG, "null layer weight or cache pointer");
   QD_REQUIRE(capacity >= 1, QD_ERR_SHAPE, "cache capacity %d", capacity);
+  // what the kernel reads or writes as vectors: 16-byte weight, norm and cache
+  // rows, the 8-byte input slice of each thread, the int64 position words
+  QD_REQUIRE(a16(w->qkv) && a16(w->o_proj) && a16(w->gate_up) && a16(w->down) && a16(w->input_norm) &&
+                 a16(w->post_norm) && a16(w->k_cache) && a16(w->v_cache),
+             QD_ERR_ARG, "weights, norms and caches must be 16-byte aligned");
+  QD_REQUIRE(aligned(hidden_in, 8) && aligned(cache_position, 8) && (!length_out || aligned(length_out, 8)) &&
+                 aligned(status, 4) && aligned(hidden_out, 2) && aligned(cos, 2) && aligned(sin, 2) &&
+                 aligned(w->q_norm, 2) && aligned(w->k_norm, 2),
+             QD_ERR_ARG, "hidden_in, cache_position and length_out must be 8-byte aligned (fp16 vectors 2-byte)");
   char why[256];
   QD_REQUIRE(!persistent_device_unsupported(why, sizeof(why)), QD_ERR_SHAPE, "%s", why);
   qd::PersistArgs p;

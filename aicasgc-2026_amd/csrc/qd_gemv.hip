@@ -277,6 +277,9 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(const GemvArgs a) {
   const int lane = lane_id();
   const long gw = (long)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
   const long nw = (long)gridDim.x * (blockDim.x / kWave);
+  // the decoder layer's running-length advance, as in gemv_kernel's EPI_STORE
+  // (one thread; next_src may equal next_dst)
+  if (a.next_dst != nullptr && blockIdx.x == 0 && threadIdx.x == 0) a.next_dst[0] = a.next_src[0] + 1;
   const TX* x = reinterpret_cast<const TX*>(a.x);
   float rstd = 1.f;
   if constexpr (PRO == PRO_RMSNORM) {

@@ -171,6 +171,17 @@ __device__ __forceinline__ void repoll4(Rsrc r, unsigned off0, unsigned step, u3
   }
 }
 
+// A wait that runs out of its budget records the failure in the status word
+// and hands its reader NaN instead of the stale words: NaN then reaches every
+// value computed from them (the RMSNorms spread it over whole vectors, the
+// attention below carries it through its softmax), so no output of a failed
+// launch looks valid.
+constexpr unsigned kPoison = 0x7fc00000u;  // quiet NaN; its tag bit is clear
+
+__device__ __forceinline__ void wait_failed(Spin& sp) {
+  __hip_atomic_fetch_or(sp.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <int N>
 __device__ __forceinline__ void await4(Rsrc r, unsigned off0, unsigned step, u32x4 (&v)[N], unsigned par,
                                        Spin& sp) {
@@ -181,7 +192,9 @@ __device__ __forceinline__ void await4(Rsrc r, unsigned off0, unsigned step, u32
     for (int k = 0; k < N; ++k) ok &= parity_ok(v[k], par);
     if (ok) break;
     if (sp.left == 0) {
-      __hip_atomic_fetch_or(sp.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      wait_failed(sp);
+#pragma unroll
+      for (int k = 0; k < N; ++k) v[k] = u32x4{kPoison, kPoison, kPoison, kPoison};
       break;
     }
     --sp.left;
@@ -196,7 +209,8 @@ __device__ __forceinline__ float take1(Rsrc r, unsigned i, unsigned par, Spin& s
 #pragma clang loop unroll(disable)
   while (((v ^ par) & 1u) != 0u) {
     if (sp.left == 0) {
-      __hip_atomic_fetch_or(sp.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      wait_failed(sp);
+      v = kPoison;
       break;
     }
     --sp.left;
@@ -667,11 +681,18 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, Ctx& cx, Sm
           den = __builtin_fmaf(s_l[s][g], e, den);
           num = __builtin_fmaf(s_acc[s][g][d], e, num);
         }
+      } else {
+        // no slot raised its maximum: an empty split (every sum 0) or NaN
+        // scores (the sums are NaN), which must stay NaN
+#pragma unroll
+        for (int s = 0; s < SLOTS; ++s) den += s_l[s][g];
+        num = den;
       }
       const int hq = kvh * 2 + g;
+      const bool live = den > 0.f, empty = den == 0.f;
       // an empty split reports lse = -FLT_MAX (finite: the parity bit must not turn -inf into a NaN)
-      put(a.opart_t + ((long)hq * NS + split) * D + d, par, den > 0.f ? num / den : 0.f);
-      if (d == 0) put(a.lse_t + (long)hq * NS + split, par, den > 0.f ? M + __logf(den) : -FLT_MAX);
+      put(a.opart_t + ((long)hq * NS + split) * D + d, par, live ? num / den : (empty ? 0.f : den));
+      if (d == 0) put(a.lse_t + (long)hq * NS + split, par, live ? M + __logf(den) : (empty ? -FLT_MAX : den));
     }
 
     // ================================================================ MERGE + O_PROJ input (wave 0)
@@ -701,7 +722,8 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, Ctx& cx, Sm
           num += s_mw[t][lane];
           den += s_mw[t][MERGE_DIMS];
         }
-        put(a.att_t + mh * D + md0 + lane, par, den > 0.f ? num / den : 0.f);
+        // den >= 1 (the largest split weighs 1) unless an input was NaN
+        put(a.att_t + mh * D + md0 + lane, par, den > 0.f ? num / den : __builtin_nanf(""));
       }
       puts_done();
       gather4<H / (4 * kWave), kWave>(r_att, s_att, (unsigned)lane, par, sp);

@@ -262,6 +262,13 @@ def _full_layer_persistent(hidden_states, qkv_weight, input_layernorm_weight, q_
     if length is not None and not (length.device == h.device and length.dtype == torch.int64
                                    and length.numel() == 1):
         return None
+    # the launch reads weights, norms and caches as 16-byte vectors and the
+    # input as 8-byte slices: offset views take the kernel chain instead
+    if any(t.data_ptr() % 16 for t in (qkv_weight, o_proj_weight, gate_up_weight, down_proj_weight,
+                                       input_layernorm_weight, post_attn_norm_weight, k_cache, v_cache)):
+        return None
+    if h.data_ptr() % 8 or cache_position.data_ptr() % 8:
+        return None
     with torch.cuda.device(h.device):   # the persistent hand-off area is per device: the current one
         return _full_layer_launch(h, qkv_weight, input_layernorm_weight, q_norm_weight, k_norm_weight, cos, sin,
                                   k_cache, v_cache, cache_position, o_proj_weight, post_attn_norm_weight,

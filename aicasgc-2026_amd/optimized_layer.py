@@ -25,6 +25,7 @@ CPU restatement of this math lives in the test oracle, not in the product.
 
 from __future__ import annotations
 
+import os
 from dataclasses import dataclass
 
 import torch
@@ -275,14 +276,40 @@ def _decoder_layers(model):
 
 
 def replace_decoder_layers(model) -> int:
-    """Swap every text decoder layer for OptimizedDecoderLayer (reference optimized_layer.py:3848-3858)."""
+    """Swap every text decoder layer for OptimizedDecoderLayer (reference
+    optimized_layer.py:3848-3858); the new layers are put in eval mode when
+    the model is, as there."""
     layers = _decoder_layers(model)
+    is_eval = not getattr(model, "training", False)
     n = 0
     for i, layer in enumerate(layers):
         if not isinstance(layer, OptimizedDecoderLayer):
             layers[i] = OptimizedDecoderLayer(layer)
+            if is_eval:
+                layers[i].eval()
             n += 1
     return n
+
+
+def check_decode_status(model, reset: bool = True) -> None:
+    """Raise RuntimeError if a swapped layer's one-launch decode step ran out of
+    its hand-off polling budget since the last check (bit 0 of the layer's
+    status word; the launch then also wrote NaN into the outputs it could not
+    compute).  That happens only when the launch's 256 workgroups could not all
+    stay resident, e.g. other work occupied CUs.  Reads every status word (one
+    device synchronisation); call it outside stream capture, e.g. after a
+    generation.  ``reset`` clears the words that were set."""
+    bad = []
+    for i, layer in enumerate(_decoder_layers(model)):
+        st = getattr(layer, "_full_layer_workspace", {}).get("status") if isinstance(
+            layer, OptimizedDecoderLayer) else None
+        if st is not None and int(st.item()) != 0:
+            bad.append(i)
+            if reset:
+                st.zero_()
+    if bad:
+        raise RuntimeError("one-launch decoder layer: a hand-off wait ran out of its polling budget in layer "
+                           + ", ".join(str(i) for i in bad) + " (its outputs are NaN)")
 
 
 def set_small_decode_triton_enabled(model, enabled: bool) -> bool:
@@ -305,6 +332,13 @@ _FUSION_FLAG_NAMES = ("add_rmsnorm_gateup", "full_layer_softsync", "post_attn_ml
 # where the shapes allow (on by default here: on MI355X it is faster than the
 # kernel chain; the reference's A800 default was off)
 _FUSION_FLAGS = {n: n in ("post_attn_mlp_persistent", "full_layer_softsync") for n in _FUSION_FLAG_NAMES}
+# The reference reads its choices from the environment at import
+# (optimized_layer.py:837-921).  A variable that is set explicitly is honoured
+# here too ("1" on, anything else off); an unset one keeps the default above.
+_FUSION_FLAG_ENV = {n: "ENABLE_CUDA_FUSED_" + n.upper() for n in _FUSION_FLAG_NAMES}
+for _n, _var in _FUSION_FLAG_ENV.items():
+    if os.environ.get(_var) is not None:
+        _FUSION_FLAGS[_n] = os.environ[_var] == "1"
 
 
 def set_cuda_mlp_fusion_flags(*, add_rmsnorm_gateup: bool | None = None, full_layer_softsync: bool | None = None,

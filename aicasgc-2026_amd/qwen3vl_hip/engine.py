@@ -72,6 +72,22 @@ class _CapturedSteps:
             torch.cuda.synchronize(self.device)
             self.graph_multi = gm
 
+    def warm_graphs(self) -> None:
+        """Replay every captured graph once and put the step state (token,
+        positions, step counter) back, so later timed replays start warm.  The
+        K/V rows those steps wrote lie at or after the current position, and
+        each is rewritten by its own step before any step reads it."""
+        if self.graph is None:
+            self.capture()
+        saved = [t.clone() for t in self._state_tensors()]
+        for g in (self.graph_multi, self.graph):
+            if g is not None:
+                g.replay()
+        torch.cuda.synchronize(self.device)
+        for t, v in zip(self._state_tensors(), saved):
+            t.copy_(v)
+        torch.cuda.synchronize(self.device)
+
     def replay_steps(self, n: int) -> None:
         """Enqueue n captured steps: n // k replays of the k-step graph, then
         single-step replays."""

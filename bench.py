@@ -101,6 +101,7 @@ def bench_batch8(w, steps: int, warmup: int = 4, cpu: bool = True) -> dict:
     eng.set_state(tokens, lens, lens)
     eng.step_counter.zero_()
     eng.capture()
+    eng.warm_graphs()
     eng.replay_steps(warmup)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -633,6 +634,9 @@ def main() -> int:
     torch.cuda.synchronize()
     log(f"prefill + capture done ({time.time() - t_start:.1f}s)")
 
+    # every captured graph (the single step and the multi-step one) is replayed
+    # once before the timed region, state restored, so no first replay is timed
+    eng.warm_graphs()
     eng.replay_steps(args.warmup)
     torch.cuda.synchronize()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -670,6 +674,7 @@ def main() -> int:
     eng4.set_state(first, 4096 - half, 4096 - half + prompt.rope_delta)
     eng4.step_counter.zero_()
     eng4.capture()
+    eng4.warm_graphs()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     eng4.replay_steps(args.ctx_steps)
@@ -845,6 +850,10 @@ def main() -> int:
                      "us_per_launch": round(us_launch, 3), "bytes_per_launch": kbytes},
         "lm_head": {"us_per_launch": round(us_head, 3), "bytes_per_launch": head_bytes,
                     "achieved_GBps": round(head_bytes / (us_head * 1e-6) / 1e9, 1)},
+        # what a graph-replayed step costs beyond its two kernels (launch gaps,
+        # the graph's own work): the step minus the persistent launch and the
+        # lm_head, each timed on its own (the launch at context ctx)
+        "step_tail_us": (round(ms * 1000.0 - us_launch - us_head, 1) if mode == "persistent" else None),
         "cpu_baseline": cpu,
         "device_copy_GBps": round(copy_gbps, 1),
         "tokens_head": tokens[:8],

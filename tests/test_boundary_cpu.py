@@ -52,6 +52,32 @@ def test_library_host_only_calls():
     assert lib.qd_persistent_set_spin_limit(0) == 0
 
 
+def test_one_launch_layer_rejects_misaligned_pointers():
+    """qd_decoder_layer_persistent_f16 reads weights, norms and caches as 16-byte
+    vectors and the input as 8-byte slices: misaligned addresses are an
+    argument error reported before any device work (the addresses below are
+    never dereferenced)."""
+    import ctypes
+
+    from qwen3vl_hip import _lib
+
+    lib = _lib.lib()
+    good = dict(qkv=0x10000, o_proj=0x20000, gate_up=0x30000, down=0x40000, input_norm=0x50000,
+                post_norm=0x50400, q_norm=0x50800, k_norm=0x50900, k_cache=0x60000, v_cache=0x70000)
+
+    def call(hidden_in=0x80000, pos=0x90000, length=0x90010, **over):
+        w = _lib.LayerDesc(**{**good, **over})
+        return lib.qd_decoder_layer_persistent_f16(
+            ctypes.c_void_p(hidden_in), ctypes.byref(w), 64, ctypes.c_void_p(pos), ctypes.c_void_p(0xa0000),
+            ctypes.c_void_p(0xa0100), 1e-6, 0.088, ctypes.c_void_p(0xb0000), ctypes.c_void_p(length),
+            ctypes.c_void_p(0xc0000), None)
+
+    for over in (dict(qkv=0x10008), dict(gate_up=0x30002), dict(input_norm=0x50004), dict(v_cache=0x70008),
+                 dict(hidden_in=0x80004), dict(pos=0x90004), dict(length=0x90014)):
+        assert call(**over) == -1, over
+        assert b"aligned" in lib.qd_last_error(), over
+
+
 def test_gemv_facade_exports_reference_names():
     import cuda_decode_gemv
 
@@ -194,3 +220,28 @@ def test_bench_batch8_and_config_bytes_are_consistent():
     assert bench.persistent_launch_bytes(513, one) == 100_672_000 + 4096 * 513 + 2 * 2048 + 4 * 2048
     # a batch of one sequence reads what the batch-1 step reads
     assert roofline_bytes_batch_step([4096]) == roofline_bytes_step(4096)
+
+
+def test_fusion_flags_follow_the_reference_environment():
+    """The reference reads ENABLE_CUDA_FUSED_* at import
+    (optimized_layer.py:837-921): an explicitly set variable selects the path,
+    an unset one keeps this build's default (one-launch layer on)."""
+    import os
+    import subprocess
+    import sys
+
+    code = ("import optimized_layer as m; print(m.set_cuda_mlp_fusion_flags()[1], m.set_cuda_mlp_fusion_flags()[0])")
+    env = {k: v for k, v in os.environ.items() if not k.startswith("ENABLE_CUDA_FUSED_")}
+    env["PYTHONPATH"] = str(REPO / "aicasgc-2026_amd")
+    out = {}
+    for val in (None, "0", "1"):
+        e = dict(env)
+        if val is not None:
+            e["ENABLE_CUDA_FUSED_FULL_LAYER_SOFTSYNC"] = val
+            e["ENABLE_CUDA_FUSED_ADD_RMSNORM_GATEUP"] = val
+        res = subprocess.run([sys.executable, "-c", code], env=e, capture_output=True, text=True, timeout=300)
+        assert res.returncode == 0, res.stderr
+        out[val] = res.stdout.split()
+    assert out[None] == ["True", "False"]
+    assert out["0"] == ["False", "False"]
+    assert out["1"] == ["True", "True"]

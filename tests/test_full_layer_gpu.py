@@ -190,6 +190,9 @@ def test_full_layer_declines_inputs_it_does_not_take(cuda):
     wide = torch.zeros(1, 8, 64, 256, dtype=torch.float16, device=cuda)[..., :128]
     assert call(k_cache=wide) is None
     assert call(cache_position=cp.to(torch.int32)) is None
+    # contiguous but 8 bytes off a 16-byte boundary: the launch reads 16-byte rows
+    shifted = torch.zeros(8 * 64 * 128 + 4, dtype=torch.float16, device=cuda)[4:].view(1, 8, 64, 128)
+    assert shifted.is_contiguous() and shifted.data_ptr() % 16 == 8 and call(k_cache=shifted) is None
     out = call()
     torch.cuda.synchronize()
     assert out is not None and out.shape == (1, 1, 2048)
@@ -215,6 +218,8 @@ def test_full_layer_exhausted_polling_budget_is_reported(cuda):
     finally:
         _lib.check(lib.qd_persistent_set_spin_limit(0), "qd_persistent_set_spin_limit")
     assert int(ws["status"].item()) & 1, "a launch with a one-poll budget reported no exhausted wait"
+    # a wait that gave up hands its readers NaN, which reaches the output
+    assert torch.isnan(ws["out"].float()).any(), "the output of a failed launch looks valid"
     ws = {}
     out = _call(lw, h, cos16.to(cuda), sin16.to(cuda), inp.k_cache.to(cuda), inp.v_cache.to(cuda), cp, ws)
     torch.cuda.synchronize()
@@ -222,3 +227,48 @@ def test_full_layer_exhausted_polling_budget_is_reported(cuda):
     ref = O.decode_layer(inp.weights.tensors(), inp.hidden.reshape(-1), inp.k_cache.clone(), inp.v_cache.clone(), 300,
                          cos16.float(), sin16.float())
     assert_close_rel(out.reshape(-1).float().cpu(), ref, what="one-launch layer after an exhausted budget")
+
+
+def test_dropin_layer_status_check_reports_an_exhausted_budget(cuda):
+    """The swapped layer's one-launch decode step under a one-poll budget:
+    optimized_layer.check_decode_status raises (naming the layer) and clears
+    the word; with the default budget the next step checks clean."""
+    import optimized_layer
+    from qwen3vl_hip import _lib
+    from test_layer_gpu import _hf_layer
+
+    inp, cos16, sin16 = _inputs(12, 200, 512)
+    layer = optimized_layer.OptimizedDecoderLayer(_hf_layer(inp.weights)).to(cuda).half()
+    model = torch.nn.Module()
+    model.layers = torch.nn.ModuleList([layer])
+    kc, vc = inp.k_cache.to(cuda), inp.v_cache.to(cuda)
+    cp = torch.tensor([200], dtype=torch.int64, device=cuda)
+    pe = (cos16.to(cuda).reshape(1, 1, 128), sin16.to(cuda).reshape(1, 1, 128))
+
+    import types
+
+    cache = types.SimpleNamespace(layers=[types.SimpleNamespace(keys=kc, values=vc, is_initialized=True,
+                                                                max_cache_len=kc.shape[2])])
+
+    def step():
+        return layer(inp.hidden.to(cuda).reshape(1, 1, 2048), pe, past_key_values=cache, cache_position=cp)
+
+    lib = _lib.lib()
+    step()
+    torch.cuda.synchronize()
+    optimized_layer.check_decode_status(model)            # clean
+    print("case drop-in layer with a one-poll budget", flush=True)
+    _lib.check(lib.qd_persistent_set_spin_limit(1), "qd_persistent_set_spin_limit")
+    try:
+        out = step()
+        torch.cuda.synchronize()
+    finally:
+        _lib.check(lib.qd_persistent_set_spin_limit(0), "qd_persistent_set_spin_limit")
+    assert torch.isnan(out.float()).any()
+    with pytest.raises(RuntimeError, match="layer 0"):
+        optimized_layer.check_decode_status(model)
+    optimized_layer.check_decode_status(model)            # the word was cleared
+    out = step()
+    torch.cuda.synchronize()
+    optimized_layer.check_decode_status(model)
+    assert not torch.isnan(out.float()).any()

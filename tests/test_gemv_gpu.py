@@ -132,6 +132,30 @@ def test_post_attn_mlp_advances_the_running_length(cuda):
     assert torch.equal(out0, out2) and int(length) == 779
 
 
+def test_post_attn_mlp_advance_at_an_unspecialised_intermediate_size(cuda):
+    """I = 1536 has no fixed-K kernel for down_proj (the generic GEMV runs it):
+    the running-length advance must still happen, and the outputs must still
+    match the oracle."""
+    from cuda_decode_gemv_ops import fused
+
+    g = torch.Generator().manual_seed(11)
+    H, I = 2048, 1536
+    res = torch.randn(1, 1, H, generator=g).half()
+    att = torch.randn(1, 1, H, generator=g).half()
+    gamma = (1 + 0.02 * torch.randn(H, generator=g)).half()
+    w_gu = (0.02 * torch.randn(2 * I, H, generator=g)).half()
+    w_d = (0.02 * torch.randn(H, I, generator=g)).half()
+    pos = torch.tensor([41], dtype=torch.int64, device=cuda)
+    length = torch.tensor(0, dtype=torch.int64, device=cuda)
+    hid, out = fused._post_attn_mlp("post_attn_mlp", res.to(cuda), att.to(cuda), gamma.to(cuda), w_gu.to(cuda),
+                                    w_d.to(cuda), None, 1e-6, None, "next", next_position=(pos, length))
+    torch.cuda.synchronize()
+    assert int(length) == 42 and int(pos) == 41
+    rh, ro, _ = O.post_attn_mlp(res.reshape(-1), att.reshape(-1), gamma, w_gu, w_d, None, 1e-6)
+    assert_close_rel(hid.reshape(-1), rh, what="I=1536 hidden")
+    assert_close_rel(out.reshape(-1), ro, what="I=1536 out")
+
+
 def test_fused_post_attn_mlp_bias_and_workspace_reuse(cuda):
     import cuda_decode_gemv as g
     from qwen3vl_hip import synthetic as syn
