@@ -3,13 +3,15 @@
 // One launch runs all 28 layers.  256 workgroups (one per CU) x 8 waves stay
 // resident; every phase of a layer is split statically over the 2048 waves:
 //
-//   QKV      x -> qkv          2 rows of W_qkv per wave (RMSNorm prologue)
+//   QKV      x -> qkv          2 rows of W_qkv per wave (RMSNorm: the x gather
+//                               stores x * gamma and the waves' sums of x^2;
+//                               each dot product is scaled by rstd)
 //   ATTN     qkv -> partials    workgroup = (kv head, split of 32); q/k head
 //                               RMSNorm + M-RoPE + KV-cache write in the prologue;
 //                               32 position slots x 16 lanes; online softmax
 //   MERGE    partials -> attn   workgroup = 8 dims of one q head (wave 0)
 //   O_PROJ   attn -> r          1 row of W_o per wave, + residual x
-//   GATE_UP  r -> hidden        3 (gate, up) row pairs per wave, RMSNorm prologue, SiLU*up
+//   GATE_UP  r -> hidden        3 (gate, up) row pairs per wave, RMSNorm as for QKV, SiLU*up
 //   DOWN     hidden -> x        1 row of W_d per wave, + residual r
 //
 // Weights never depend on activations, so each wave issues the register loads
@@ -233,6 +235,42 @@ __device__ __forceinline__ void gather4(Rsrc r, float* dst, unsigned t, unsigned
   for (int k = 0; k < N; ++k) *reinterpret_cast<f32x4*>(dst + (t + k * THREADS) * 4) = values_of(v[k]);
 }
 
+// gather4 with the RMSNorm weight folded in: dst[i] = v[i] * g[i] (g: the fp16
+// norm weight in LDS), so the GEMV that reads dst needs only rstd, applied to
+// its sums.  Returns this thread's sum of v[i]^2; the raw values of the
+// workgroup's own rows [res0, res0 + NW) (the residual of its outputs) go to
+// res.
+template <int N, int THREADS>
+__device__ __forceinline__ float gather4_scaled(Rsrc r, float* dst, const uint16_t* g, float* res, unsigned res0,
+                                                unsigned t, unsigned par, Spin& sp) {
+  u32x4 v[N];
+#pragma unroll
+  for (int k = 0; k < N; ++k) v[k] = peek4(r, (t + k * THREADS) * 16u);
+  await4<N>(r, t * 16u, THREADS * 16u, v, par, sp);
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < N; ++k) {
+    const unsigned i = (t + k * THREADS) * 4u;
+    const f32x4 x = values_of(v[k]);
+    const uint2 gw = *reinterpret_cast<const uint2*>(g + i);
+    *reinterpret_cast<f32x4*>(dst + i) = f32x4{x.x * lo_f(gw.x), x.y * hi_f(gw.x), x.z * lo_f(gw.y), x.w * hi_f(gw.y)};
+    ss = __builtin_fmaf(x.x, x.x, ss);
+    ss = __builtin_fmaf(x.y, x.y, ss);
+    ss = __builtin_fmaf(x.z, x.z, ss);
+    ss = __builtin_fmaf(x.w, x.w, ss);
+    if (i - res0 < (unsigned)NW) *reinterpret_cast<f32x4*>(res + (i - res0)) = x;
+  }
+  return ss;
+}
+
+// rsqrt(mean + eps) from the per-wave partial sums of squares in LDS.
+__device__ __forceinline__ float rstd_of(const float (&ss)[NW], float n, float eps) {
+  float t = 0.f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) t += ss[w];
+  return rsqrtf(t / n + eps);
+}
+
 template <int KCH>
 __device__ __forceinline__ void load_row(const uint16_t* row, int lane, u32x4 (&w)[KCH]) {
 #pragma unroll
@@ -245,20 +283,6 @@ __device__ __forceinline__ void lds8(const float* s, int c, int lane, float (&x)
   const f32x4 b = *reinterpret_cast<const f32x4*>(s + c * 512 + lane * 8 + 4);
   x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
   x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
-}
-
-// rsqrt(mean(s^2) + eps) over the K = 512 * KCH values of s (whole wave).
-template <int KCH>
-__device__ __forceinline__ float lds_rstd(const float* s, int lane, float eps) {
-  float ss = 0.f;
-#pragma unroll
-  for (int c = 0; c < KCH; ++c) {
-    float x[8];
-    lds8(s, c, lane, x);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(x[i], x[i], ss);
-  }
-  return rsqrtf(wave_sum(ss) / (float)(KCH * 512) + eps);
 }
 
 // The dot products below read x from LDS one chunk ahead of its use and keep
@@ -287,32 +311,6 @@ __device__ __forceinline__ void rows_dot(const u32x4 (&w)[R][KCH], const float* 
   for (int r = 0; r < R; ++r) y[r] = wave_sum(acc[r]);
 }
 
-// y[r] = W_r . (x * rstd * gamma), gamma (fp16) staged in LDS.
-template <int KCH, int R>
-__device__ __forceinline__ void rows_dot_norm(const u32x4 (&w)[R][KCH], const float* s, const uint16_t* g,
-                                              float rstd, int lane, float (&y)[R]) {
-  float acc[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) acc[r] = 0.f;
-  float x[8], xn[8];
-  lds8(s, 0, lane, x);
-#pragma unroll
-  for (int c = 0; c < KCH; ++c) {
-    if (c + 1 < KCH) lds8(s, c + 1, lane, xn);
-    float gf[8];
-    unpack8(*reinterpret_cast<const u32x4*>(g + c * 512 + lane * 8), gf);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) x[i] = (x[i] * rstd) * gf[i];
-#pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = dot8(w[r][c], x, acc[r]);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) x[i] = xn[i];
-    __builtin_amdgcn_sched_barrier(0);
-  }
-#pragma unroll
-  for (int r = 0; r < R; ++r) y[r] = wave_sum(acc[r]);
-}
-
 // Weight streaming.  A wave's vector-memory loads complete in issue order, so a
 // wave that polls a hand-off waits for every load it issued before the poll.
 // The waves therefore split into two groups:
@@ -325,21 +323,29 @@ __device__ __forceinline__ void rows_dot_norm(const u32x4 (&w)[R][KCH], const fl
 // Both groups hold the same number of rows, so a phase ends when the pollers'
 // later loads land; the streamers keep HBM busy across the hand-offs.
 
-// LDS of one workgroup.
+// LDS of one workgroup.  Buffers whose lifetimes do not overlap share memory
+// (a workgroup barrier always separates the last read of one from the first
+// write of the other).
 struct __align__(16) Smem {
-  float x[H];                 // layer input (residual of o_proj)
-  float att[H];               // merged attention output
+  union {
+    float x[H];               // layer input (QKV phase)
+    float att[H];             // merged attention output (MERGE .. O_PROJ)
+  } xa;
   float r[H];                 // post-attention residual
-  float h[I];                 // SiLU(gate) * up
+  union {
+    float h[I];               // SiLU(gate) * up (DOWN)
+    float acc[SLOTS][2][D];   // per-slot attention partials (ATTN .. slot merge)
+  } ha;
   float raw[4][D];            // raw q0, q1, k, v of this kv head
   float q[2][D];              // rotated q
   uint16_t kv[2][D];          // new K_rot / V rows, fp16 as cached
-  float acc[SLOTS][2][D];     // per-slot attention partials
   float m[SLOTS][2];
   float l[SLOTS][2];
   float mw[NS][MERGE_DIMS + 1];
   uint16_t gin[H];            // input RMSNorm weight of the current / next layer
-  uint16_t gpost[H];          // post-attention RMSNorm weight of the current layer
+  uint16_t gpost[H];          // post-attention RMSNorm weight of the current / next layer
+  float xres[NW], rres[NW];   // raw x and r of the workgroup's rows (residuals of o_proj / down)
+  float ssx[NW], ssr[NW];     // per-wave partial sums of squares of x and r
 };
 
 // Rows [t0, t1) of the attended length min(pos + 1, T) that split `split`
@@ -355,7 +361,7 @@ __device__ __forceinline__ void split_window(const PersistArgs& a, long pos, int
 
 // Per-workgroup constants of a launch.
 struct Ctx {
-  int w, gw, kvh, split, t0, t1, mh, md0;
+  int b, w, gw, kvh, split, t0, t1, mh, md0;
   long pos;
   unsigned gen;
   float rc, rs;               // M-RoPE cos / sin of rotary pair `lane`
@@ -368,7 +374,7 @@ struct Ctx {
 // Both instances execute the same sequence of workgroup barriers.
 template <bool STREAM, bool LAYER>
 __device__ __forceinline__ void persist_layers(const PersistArgs& a, Ctx& cx, Smem& sm, Spin& sp,
-                                               uint2 x_first) {
+                                               uint2 x_first, uint2 g_first) {
   const int w = cx.w, gw = cx.gw, kvh = cx.kvh, split = cx.split, mh = cx.mh, md0 = cx.md0;
   // (LAYER: read below, once the first weight rows are in flight)
   int t0 = cx.t0, t1 = cx.t1;
@@ -382,14 +388,14 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, Ctx& cx, Sm
   const Rsrc r_x = rsrc_of(a.x_t, H), r_qkv = rsrc_of(a.qkv_t, NQKV), r_op = rsrc_of(a.opart_t, HQ * NS * D),
              r_lse = rsrc_of(a.lse_t, HQ * NS), r_att = rsrc_of(a.att_t, HQ * D), r_r = rsrc_of(a.r_t, H),
              r_hid = rsrc_of(a.hid_t, I);
-  float(&s_x)[H] = sm.x;
-  float(&s_att)[H] = sm.att;
+  float(&s_x)[H] = sm.xa.x;
+  float(&s_att)[H] = sm.xa.att;
   float(&s_r)[H] = sm.r;
-  float(&s_h)[I] = sm.h;
+  float(&s_h)[I] = sm.ha.h;
   float(&s_raw)[4][D] = sm.raw;
   float(&s_q)[2][D] = sm.q;
   uint16_t(&s_kv)[2][D] = sm.kv;
-  float(&s_acc)[SLOTS][2][D] = sm.acc;
+  float(&s_acc)[SLOTS][2][D] = sm.ha.acc;
   float(&s_m)[SLOTS][2] = sm.m;
   float(&s_l)[SLOTS][2] = sm.l;
   float(&s_mw)[NS][MERGE_DIMS + 1] = sm.mw;
@@ -457,8 +463,9 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, Ctx& cx, Sm
   };
 
   // RMSNorm weights of a layer are staged in LDS by the polling waves: 16 bytes
-  // of each vector per thread, loaded together with their W_down rows of the
-  // previous layer and written after the DOWN hand-off.
+  // of each vector per thread, loaded in the previous layer and written once
+  // that layer has no further use for them (after its gate_up stores).  The
+  // gathers of x and r multiply by them (gather4_scaled).
   // (LAYER: stored after the first weight rows are issued, so no wave waits for
   // them before its W_qkv rows are in flight)
   u32x4 gi0 = {0u, 0u, 0u, 0u}, gp0 = {0u, 0u, 0u, 0u};
@@ -513,30 +520,41 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, Ctx& cx, Sm
     QD_TRACE_AT(l, 0);
     QD_TRACE_ST(l, 0);
     QD_FRESH_LANE();
+    // s_x = x * input_norm; the raw x of this workgroup's rows and the waves'
+    // partial sums of x^2 beside it
     if (l == 0) {
-      if constexpr (LAYER) {
-        // loaded at kernel start: 4 values per thread
-        s_x[tid * 4 + 0] = h2f((uint16_t)(x_first.x & 0xffffu));
-        s_x[tid * 4 + 1] = h2f((uint16_t)(x_first.x >> 16));
-        s_x[tid * 4 + 2] = h2f((uint16_t)(x_first.y & 0xffffu));
-        s_x[tid * 4 + 3] = h2f((uint16_t)(x_first.y >> 16));
-      } else {
+      // every thread: values 4 tid .. 4 tid + 3 and their norm weights (g_first,
+      // loaded at kernel start)
+      uint2 xb = x_first;
+      if constexpr (!LAYER) {
         long tok = a.token[0];
         if (tok < 0 || tok >= a.vocab) tok = 0;
-        const uint16_t* row = a.embed + tok * (long)H;
-        for (int i = tid; i < H; i += NW * kWave) s_x[i] = h2f(row[i]);
+        xb = *reinterpret_cast<const uint2*>(a.embed + tok * (long)H + tid * 4);
       }
-    } else if (!streamer) {
-      gather4<H / (4 * NA * kWave), NA * kWave>(r_x, s_x, (unsigned)tid, par ^ 1u, sp);
+      const f32x4 xv = {lo_f(xb.x), hi_f(xb.x), lo_f(xb.y), hi_f(xb.y)};
+      *reinterpret_cast<f32x4*>(s_x + tid * 4) =
+          f32x4{xv.x * lo_f(g_first.x), xv.y * hi_f(g_first.x), xv.z * lo_f(g_first.y), xv.w * hi_f(g_first.y)};
+      if ((unsigned)(tid * 4 - cx.b * NW) < (unsigned)NW) *reinterpret_cast<f32x4*>(sm.xres + (tid * 4 - cx.b * NW)) = xv;
+      const float ss = wave_sum(xv.x * xv.x + xv.y * xv.y + xv.z * xv.z + xv.w * xv.w);
+      if (lane == 0) sm.ssx[w] = ss;
+    } else {
+      float ss = 0.f;
+      if (!streamer)
+        ss = wave_sum(gather4_scaled<H / (4 * NA * kWave), NA * kWave>(r_x, s_x, s_gin, sm.xres, cx.b * NW,
+                                                                       (unsigned)tid, par ^ 1u, sp));
+      if (lane == 0) sm.ssx[w] = ss;
     }
     __syncthreads();
     QD_TRACE_AT(l, 1);
     QD_TRACE_ST(l, 1);
     QD_FRESH_LANE();
+    // o_proj's residual (s_x shares its memory with the merged attention output)
+    const float xres = sm.xres[w];
     {
       float y[2];
-      rows_dot_norm<4, 2>(wq, s_x, s_gin, lds_rstd<4>(s_x, lane, a.eps), lane, y);
-      if (lane == 0) put2(a.qkv_t + 2 * gw, par, y[0], y[1]);
+      rows_dot<4, 2>(wq, s_x, lane, y);
+      const float rstd = rstd_of(sm.ssx, (float)H, a.eps);
+      if (lane == 0) put2(a.qkv_t + 2 * gw, par, y[0] * rstd, y[1] * rstd);
       if (!streamer) puts_done();
     }
     QD_TRACE_AT(l, 2);
@@ -742,7 +760,7 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, Ctx& cx, Sm
     {
       float y[1];
       rows_dot<4, 1>(wo, s_att, lane, y);
-      if (lane == 0) put(a.r_t + gw, par, y[0] + s_x[gw]);
+      if (lane == 0) put(a.r_t + gw, par, y[0] + xres);
       if (!streamer) puts_done();
     }
     QD_TRACE_AT(l, 8);
@@ -750,7 +768,13 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, Ctx& cx, Sm
 
     // ================================================================ GATE_UP
     QD_FRESH_LANE();
-    if (!streamer) gather4<H / (4 * NA * kWave), NA * kWave>(r_r, s_r, (unsigned)tid, par, sp);
+    {
+      float ss = 0.f;
+      if (!streamer)
+        ss = wave_sum(gather4_scaled<H / (4 * NA * kWave), NA * kWave>(r_r, s_r, s_gpost, sm.rres, cx.b * NW,
+                                                                       (unsigned)tid, par, sp));
+      if (lane == 0) sm.ssr[w] = ss;
+    }
     __syncthreads();
     QD_TRACE_AT(l, 9);
     QD_TRACE_ST(l, 11);
@@ -764,15 +788,23 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, Ctx& cx, Sm
     QD_TRACE_AT(l, 14);
     {
       float gu[6];
-      rows_dot_norm<4, 6>(wgu, s_r, s_gpost, lds_rstd<4>(s_r, lane, a.eps), lane, gu);
+      rows_dot<4, 6>(wgu, s_r, lane, gu);
+      const float rstd = rstd_of(sm.ssr, (float)H, a.eps);
       if (lane == 0) {
 #pragma unroll
         for (int p = 0; p < 3; ++p) {
-          const float g = gu[p];
-          put(a.hid_t + (long)gw * 3 + p, par, (g / (1.0f + __expf(-g))) * gu[3 + p]);
+          const float g = gu[p] * rstd;
+          put(a.hid_t + (long)gw * 3 + p, par, (g / (1.0f + __expf(-g))) * (gu[3 + p] * rstd));
         }
       }
-      if (!streamer) puts_done();
+      if (!streamer) {
+        puts_done();
+        // this layer's reads of both norms are done (the x and r gathers); the
+        // hidden hand-off's barrier below orders these stores before the next
+        // layer's gathers
+        *reinterpret_cast<u32x4*>(s_gin + tid * 8) = gi_next;
+        *reinterpret_cast<u32x4*>(s_gpost + tid * 8) = gp_next;
+      }
     }
     QD_TRACE_AT(l, 10);
     QD_TRACE_ST(l, 12);
@@ -790,17 +822,12 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, Ctx& cx, Sm
     QD_TRACE_AT(l, 11);
     QD_TRACE_ST(l, 14);
     QD_FRESH_LANE();
-    if (!streamer) {
-      // every wave finished this layer's norms before the barrier above
-      *reinterpret_cast<u32x4*>(s_gin + tid * 8) = gi_next;
-      *reinterpret_cast<u32x4*>(s_gpost + tid * 8) = gp_next;
-      issue_qkv(Ln, rs_n);
-    }
+    if (!streamer) issue_qkv(Ln, rs_n);
     {
       float y[1];
       rows_dot<12, 1>(wd, s_h, lane, y);
       if (lane == 0) {
-        const float v = y[0] + s_r[gw];
+        const float v = y[0] + sm.rres[w];
         put(a.x_t + gw, par, v);
         if (l + 1 == a.num_layers) {
           if constexpr (LAYER) a.x_out16[gw] = f2h(v);
@@ -834,12 +861,13 @@ __global__ __launch_bounds__(512) void decode_persistent_kernel(const PersistArg
   // issued before the scalar reads below: loads complete in issue order, so the
   // QKV phase waits for it and not for the weight rows issued later
   uint2 x_first = {0u, 0u};
-  if constexpr (LAYER) {
-    x_first = *reinterpret_cast<const uint2*>(a.x_in + tid * 4);
-    __builtin_amdgcn_sched_barrier(0);
-  }
+  if constexpr (LAYER) x_first = *reinterpret_cast<const uint2*>(a.x_in + tid * 4);
+  // the first layer's input-norm weights of the same 4 values
+  const uint2 g_first = *reinterpret_cast<const uint2*>(a.layers[0].input_norm + tid * 4);
+  __builtin_amdgcn_sched_barrier(0);
 
   Ctx cx;
+  cx.b = b;
   cx.w = w;
   cx.gw = b * NW + w;
   cx.kvh = b % HKV;
@@ -868,8 +896,8 @@ __global__ __launch_bounds__(512) void decode_persistent_kernel(const PersistArg
     sincosf((float)a.rope_position[stream] * a.inv_freq[lane], &cx.rs, &cx.rc);
   }
 
-  if (w >= NA) persist_layers<true, LAYER>(a, cx, sm, sp, x_first);
-  else persist_layers<false, LAYER>(a, cx, sm, sp, x_first);
+  if (w >= NA) persist_layers<true, LAYER>(a, cx, sm, sp, x_first, g_first);
+  else persist_layers<false, LAYER>(a, cx, sm, sp, x_first, g_first);
 
   // The last workgroup to finish advances the generation by this launch's
   // layer count.  Every workgroup read the generation before it produced
