@@ -737,7 +737,7 @@ int launch_persistent(const qd_model_desc* d, const StepBuffers& b, hipStream_t 
     p.layers[l] = qd::PersistLayer{(const u16*)w.qkv,        (const u16*)w.o_proj,    (const u16*)w.gate_up,
                                    (const u16*)w.down,       (const u16*)w.input_norm, (const u16*)w.post_norm,
                                    (const u16*)w.q_norm,     (const u16*)w.k_norm,    (u16*)w.k_cache,
-                                   (u16*)w.v_cache};
+                                   (u16*)w.v_cache,          nullptr};
   }
   p.num_layers = d->num_layers;
   p.T = d->capacity;
@@ -960,33 +960,44 @@ int qd_persistent_prepare(void* stream) {
   return persist_area(S(stream), &t, &ctrl);
 }
 
-int qd_decoder_layer_persistent_f16(const void* hidden_in, const qd_layer_weights* w, int capacity,
-                                    const int64_t* cache_position, const void* cos, const void* sin, float eps,
-                                    float scale, void* hidden_out, int64_t* length_out, unsigned* status,
-                                    void* stream) {
-  QD_REQUIRE(hidden_in && w && cache_position && cos && sin && hidden_out && status, QD_ERR_ARG, "null pointer");
-  QD_REQUIRE(w->qkv && w->o_proj && w->gate_up && w->down && w->input_norm && w->post_norm && w->q_norm &&
-                 w->k_norm && w->k_cache && w->v_cache,
-             QD_ERR_ARG, "null layer weight or cache pointer");
+static int decoder_layers_persistent(const void* hidden_in, const qd_layer_weights* layers, int n_layers,
+                                     int capacity, const int64_t* cache_position, const void* cos, const void* sin,
+                                     float eps, float scale, void* hidden_out, int64_t* const* length_out,
+                                     unsigned* status, void* stream) {
+  QD_REQUIRE(hidden_in && layers && cache_position && cos && sin && hidden_out && status, QD_ERR_ARG,
+             "null pointer");
+  QD_REQUIRE(n_layers >= 1 && n_layers <= qd::kPersistMaxLayers, QD_ERR_SHAPE, "layer count %d outside 1..%d",
+             n_layers, qd::kPersistMaxLayers);
   QD_REQUIRE(capacity >= 1, QD_ERR_SHAPE, "cache capacity %d", capacity);
   // what the kernel reads or writes as vectors: 16-byte weight, norm and cache
   // rows, the 8-byte input slice of each thread, the int64 position words
-  QD_REQUIRE(a16(w->qkv) && a16(w->o_proj) && a16(w->gate_up) && a16(w->down) && a16(w->input_norm) &&
-                 a16(w->post_norm) && a16(w->k_cache) && a16(w->v_cache),
-             QD_ERR_ARG, "weights, norms and caches must be 16-byte aligned");
-  QD_REQUIRE(aligned(hidden_in, 8) && aligned(cache_position, 8) && (!length_out || aligned(length_out, 8)) &&
-                 aligned(status, 4) && aligned(hidden_out, 2) && aligned(cos, 2) && aligned(sin, 2) &&
-                 aligned(w->q_norm, 2) && aligned(w->k_norm, 2),
+  for (int l = 0; l < n_layers; ++l) {
+    const qd_layer_weights* w = layers + l;
+    QD_REQUIRE(w->qkv && w->o_proj && w->gate_up && w->down && w->input_norm && w->post_norm && w->q_norm &&
+                   w->k_norm && w->k_cache && w->v_cache,
+               QD_ERR_ARG, "null layer weight or cache pointer (layer %d)", l);
+    QD_REQUIRE(a16(w->qkv) && a16(w->o_proj) && a16(w->gate_up) && a16(w->down) && a16(w->input_norm) &&
+                   a16(w->post_norm) && a16(w->k_cache) && a16(w->v_cache),
+               QD_ERR_ARG, "weights, norms and caches must be 16-byte aligned (layer %d)", l);
+    QD_REQUIRE(aligned(w->q_norm, 2) && aligned(w->k_norm, 2), QD_ERR_ARG, "q/k norm weights not 2-byte aligned");
+    QD_REQUIRE(!length_out || !length_out[l] || aligned(length_out[l], 8), QD_ERR_ARG,
+               "length_out must be 8-byte aligned (layer %d)", l);
+  }
+  QD_REQUIRE(aligned(hidden_in, 8) && aligned(cache_position, 8) && aligned(status, 4) && aligned(hidden_out, 2) &&
+                 aligned(cos, 2) && aligned(sin, 2),
              QD_ERR_ARG, "hidden_in, cache_position and length_out must be 8-byte aligned (fp16 vectors 2-byte)");
   char why[256];
   QD_REQUIRE(!persistent_device_unsupported(why, sizeof(why)), QD_ERR_SHAPE, "%s", why);
   qd::PersistArgs p;
   memset(&p, 0, sizeof(p));
-  p.layers[0] = qd::PersistLayer{(const u16*)w->qkv,        (const u16*)w->o_proj,    (const u16*)w->gate_up,
-                                 (const u16*)w->down,       (const u16*)w->input_norm, (const u16*)w->post_norm,
-                                 (const u16*)w->q_norm,     (const u16*)w->k_norm,    (u16*)w->k_cache,
-                                 (u16*)w->v_cache};
-  p.num_layers = 1;
+  for (int l = 0; l < n_layers; ++l) {
+    const qd_layer_weights* w = layers + l;
+    p.layers[l] = qd::PersistLayer{(const u16*)w->qkv,        (const u16*)w->o_proj,    (const u16*)w->gate_up,
+                                   (const u16*)w->down,       (const u16*)w->input_norm, (const u16*)w->post_norm,
+                                   (const u16*)w->q_norm,     (const u16*)w->k_norm,    (u16*)w->k_cache,
+                                   (u16*)w->v_cache,          length_out ? length_out[l] : nullptr};
+  }
+  p.num_layers = n_layers;
   p.T = capacity;
   p.eps = eps;
   p.scale = scale;
@@ -995,7 +1006,6 @@ int qd_decoder_layer_persistent_f16(const void* hidden_in, const qd_layer_weight
   p.rope_cos = (const u16*)cos;
   p.rope_sin = (const u16*)sin;
   p.x_out16 = (u16*)hidden_out;
-  p.length_out = length_out;
   unsigned *t = nullptr, *ctrl = nullptr;
   int st = persist_area(S(stream), &t, &ctrl);
   if (st) return st;
@@ -1005,6 +1015,24 @@ int qd_decoder_layer_persistent_f16(const void* hidden_in, const qd_layer_weight
   p.done = ctrl + 1;
   p.spin_limit = g_spin_limit.load();
   return qd::decode_persistent_layer_launch(p, S(stream));
+}
+
+int qd_decoder_layer_persistent_f16(const void* hidden_in, const qd_layer_weights* w, int capacity,
+                                    const int64_t* cache_position, const void* cos, const void* sin, float eps,
+                                    float scale, void* hidden_out, int64_t* length_out, unsigned* status,
+                                    void* stream) {
+  QD_REQUIRE(w, QD_ERR_ARG, "null pointer");
+  int64_t* lengths[1] = {length_out};
+  return decoder_layers_persistent(hidden_in, w, 1, capacity, cache_position, cos, sin, eps, scale, hidden_out,
+                                   lengths, status, stream);
+}
+
+int qd_decoder_layers_persistent_f16(const void* hidden_in, const qd_layer_weights* layers, int n_layers,
+                                     int capacity, const int64_t* cache_position, const void* cos, const void* sin,
+                                     float eps, float scale, void* hidden_out, int64_t* const* length_out,
+                                     unsigned* status, void* stream) {
+  return decoder_layers_persistent(hidden_in, layers, n_layers, capacity, cache_position, cos, sin, eps, scale,
+                                   hidden_out, length_out, status, stream);
 }
 
 int qd_persistent_set_spin_limit(unsigned polls) {

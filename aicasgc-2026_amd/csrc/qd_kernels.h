@@ -157,6 +157,8 @@ struct PersistLayer {
   const uint16_t* k_norm;
   uint16_t* k_cache;
   uint16_t* v_cache;
+  int64_t* length_out;            // LAYER instance: the cache's running length, set to
+                                  // cache_position + 1 after the launch (nullable)
 };
 
 // Everything one persistent launch reads: passed by value, so the layer
@@ -189,15 +191,16 @@ struct PersistArgs {
   // parity follows it) and the workgroups finished in this launch (self-resetting)
   unsigned* generation;
   unsigned* done;
-  // one-layer launch of the drop-in decoder layer (the kernel's LAYER
-  // instance): the layer input instead of the embedding row, transformers'
-  // cos / sin instead of the M-RoPE positions, the output in fp16, and the
-  // cache's running length set to cache_position + 1 after the layer
+  // drop-in decoder layers (the kernel's LAYER instance, one or more layers
+  // of the swapped model): the first layer's input instead of the embedding
+  // row, transformers' cos / sin instead of the M-RoPE positions, every
+  // layer's output in fp16 (the next layer reads that fp16 value, as it would
+  // from a launch of its own), and each cache's running length set to
+  // cache_position + 1 after the launch
   const uint16_t* x_in;           // fp16 [H]
   const uint16_t* rope_cos;       // fp16 [D] (two equal halves)
   const uint16_t* rope_sin;       // fp16 [D]
-  uint16_t* x_out16;              // fp16 [H]
-  int64_t* length_out;            // int64 [1] or null
+  uint16_t* x_out16;              // fp16 [num_layers][H]
   unsigned spin_limit;            // polls per thread and launch before a wait gives up (0: the default)
 };
 

@@ -235,32 +235,35 @@ __device__ __forceinline__ void gather4(Rsrc r, float* dst, unsigned t, unsigned
   for (int k = 0; k < N; ++k) *reinterpret_cast<f32x4*>(dst + (t + k * THREADS) * 4) = values_of(v[k]);
 }
 
+// Sum of squares of four values, in the one order every path uses (the
+// per-wave partials of a vector must not depend on how it reached LDS).
+__device__ __forceinline__ float sumsq4(f32x4 x) {
+  return __builtin_fmaf(x.w, x.w, __builtin_fmaf(x.z, x.z, __builtin_fmaf(x.y, x.y, x.x * x.x)));
+}
+
 // gather4 with the RMSNorm weight folded in: dst[i] = v[i] * g[i] (g: the fp16
 // norm weight in LDS), so the GEMV that reads dst needs only rstd, applied to
-// its sums.  Returns this thread's sum of v[i]^2; the raw values of the
-// workgroup's own rows [res0, res0 + NW) (the residual of its outputs) go to
-// res.
+// its sums.  Thread t holds words 4 (t + k THREADS) .. +4, as a thread of
+// THREADS * k + t would in a layout of 4 words per thread: the sums of squares
+// come back per k (ss[k]), so a wave's sums over them equal those of that
+// layout's waves.  The raw values of the workgroup's own rows [res0, res0 +
+// NW) (the residual of its outputs) go to res.
 template <int N, int THREADS>
-__device__ __forceinline__ float gather4_scaled(Rsrc r, float* dst, const uint16_t* g, float* res, unsigned res0,
-                                                unsigned t, unsigned par, Spin& sp) {
+__device__ __forceinline__ void gather4_scaled(Rsrc r, float* dst, const uint16_t* g, float* res, unsigned res0,
+                                               unsigned t, unsigned par, Spin& sp, float (&ss)[N]) {
   u32x4 v[N];
 #pragma unroll
   for (int k = 0; k < N; ++k) v[k] = peek4(r, (t + k * THREADS) * 16u);
   await4<N>(r, t * 16u, THREADS * 16u, v, par, sp);
-  float ss = 0.f;
 #pragma unroll
   for (int k = 0; k < N; ++k) {
     const unsigned i = (t + k * THREADS) * 4u;
     const f32x4 x = values_of(v[k]);
     const uint2 gw = *reinterpret_cast<const uint2*>(g + i);
     *reinterpret_cast<f32x4*>(dst + i) = f32x4{x.x * lo_f(gw.x), x.y * hi_f(gw.x), x.z * lo_f(gw.y), x.w * hi_f(gw.y)};
-    ss = __builtin_fmaf(x.x, x.x, ss);
-    ss = __builtin_fmaf(x.y, x.y, ss);
-    ss = __builtin_fmaf(x.z, x.z, ss);
-    ss = __builtin_fmaf(x.w, x.w, ss);
+    ss[k] = sumsq4(x);
     if (i - res0 < (unsigned)NW) *reinterpret_cast<f32x4*>(res + (i - res0)) = x;
   }
-  return ss;
 }
 
 // rsqrt(mean + eps) from the per-wave partial sums of squares in LDS.
@@ -535,14 +538,19 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, Ctx& cx, Sm
       *reinterpret_cast<f32x4*>(s_x + tid * 4) =
           f32x4{xv.x * lo_f(g_first.x), xv.y * hi_f(g_first.x), xv.z * lo_f(g_first.y), xv.w * hi_f(g_first.y)};
       if ((unsigned)(tid * 4 - cx.b * NW) < (unsigned)NW) *reinterpret_cast<f32x4*>(sm.xres + (tid * 4 - cx.b * NW)) = xv;
-      const float ss = wave_sum(xv.x * xv.x + xv.y * xv.y + xv.z * xv.z + xv.w * xv.w);
+      const float ss = wave_sum(sumsq4(xv));
       if (lane == 0) sm.ssx[w] = ss;
-    } else {
-      float ss = 0.f;
-      if (!streamer)
-        ss = wave_sum(gather4_scaled<H / (4 * NA * kWave), NA * kWave>(r_x, s_x, s_gin, sm.xres, cx.b * NW,
-                                                                       (unsigned)tid, par ^ 1u, sp));
-      if (lane == 0) sm.ssx[w] = ss;
+    } else if (!streamer) {
+      // polling wave w holds the values of waves w and w + NA of the layout above
+      float ss[H / (4 * NA * kWave)];
+      gather4_scaled<H / (4 * NA * kWave), NA * kWave>(r_x, s_x, s_gin, sm.xres, cx.b * NW, (unsigned)tid, par ^ 1u,
+                                                       sp, ss);
+      static_assert(H / (4 * NA * kWave) == 2, "x gather: two 4-value groups per polling thread");
+      const float s0 = wave_sum(ss[0]), s1 = wave_sum(ss[1]);
+      if (lane == 0) {
+        sm.ssx[w] = s0;
+        sm.ssx[w + NA] = s1;
+      }
     }
     __syncthreads();
     QD_TRACE_AT(l, 1);
@@ -768,12 +776,15 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, Ctx& cx, Sm
 
     // ================================================================ GATE_UP
     QD_FRESH_LANE();
-    {
-      float ss = 0.f;
-      if (!streamer)
-        ss = wave_sum(gather4_scaled<H / (4 * NA * kWave), NA * kWave>(r_r, s_r, s_gpost, sm.rres, cx.b * NW,
-                                                                       (unsigned)tid, par, sp));
-      if (lane == 0) sm.ssr[w] = ss;
+    if (!streamer) {
+      float ss[H / (4 * NA * kWave)];
+      gather4_scaled<H / (4 * NA * kWave), NA * kWave>(r_r, s_r, s_gpost, sm.rres, cx.b * NW, (unsigned)tid, par, sp,
+                                                       ss);
+      const float s0 = wave_sum(ss[0]), s1 = wave_sum(ss[1]);
+      if (lane == 0) {
+        sm.ssr[w] = s0;
+        sm.ssr[w + NA] = s1;
+      }
     }
     __syncthreads();
     QD_TRACE_AT(l, 9);
@@ -828,10 +839,15 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, Ctx& cx, Sm
       rows_dot<12, 1>(wd, s_h, lane, y);
       if (lane == 0) {
         const float v = y[0] + sm.rres[w];
-        put(a.x_t + gw, par, v);
-        if (l + 1 == a.num_layers) {
-          if constexpr (LAYER) a.x_out16[gw] = f2h(v);
-          else a.x_out[gw] = v;
+        if constexpr (LAYER) {
+          // every layer's output in fp16; the next layer reads that value, as a
+          // launch of its own would (its tag bit lies in the zero low mantissa)
+          const uint16_t vh = f2h(v);
+          a.x_out16[(long)l * H + gw] = vh;
+          put(a.x_t + gw, par, h2f(vh));
+        } else {
+          put(a.x_t + gw, par, v);
+          if (l + 1 == a.num_layers) a.x_out[gw] = v;
         }
       }
       QD_TRACE_ST(l, 15);
@@ -910,7 +926,8 @@ __global__ __launch_bounds__(512) void decode_persistent_kernel(const PersistArg
       __hip_atomic_store(a.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(a.generation, cx.gen + (unsigned)a.num_layers, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if constexpr (LAYER) {
-        if (a.length_out != nullptr) *a.length_out = cx.pos + 1;
+        for (int l = 0; l < a.num_layers; ++l)
+          if (a.layers[l].length_out != nullptr) *a.layers[l].length_out = cx.pos + 1;
       }
     }
   }

@@ -227,52 +227,86 @@ def _persistent_layer_device_ok(device: torch.device) -> bool:
     return ok
 
 
-def _full_layer_persistent(hidden_states, qkv_weight, input_layernorm_weight, q_norm_weight, k_norm_weight, cos,
-                           sin, k_cache, v_cache, cache_position, o_proj_weight, o_proj_bias, post_attn_norm_weight,
-                           gate_up_weight, down_proj_weight, down_proj_bias, eps, attn_scale, workspace=None,
-                           length=None):
-    """One Qwen3-VL-2B decoder layer as one persistent launch
-    (qd_decoder_layer_persistent_f16), or None where it does not apply: the
-    reference's eligibility of its one-launch layer (optimized_layer.py:1511-1600:
+def _full_layer_eligible(h, qkv_weight, input_layernorm_weight, q_norm_weight, k_norm_weight, cos, sin, k_cache,
+                         v_cache, cache_position, o_proj_weight, o_proj_bias, post_attn_norm_weight, gate_up_weight,
+                         down_proj_weight, down_proj_bias, length=None) -> bool:
+    """The reference's eligibility of its one-launch layer (optimized_layer.py:1511-1600:
     fp16 GPU tensors at the 2B shapes, contiguous last dims, static [1, 8, T, 128]
-    caches, one cache position) with no biases, contiguous caches and a device
-    that keeps the grid resident.  ``length``: the cache's running-length word,
-    set to position + 1 by the launch.  The output and the status word live in
-    ``workspace`` (stable addresses for graph capture)."""
-    h = hidden_states
+    caches, one cache position) with no biases, contiguous 16-byte aligned
+    weights, norms and caches and 8-byte aligned input and position words."""
     if not (h.device.type == "cuda" and h.dtype == torch.float16 and h.numel() == 2048 and h.shape[-1] == 2048
             and o_proj_bias is None and down_proj_bias is None):
-        return None
+        return False
     mats = ((qkv_weight, (4096, 2048)), (o_proj_weight, (2048, 2048)), (gate_up_weight, (12288, 2048)),
             (down_proj_weight, (2048, 6144)))
     vecs = ((input_layernorm_weight, 2048), (post_attn_norm_weight, 2048), (q_norm_weight, 128),
             (k_norm_weight, 128), (cos, 128), (sin, 128))
     if not all(t.device == h.device and t.dtype == torch.float16 and tuple(t.shape) == shp and t.is_contiguous()
                for t, shp in mats):
-        return None
+        return False
     if not all(t.device == h.device and t.dtype == torch.float16 and t.numel() == n and t.is_contiguous()
                for t, n in vecs):
-        return None
+        return False
     if not all(c.device == h.device and c.dtype == torch.float16 and c.ndim == 4 and c.shape[0] == 1
                and c.shape[1] == 8 and c.shape[3] == 128 and c.is_contiguous() for c in (k_cache, v_cache)):
-        return None
+        return False
     if k_cache.shape != v_cache.shape or not (cache_position.device == h.device and cache_position.numel() == 1
                                               and cache_position.dtype == torch.int64):
-        return None
+        return False
     if length is not None and not (length.device == h.device and length.dtype == torch.int64
                                    and length.numel() == 1):
-        return None
+        return False
     # the launch reads weights, norms and caches as 16-byte vectors and the
     # input as 8-byte slices: offset views take the kernel chain instead
     if any(t.data_ptr() % 16 for t in (qkv_weight, o_proj_weight, gate_up_weight, down_proj_weight,
                                        input_layernorm_weight, post_attn_norm_weight, k_cache, v_cache)):
-        return None
-    if h.data_ptr() % 8 or cache_position.data_ptr() % 8:
+        return False
+    return not (h.data_ptr() % 8 or cache_position.data_ptr() % 8)
+
+
+def _full_layer_persistent(hidden_states, qkv_weight, input_layernorm_weight, q_norm_weight, k_norm_weight, cos,
+                           sin, k_cache, v_cache, cache_position, o_proj_weight, o_proj_bias, post_attn_norm_weight,
+                           gate_up_weight, down_proj_weight, down_proj_bias, eps, attn_scale, workspace=None,
+                           length=None):
+    """One Qwen3-VL-2B decoder layer as one persistent launch
+    (qd_decoder_layer_persistent_f16), or None where it does not apply
+    (_full_layer_eligible, and a device that keeps the grid resident).
+    ``length``: the cache's running-length word, set to position + 1 by the
+    launch.  The output and the status word live in ``workspace`` (stable
+    addresses for graph capture)."""
+    h = hidden_states
+    if not _full_layer_eligible(h, qkv_weight, input_layernorm_weight, q_norm_weight, k_norm_weight, cos, sin,
+                                k_cache, v_cache, cache_position, o_proj_weight, o_proj_bias, post_attn_norm_weight,
+                                gate_up_weight, down_proj_weight, down_proj_bias, length):
         return None
     with torch.cuda.device(h.device):   # the persistent hand-off area is per device: the current one
         return _full_layer_launch(h, qkv_weight, input_layernorm_weight, q_norm_weight, k_norm_weight, cos, sin,
                                   k_cache, v_cache, cache_position, o_proj_weight, post_attn_norm_weight,
                                   gate_up_weight, down_proj_weight, eps, attn_scale, workspace, length)
+
+
+def _layer_stack_launch(h, layers, cos, sin, cache_position, lengths, out, status, eps, attn_scale) -> bool:
+    """Consecutive decoder layers as one persistent launch
+    (qd_decoder_layers_persistent_f16): ``layers`` holds per layer the tuple
+    (qkv, o_proj, gate_up, down, input_norm, post_norm, q_norm, k_norm,
+    k_cache, v_cache), each layer already checked with _full_layer_eligible
+    and all caches of one capacity; ``lengths`` per layer a running-length
+    word or None; ``out`` fp16 [n, 2048] receives every layer's output.
+    False when the device cannot keep the grid resident."""
+    with torch.cuda.device(h.device):
+        if not _persistent_layer_device_ok(h.device):
+            return False
+        n = len(layers)
+        descs = (_lib.LayerDesc * n)()
+        for d, t in zip(descs, layers):
+            (d.qkv, d.o_proj, d.gate_up, d.down, d.input_norm, d.post_norm, d.q_norm, d.k_norm, d.k_cache,
+             d.v_cache) = (x.data_ptr() for x in t)
+        lens = (ctypes.c_void_p * n)(*[(L.data_ptr() if L is not None else None) for L in lengths])
+        _check(_load_ext().qd_decoder_layers_persistent_f16(
+            _p(h.reshape(-1)), ctypes.cast(descs, ctypes.c_void_p), n, int(layers[0][8].shape[2]),
+            _p(cache_position), _p(cos), _p(sin), float(eps), float(attn_scale), _p(out),
+            ctypes.cast(lens, ctypes.c_void_p), _p(status), _stream(h)), "qd_decoder_layers_persistent_f16")
+        return True
 
 
 def _full_layer_launch(h, qkv_weight, input_layernorm_weight, q_norm_weight, k_norm_weight, cos, sin, k_cache,

@@ -98,6 +98,8 @@ class OptimizedDecoderLayer(nn.Module):
         self._post_attn_mlp_workspace: dict = {"type": "fused_post_attn_mlp_softsync"}
         self._o_proj_workspace: dict = {"type": "nosplit"}
         self._full_layer_workspace: dict = {}
+        self._stack: _LayerStack | None = None   # set by replace_decoder_layers
+        self._stack_index = -1
 
     # ------------------------------------------------------------ dispatch
     def _static_layer(self, past_key_values, k_like: torch.Tensor):
@@ -175,6 +177,10 @@ class OptimizedDecoderLayer(nn.Module):
             pos = self._decode_position(layer, cache_position, hidden_states.device) if layer is not None else None
             if pos is not None:
                 length = self._length_word(layer, pos)
+                if _LOOKAHEAD[0] and self._stack is not None:
+                    out = self._stack.step(self, hidden_states, position_embeddings, past_key_values, pos)
+                    if out is not None:
+                        return out
                 out = self._decode_step(hidden_states, position_embeddings, (layer.keys, layer.values), pos, length)
                 if length is None:
                     self._advance_length(layer, pos)
@@ -255,6 +261,111 @@ class OptimizedDecoderLayer(nn.Module):
         return h + F.linear(F.silu(gate) * up, self.down_proj_weight, self.down_proj_bias)
 
 
+_LOOKAHEAD = [os.environ.get("QD_DECODE_LAYER_LOOKAHEAD", "0") == "1"]
+
+
+def set_decode_layer_lookahead(enabled: bool) -> bool:
+    """Opt-in look-ahead of the swapped layers' decode step (off by default;
+    also QD_DECODE_LAYER_LOOKAHEAD=1): the first swapped layer of a step runs
+    every swapped layer in one persistent launch when all of them qualify for
+    the one-launch layer and carry no hooks, and each later layer returns its
+    row of that launch's output when its input is the previous layer's row,
+    untouched.  Each row is bit for bit what the layer's own launch would
+    return (the launch hands fp16 outputs from layer to layer).  In any other
+    case a layer runs its own launch.  Returns the previous setting."""
+    prev = _LOOKAHEAD[0]
+    _LOOKAHEAD[0] = bool(enabled)
+    return prev
+
+
+class _LayerStack:
+    """The swapped decoder layers of one model, in order (replace_decoder_layers
+    makes one per model), and the state of a look-ahead launch in flight: its
+    output rows [n, 2048] (a stable buffer, so a captured graph keeps reading
+    it), its status word, the next layer allowed to take its row and the
+    rows' version when they were written."""
+
+    def __init__(self, layers):
+        self.layers = layers            # the model's own layer list
+        self.out = None
+        self.status = None
+        self.next = -1
+        self.version = -1
+
+    def _members(self):
+        ls = list(self.layers)
+        ok = all(isinstance(L, OptimizedDecoderLayer) and L._stack is self and L._stack_index == i
+                 for i, L in enumerate(ls))
+        return ls if ok else None
+
+    @staticmethod
+    def _hook_free(layer) -> bool:
+        from torch.nn.modules import module as _m
+
+        return not (layer._forward_hooks or layer._forward_pre_hooks or getattr(layer, "_backward_hooks", None)
+                    or _m._global_forward_hooks or _m._global_forward_pre_hooks)
+
+    def step(self, layer, hidden_states, position_embeddings, past_key_values, pos):
+        i = layer._stack_index
+        if i > 0:
+            out = self.out
+            if (self.next == i and out is not None and hidden_states.shape == (1, 1, 2048)
+                    and hidden_states.data_ptr() == out[i - 1].data_ptr()
+                    and hidden_states._version == self.version):
+                self.next = i + 1 if i + 1 < out.shape[0] else -1
+                return out[i].view(1, 1, 2048)
+            self.next = -1
+            return None
+        self.next = -1
+        return self._launch(hidden_states, position_embeddings, past_key_values, pos)
+
+    def _launch(self, h, position_embeddings, past_key_values, pos):
+        members = self._members()
+        if members is None or len(members) < 2 or not _FUSION_FLAGS["full_layer_softsync"]:
+            return None
+        cos, sin = position_embeddings
+        cos, sin = cos.reshape(-1), sin.reshape(-1)
+        rows, lengths, statics = [], [], []
+        cap = None
+        for L in members:
+            if not self._hook_free(L) or not L._decode_ok(h, position_embeddings):
+                return None
+            st = L._static_layer(past_key_values, h.new_empty(1, L.num_kv_heads, 1, L.head_dim))
+            if st is None:
+                return None
+            kc, vc = st.keys, st.values
+            length = L._length_word(st, pos)
+            if cap is None:
+                cap = kc.shape[2]
+            if kc.shape[2] != cap or not fused_ops._full_layer_eligible(
+                    h, L.qkv_weight, L.input_layernorm_weight, L.q_norm_weight, L.k_norm_weight, cos, sin, kc, vc,
+                    pos, L.o_proj_weight, L.o_proj_bias, L.post_attn_layernorm_weight, L.gate_up_weight,
+                    L.down_proj_weight, L.down_proj_bias, length):
+                return None
+            rows.append((L.qkv_weight, L.o_proj_weight, L.gate_up_weight, L.down_proj_weight,
+                         L.input_layernorm_weight, L.post_attn_layernorm_weight, L.q_norm_weight, L.k_norm_weight,
+                         kc, vc))
+            lengths.append(length)
+            statics.append(st)
+        n = len(members)
+        if self.out is None or self.out.shape[0] != n or self.out.device != h.device:
+            if torch.cuda.is_current_stream_capturing():
+                return None            # the buffers are allocated outside capture
+            self.out = torch.empty(n, 2048, dtype=torch.float16, device=h.device)
+            self.status = torch.zeros(1, dtype=torch.int32, device=h.device)
+        eps, scale = members[0].rms_norm_eps, members[0].scaling
+        if any(L.rms_norm_eps != eps or L.scaling != scale for L in members):
+            return None
+        if not fused_ops._layer_stack_launch(h, rows, cos, sin, pos, lengths, self.out, self.status, eps, scale):
+            return None
+        for st, length in zip(statics, lengths):
+            if length is None:
+                OptimizedDecoderLayer._advance_length(st, pos)
+        self.version = self.out._version
+        self.next = 1
+        return self.out[0].view(1, 1, 2048)
+
+
 def _rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
     """HF Qwen3VLTextRMSNorm (modeling_qwen3_vl.py:400-405)."""
     dt = x.dtype
@@ -288,6 +399,12 @@ def replace_decoder_layers(model) -> int:
             if is_eval:
                 layers[i].eval()
             n += 1
+    # the model's swapped layers in order, for the opt-in look-ahead launch
+    stack = _LayerStack(layers)
+    for i, layer in enumerate(layers):
+        if isinstance(layer, OptimizedDecoderLayer):
+            layer._stack = stack
+            layer._stack_index = i
     return n
 
 
@@ -300,16 +417,25 @@ def check_decode_status(model, reset: bool = True) -> None:
     device synchronisation); call it outside stream capture, e.g. after a
     generation.  ``reset`` clears the words that were set."""
     bad = []
+    stacks = []
     for i, layer in enumerate(_decoder_layers(model)):
         st = getattr(layer, "_full_layer_workspace", {}).get("status") if isinstance(
             layer, OptimizedDecoderLayer) else None
         if st is not None and int(st.item()) != 0:
-            bad.append(i)
+            bad.append(str(i))
             if reset:
                 st.zero_()
+        stack = getattr(layer, "_stack", None)
+        if stack is not None and stack not in stacks:
+            stacks.append(stack)
+    for stack in stacks:
+        if stack.status is not None and int(stack.status.item()) != 0:
+            bad.append("stack (look-ahead launch)")
+            if reset:
+                stack.status.zero_()
     if bad:
         raise RuntimeError("one-launch decoder layer: a hand-off wait ran out of its polling budget in layer "
-                           + ", ".join(str(i) for i in bad) + " (its outputs are NaN)")
+                           + ", ".join(bad) + " (its outputs are NaN)")
 
 
 def set_small_decode_triton_enabled(model, enabled: bool) -> bool:

@@ -73,6 +73,7 @@ _SIGS = {
     "qd_decode_step_mode": (c_int, [P]),
     "qd_decode_layers_persistent": (c_int, [P, P]),
     "qd_decoder_layer_persistent_f16": (c_int, [P, P, c_int, P, P, P, c_float, c_float, P, P, P, P]),
+    "qd_decoder_layers_persistent_f16": (c_int, [P, P, c_int, c_int, P, P, P, c_float, c_float, P, P, P, P]),
     "qd_persistent_prepare": (c_int, [P]),
     "qd_persistent_set_spin_limit": (c_int, [ctypes.c_uint]),
     "qd_decode_status": (c_int, [P, POINTER(ctypes.c_uint), c_int]),

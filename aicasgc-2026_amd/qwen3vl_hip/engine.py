@@ -4,8 +4,8 @@ The hot path is one call of the native ``qd_decode_step`` (embedding row,
 28 layers of HIP kernels, final norm, lm_head + argmax) followed by
 ``qd_decode_advance`` (append the token, advance cache/rope positions on the
 device).  Both are captured once into a HIP graph (``torch.cuda.CUDAGraph``),
-and 8 consecutive steps into a second graph; generation is a loop of graph
-replays with no host writes in between.
+and 2, 4 and 8 consecutive steps into further graphs; generation is a loop of
+graph replays with no host writes in between.
 
 Mirrors the reference's decode engine: GreedyDecodeEngine.generate
 (evaluation_wrapper.py:149-315) and DecodeCudaGraphRunner
@@ -35,10 +35,13 @@ def rope_inv_freq(shape: Qwen3VLTextShape = QWEN3VL_2B) -> torch.Tensor:
 
 class _CapturedSteps:
     """HIP-graph capture shared by the engines: one step (``step_eager``:
-    decode + advance) in one graph, and ``steps_per_graph`` consecutive steps
-    in a second.  Each step reads the token and positions the previous step's
-    advance wrote on the device, so k steps replay as one graph launch and the
-    launch gap between graph replays is paid once per k tokens."""
+    decode + advance) in one graph, and k consecutive steps in one graph for
+    every power of two k up to ``steps_per_graph``.  Each step reads the token
+    and positions the previous step's advance wrote on the device, so k steps
+    replay as one graph launch; n steps take one replay per set bit of n (at
+    most steps_per_graph steps per replay), and each replay's launch gap (a
+    single-step replay costs ~8 us more than a step inside a longer graph) is
+    paid once per replay."""
 
     def _state_tensors(self):
         return (self.token, self.cache_position, self.rope_position, self.step_counter)
@@ -58,19 +61,19 @@ class _CapturedSteps:
         for t, v in zip(self._state_tensors(), saved):
             t.copy_(v)
         self._restore(snap)
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            self.step_eager()
-        torch.cuda.synchronize(self.device)
-        self.graph = g
-        self.graph_multi = None
-        if self.steps_per_graph > 1:
-            gm = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(gm):
-                for _ in range(self.steps_per_graph):
+        self.graphs = {}
+        k = 1
+        while k <= self.steps_per_graph:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for _ in range(k):
                     self.step_eager()
             torch.cuda.synchronize(self.device)
-            self.graph_multi = gm
+            self.graphs[k] = g
+            k *= 2
+        self.graph = self.graphs[1]
+        top = max(self.graphs)
+        self.graph_multi = self.graphs[top] if top > 1 else None
 
     def warm_graphs(self) -> None:
         """Replay every captured graph once and put the step state (token,
@@ -80,24 +83,22 @@ class _CapturedSteps:
         if self.graph is None:
             self.capture()
         saved = [t.clone() for t in self._state_tensors()]
-        for g in (self.graph_multi, self.graph):
-            if g is not None:
-                g.replay()
+        for g in self.graphs.values():
+            g.replay()
         torch.cuda.synchronize(self.device)
         for t, v in zip(self._state_tensors(), saved):
             t.copy_(v)
         torch.cuda.synchronize(self.device)
 
     def replay_steps(self, n: int) -> None:
-        """Enqueue n captured steps: n // k replays of the k-step graph, then
-        single-step replays."""
+        """Enqueue n captured steps: replays of the largest graph, then one
+        replay per remaining set bit of n (20 = 8 + 8 + 4)."""
         if self.graph is None:
             self.capture()
-        k = self.steps_per_graph if self.graph_multi is not None else 1
-        for _ in range(n // k):
-            (self.graph_multi if k > 1 else self.graph).replay()
-        for _ in range(n % k):
-            self.graph.replay()
+        while n > 0:
+            k = max(k for k in self.graphs if k <= n)
+            self.graphs[k].replay()
+            n -= k
 
 
 class DecodeEngine(_CapturedSteps):
@@ -170,6 +171,7 @@ class DecodeEngine(_CapturedSteps):
         self.desc = d
         self.graph = None
         self.graph_multi = None
+        self.graphs = {}
         self._graph_max_tokens = 0
         if fuse_advance:
             self._bind_advance()
@@ -208,6 +210,7 @@ class DecodeEngine(_CapturedSteps):
             self.out_tokens = torch.zeros(n, dtype=torch.int64, device=self.device)
             self.graph = None  # the captured advance points at the old buffer
             self.graph_multi = None
+            self.graphs = {}
             self._bind_advance()
 
     def _bind_advance(self) -> None:
@@ -489,6 +492,7 @@ class BatchDecodeEngine(_CapturedSteps):
         self.desc = d
         self.graph = None
         self.graph_multi = None
+        self.graphs = {}
         if fuse_advance:
             self._bind_advance()
 
@@ -510,6 +514,7 @@ class BatchDecodeEngine(_CapturedSteps):
             self.out_tokens = torch.zeros(n, self.batch, dtype=torch.int64, device=self.device)
             self.graph = None
             self.graph_multi = None
+            self.graphs = {}
             if self.desc.advance_counter:
                 self._bind_advance()
 

@@ -54,17 +54,6 @@ WEIGHT_SEED = 3
 PROMPT_SEED = 3
 
 
-def head_start() -> None:
-    """A short GPU spin (torch.cuda._sleep, tens of milliseconds at most) in
-    front of a timed region: the host enqueues the timed graph replays while
-    the stream is busy, so the events time the GPU's work and not the host's
-    latency in launching the first replay (a serving loop enqueues its steps
-    ahead of the GPU the same way)."""
-    import torch
-
-    torch.cuda._sleep(20_000_000)
-
-
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -116,7 +105,6 @@ def bench_batch8(w, steps: int, warmup: int = 4, cpu: bool = True) -> dict:
     eng.replay_steps(warmup)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    head_start()
     e0.record()
     eng.replay_steps(steps)
     e1.record()
@@ -201,7 +189,6 @@ def _graph_us(fns, reps: int) -> float:
     g.replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    head_start()
     e0.record()
     for _ in range(reps):
         g.replay()
@@ -458,13 +445,15 @@ def bench_dropin(w, prompt, k_caches, v_caches, first: int, steps: int, warmup: 
         position_ids.fill_(p + prompt.rope_delta)
         mask[:, p] = 1
 
-    def timed(one_launch: bool):
+    def timed(one_launch: bool, lookahead: bool = False):
         """Capture the step with the swapped layers on one decode path (the
-        one-launch persistent layer, or the kernel chain) and time its replays
+        one-launch persistent layer, or the kernel chain; with ``lookahead``
+        the first swapped layer launches the whole stack) and time its replays
         from the prompt's end; returns (ms per token, tokens)."""
         import optimized_layer
 
         prev = optimized_layer.set_cuda_mlp_fusion_flags(full_layer_softsync=one_launch)
+        prev_la = optimized_layer.set_decode_layer_lookahead(lookahead)
         try:
             next_token.fill_(first)
             write_inputs(S)
@@ -481,12 +470,11 @@ def bench_dropin(w, prompt, k_caches, v_caches, first: int, steps: int, warmup: 
                 run()
         finally:
             optimized_layer.set_cuda_mlp_fusion_flags(full_layer_softsync=prev[1])
+            optimized_layer.set_decode_layer_lookahead(prev_la)
         next_token.fill_(first)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         for i in range(n):
             if i == warmup:
-                torch.cuda.synchronize()
-                head_start()
                 e0.record()
             write_inputs(S + i)
             graph.replay()
@@ -498,10 +486,15 @@ def bench_dropin(w, prompt, k_caches, v_caches, first: int, steps: int, warmup: 
 
     gold = golden["tokens"][1:1 + n]
     res = {}
-    for label, one_launch in (("one_launch", True), ("chain", False)):
-        ms, toks = timed(one_launch)
+    toks_by = {}
+    for label, one_launch, la in (("one_launch", True, False), ("chain", False, False), ("lookahead", True, True)):
+        ms, toks = timed(one_launch, la)
         match = next((i for i, (a, b) in enumerate(zip(toks, gold)) if a != b), min(len(toks), len(gold)))
         res[label] = (ms, match, min(len(toks), len(gold)))
+        toks_by[label] = toks
+    import optimized_layer
+
+    optimized_layer.check_decode_status(model)
     fused_layers = sum(1 for L in model.layers if L._full_layer_workspace.get("out") is not None)
     del model, cache
     torch.cuda.empty_cache()
@@ -517,7 +510,13 @@ def bench_dropin(w, prompt, k_caches, v_caches, first: int, steps: int, warmup: 
             "context_start": S, "tokens_match_golden_prefix": match, "tokens_compared": n_cmp,
             "chain": {"layer_path": "kernel chain per swapped layer (full_layer_softsync fusion flag off)",
                       "ms_per_token": round(res["chain"][0], 4),
-                      "tokens_match_golden_prefix": res["chain"][1], "tokens_compared": res["chain"][2]}}
+                      "tokens_match_golden_prefix": res["chain"][1], "tokens_compared": res["chain"][2]},
+            "lookahead": {"layer_path": "opt-in look-ahead (optimized_layer.set_decode_layer_lookahead): the first "
+                                        "swapped layer launches all 28 in one persistent launch, the others "
+                                        "return their rows",
+                          "ms_per_token": round(res["lookahead"][0], 4),
+                          "tokens_match_golden_prefix": res["lookahead"][1], "tokens_compared": res["lookahead"][2],
+                          "tokens_equal_one_launch": toks_by["lookahead"] == toks_by["one_launch"]}}
 
 
 def phase_trace(contexts) -> list:
@@ -655,7 +654,6 @@ def main() -> int:
     eng.replay_steps(args.warmup)
     torch.cuda.synchronize()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    head_start()
     ev0.record()
     eng.replay_steps(args.steps)
     ev1.record()
@@ -692,7 +690,6 @@ def main() -> int:
     eng4.capture()
     eng4.warm_graphs()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    head_start()
     e0.record()
     eng4.replay_steps(args.ctx_steps)
     e1.record()
@@ -772,6 +769,8 @@ def main() -> int:
         dropin = bench_dropin(w, prompt, eng.k_caches, eng.v_caches, first, args.dropin_steps, 4, gold)
         log(f"drop-in (transformers model + swapped layers, HIP graph): {dropin['ms_per_token']:.4f} ms/token "
             f"one launch per layer ({dropin['layers_on_one_launch_path']} layers), "
+            f"{dropin['lookahead']['ms_per_token']:.4f} ms/token with the look-ahead (tokens equal: "
+            f"{dropin['lookahead']['tokens_equal_one_launch']}), "
             f"{dropin['chain']['ms_per_token']:.4f} ms/token kernel chain; golden prefix "
             f"{dropin['tokens_match_golden_prefix']} / {dropin['chain']['tokens_match_golden_prefix']} of "
             f"{dropin['tokens_compared']}")

@@ -411,6 +411,26 @@ int qd_decoder_layer_persistent_f16(const void* hidden_in, const qd_layer_weight
                                     float scale, void* hidden_out, int64_t* length_out, unsigned* status,
                                     void* stream);
 
+/* Several consecutive decoder layers of the swapped model in one persistent
+ * launch: layer l reads layer l - 1's output rounded to fp16, exactly what a
+ * launch of qd_decoder_layer_persistent_f16 for layer l would read, so every
+ * output equals (bit for bit) that of n_layers one-layer launches in a row.
+ * hidden_out: fp16 [n_layers][2048], layer l's output in row l.  length_out:
+ * nullable array of n_layers nullable words, each set to *cache_position + 1
+ * after the launch.  All layers decode the same cache position with the same
+ * cos / sin (transformers passes one rotary embedding to every layer).  Other
+ * arguments, the status word and the hand-off area's rules as for
+ * qd_decoder_layer_persistent_f16.  Used by the swapped layers' opt-in
+ * look-ahead: the first swapped layer of a step launches the whole stack when
+ * every layer after it is swapped and hook-free, and the later layers return
+ * their rows (optimized_layer.set_decode_layer_lookahead).  No counterpart in
+ * the reference, whose OptimizedDecoderLayer.forward launches one layer per
+ * call (optimized_layer.py:108-154); it serves that forward's callers. */
+int qd_decoder_layers_persistent_f16(const void* hidden_in, const qd_layer_weights* layers, int n_layers,
+                                     int capacity, const int64_t* cache_position, const void* cos, const void* sin,
+                                     float eps, float scale, void* hidden_out, int64_t* const* length_out,
+                                     unsigned* status, void* stream);
+
 /* Allocates and zeroes the current device's persistent hand-off area if it is
  * not there yet (outside stream capture; synchronous the first time), so that
  * later persistent launches may be captured.  QD_ERR_SHAPE when the device
