@@ -75,19 +75,22 @@ class _CapturedSteps:
         top = max(self.graphs)
         self.graph_multi = self.graphs[top] if top > 1 else None
 
-    def warm_graphs(self) -> None:
-        """Replay every captured graph once and put the step state (token,
-        positions, step counter) back, so later timed replays start warm.  The
-        K/V rows those steps wrote lie at or after the current position, and
-        each is rewritten by its own step before any step reads it."""
+    def warm_graphs(self, rounds: int = 6) -> None:
+        """Replay every captured graph once, then the longest one ``rounds`` - 1
+        more times, each time putting the step state (token, positions, step
+        counter) back, so later timed replays start warm: on MI355X the first
+        ~40 ms of decoding after an idle host sync run ~2% slower per step
+        (clocks ramping up).  The K/V rows those steps wrote lie at or after the
+        current position, and each is rewritten by its own step before any
+        step reads it."""
         if self.graph is None:
             self.capture()
         saved = [t.clone() for t in self._state_tensors()]
-        for g in self.graphs.values():
+        order = list(self.graphs.values()) + [self.graphs[max(self.graphs)]] * max(0, rounds - 1)
+        for g in order:
             g.replay()
-        torch.cuda.synchronize(self.device)
-        for t, v in zip(self._state_tensors(), saved):
-            t.copy_(v)
+            for t, v in zip(self._state_tensors(), saved):
+                t.copy_(v)
         torch.cuda.synchronize(self.device)
 
     def replay_steps(self, n: int) -> None:

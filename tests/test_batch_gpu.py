@@ -275,32 +275,33 @@ def test_batch_two_layers_config4_lengths(cuda, two_layer_weights):
 
 def test_batch_full_model_config4_lengths(cuda):
     """Config 4 at its own workload: the full 28-layer model, 8 sequences at the
-    seeded config-4 KV lengths (2273..4067) with random K/V prefixes, two
-    graph-replayed steps against the oracle's batch step (which is pinned per
-    sequence against transformers): both steps' tokens and the second step's
-    logits (bar 2e-3 * max|ref|)."""
+    seeded config-4 KV lengths (2273..4067) with random K/V prefixes, eight
+    graph-replayed steps (two replays of the 4-step graph) against the
+    oracle's batch step (which is pinned per sequence against transformers):
+    every step's tokens and the last step's logits (bar 2e-3 * max|ref|)."""
     from qwen3vl_hip import synthetic as syn
     from qwen3vl_hip.engine import BatchDecodeEngine
 
     w = syn.model_weights(3, device=cuda)
     positions = [int(v) for v in syn.batch8_kv_lengths()]
     tokens = [int(t) for t in syn.randint(4, ("text_ids",), (8,), 0, w.shape.vocab)]
-    eng = BatchDecodeEngine(w, batch=8, capacity=max(positions) + 4, keep_logits=True)
+    n_steps = 8
+    eng = BatchDecodeEngine(w, batch=8, capacity=max(positions) + n_steps + 2, keep_logits=True)
     caches = _fill_caches_device(eng, positions, 43)
     print("case config4 28 layers: GPU steps", flush=True)
-    got = eng.decode(tokens, positions, positions, 2, use_graph=True)
+    got = eng.decode(tokens, positions, positions, n_steps, use_graph=True)
     gpu_logits = eng.logits.cpu()
     del eng
     f32 = types.SimpleNamespace(
         embed_tokens=w.embed_tokens.float().cpu(), final_norm_weight=w.final_norm_weight.float().cpu(),
         layers=[{k: v.float().cpu() for k, v in lw.tensors().items()} for lw in w.layers])
     cur, pos, ref, logits, margins = list(tokens), list(positions), [], None, []
-    for step in range(2):
+    for step in range(n_steps):
         print(f"case config4 28 layers: oracle step {step}", flush=True)
         logits, cur = O.decode_step_batch(f32, cur, caches, pos, pos)
         ref.append(list(cur))
         margins.append([round(O.top2_margin(r), 5) for r in logits])
         pos = [p + 1 for p in pos]
     print(f"gpu {got}\noracle {ref}\nmargins {margins}", flush=True)
-    assert_close_rel(gpu_logits, logits, what="28-layer batch logits at config-4 lengths (second step)")
+    assert_close_rel(gpu_logits, logits, what=f"28-layer batch logits at config-4 lengths (step {n_steps - 1})")
     assert got == ref
