@@ -102,9 +102,9 @@ def bench_batch8(w, steps: int, warmup: int = 4, cpu: bool = True) -> dict:
     eng.step_counter.zero_()
     eng.capture()
     eng.warm_graphs()
-    eng.replay_steps(warmup)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    eng.replay_steps(warmup)   # enqueued right before the timed steps (no idle gap)
     e0.record()
     eng.replay_steps(steps)
     e1.record()
@@ -651,9 +651,12 @@ def main() -> int:
     # every captured graph (the single step and the multi-step one) is replayed
     # once before the timed region, state restored, so no first replay is timed
     eng.warm_graphs()
-    eng.replay_steps(args.warmup)
     torch.cuda.synchronize()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # the W untimed warm-up steps are enqueued right before the timed ones, so
+    # the GPU goes from warm-up into the timed steps without an idle gap (an
+    # idle GPU after a host sync runs its next steps slower)
+    eng.replay_steps(args.warmup)
     ev0.record()
     eng.replay_steps(args.steps)
     ev1.record()
@@ -684,12 +687,14 @@ def main() -> int:
     for k, v in zip(eng4.k_caches, eng4.v_caches):
         k.normal_()
         v.normal_()
-    eng4.reserve_tokens(args.ctx_steps)
-    eng4.set_state(first, 4096 - half, 4096 - half + prompt.rope_delta)
+    w4 = 4   # untimed warm-up steps, enqueued right before the timed ones
+    eng4.reserve_tokens(args.ctx_steps + w4)
+    eng4.set_state(first, 4096 - half - w4, 4096 - half - w4 + prompt.rope_delta)
     eng4.step_counter.zero_()
     eng4.capture()
     eng4.warm_graphs()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    eng4.replay_steps(w4)
     e0.record()
     eng4.replay_steps(args.ctx_steps)
     e1.record()
@@ -701,7 +706,7 @@ def main() -> int:
     if eng4.step_mode == "persistent" and eng4.status() != 0:
         log("FAIL: a persistent-step hand-off timed out in the 4096-context run")
         return 1
-    if int(eng4.step_counter.item()) != args.ctx_steps:
+    if int(eng4.step_counter.item()) != args.ctx_steps + w4:
         log("FAIL: the 4096-context run did not advance every step")
         return 1
     del eng4
