@@ -222,17 +222,31 @@ __device__ __forceinline__ float take1(Rsrc r, unsigned i, unsigned par, Spin& s
   return __builtin_bit_cast(float, v & ~1u);
 }
 
+// The GEMV inputs in LDS (x * gamma, the merged attention output, r * gamma,
+// the MLP hidden vector) are fp16, the rounding the reference's fp16 model
+// applies to every linear layer's input: a dot product then takes two
+// products per instruction (v_dot2_f32_f16, fp32 accumulation) and reads half
+// the LDS bytes.  Hand-off words, residuals and sums of squares stay fp32.
+typedef uint16_t Act;
+typedef _Float16 h2t __attribute__((ext_vector_type(2)));
+typedef _Float16 h8t __attribute__((ext_vector_type(8)));
+
+// Four values into an activation vector in LDS at element i (i % 4 == 0).
+__device__ __forceinline__ void act_store4(Act* dst, unsigned i, f32x4 v) {
+  *reinterpret_cast<uint2*>(dst + i) = uint2{pack2(v.x, v.y), pack2(v.z, v.w)};
+}
+
 // THREADS threads (ids t = 0..THREADS-1) gather N * THREADS * 4 words into
 // dst: thread t takes words 4 (t + k THREADS) .. +4; every load is issued
 // before the first wait.
 template <int N, int THREADS>
-__device__ __forceinline__ void gather4(Rsrc r, float* dst, unsigned t, unsigned par, Spin& sp) {
+__device__ __forceinline__ void gather4(Rsrc r, Act* dst, unsigned t, unsigned par, Spin& sp) {
   u32x4 v[N];
 #pragma unroll
   for (int k = 0; k < N; ++k) v[k] = peek4(r, (t + k * THREADS) * 16u);
   await4<N>(r, t * 16u, THREADS * 16u, v, par, sp);
 #pragma unroll
-  for (int k = 0; k < N; ++k) *reinterpret_cast<f32x4*>(dst + (t + k * THREADS) * 4) = values_of(v[k]);
+  for (int k = 0; k < N; ++k) act_store4(dst, (t + k * THREADS) * 4u, values_of(v[k]));
 }
 
 // Sum of squares of four values, in the one order every path uses (the
@@ -249,7 +263,7 @@ __device__ __forceinline__ float sumsq4(f32x4 x) {
 // layout's waves.  The raw values of the workgroup's own rows [res0, res0 +
 // NW) (the residual of its outputs) go to res.
 template <int N, int THREADS>
-__device__ __forceinline__ void gather4_scaled(Rsrc r, float* dst, const uint16_t* g, float* res, unsigned res0,
+__device__ __forceinline__ void gather4_scaled(Rsrc r, Act* dst, const uint16_t* g, float* res, unsigned res0,
                                                unsigned t, unsigned par, Spin& sp, float (&ss)[N]) {
   u32x4 v[N];
 #pragma unroll
@@ -260,7 +274,7 @@ __device__ __forceinline__ void gather4_scaled(Rsrc r, float* dst, const uint16_
     const unsigned i = (t + k * THREADS) * 4u;
     const f32x4 x = values_of(v[k]);
     const uint2 gw = *reinterpret_cast<const uint2*>(g + i);
-    *reinterpret_cast<f32x4*>(dst + i) = f32x4{x.x * lo_f(gw.x), x.y * hi_f(gw.x), x.z * lo_f(gw.y), x.w * hi_f(gw.y)};
+    act_store4(dst, i, f32x4{x.x * lo_f(gw.x), x.y * hi_f(gw.x), x.z * lo_f(gw.y), x.w * hi_f(gw.y)});
     ss[k] = sumsq4(x);
     if (i - res0 < (unsigned)NW) *reinterpret_cast<f32x4*>(res + (i - res0)) = x;
   }
@@ -280,34 +294,43 @@ __device__ __forceinline__ void load_row(const uint16_t* row, int lane, u32x4 (&
   for (int c = 0; c < KCH; ++c) w[c] = ld_stream(row + c * 512 + lane * 8);
 }
 
-// Chunk c (8 values at c * 512 + lane * 8) of an fp32 vector in LDS.
-__device__ __forceinline__ void lds8(const float* s, int c, int lane, float (&x)[8]) {
-  const f32x4 a = *reinterpret_cast<const f32x4*>(s + c * 512 + lane * 8);
-  const f32x4 b = *reinterpret_cast<const f32x4*>(s + c * 512 + lane * 8 + 4);
-  x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
-  x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
-}
-
 // The dot products below read x from LDS one chunk ahead of its use and keep
 // the scheduler from hoisting further reads (sched_barrier): left alone it
 // issues every chunk's LDS reads up front, and with the prefetched weights of
 // the next phases also live the registers run out.
 
-// y[r] = W_r . x for R rows held in registers, x streamed chunk by chunk from LDS.
+// acc + sum of the 8 products of fp16 weights and fp16 inputs, two per
+// v_dot2_f32_f16 (fp32 accumulation).  The pairs are taken from whole-vector
+// bit casts: element-wise casts of an integer ext-vector are folded wrongly by
+// this compiler.
+__device__ __forceinline__ float dot8h(const u32x4 w, const u32x4 x, float acc) {
+  const h8t wh = __builtin_bit_cast(h8t, w);
+  const h8t xh = __builtin_bit_cast(h8t, x);
+  acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(wh, wh, 0, 1), __builtin_shufflevector(xh, xh, 0, 1), acc,
+                               false);
+  acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(wh, wh, 2, 3), __builtin_shufflevector(xh, xh, 2, 3), acc,
+                               false);
+  acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(wh, wh, 4, 5), __builtin_shufflevector(xh, xh, 4, 5), acc,
+                               false);
+  acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(wh, wh, 6, 7), __builtin_shufflevector(xh, xh, 6, 7), acc,
+                               false);
+  return acc;
+}
+
+// y[r] = W_r . x for R rows held in registers, x (fp16) streamed chunk by
+// chunk from LDS: 8 values per lane and chunk, one 16-byte read.
 template <int KCH, int R>
-__device__ __forceinline__ void rows_dot(const u32x4 (&w)[R][KCH], const float* s, int lane, float (&y)[R]) {
+__device__ __forceinline__ void rows_dot(const u32x4 (&w)[R][KCH], const Act* s, int lane, float (&y)[R]) {
   float acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = 0.f;
-  float x[8], xn[8];
-  lds8(s, 0, lane, x);
+  u32x4 x = *reinterpret_cast<const u32x4*>(s + lane * 8), xn = x;
 #pragma unroll
   for (int c = 0; c < KCH; ++c) {
-    if (c + 1 < KCH) lds8(s, c + 1, lane, xn);
+    if (c + 1 < KCH) xn = *reinterpret_cast<const u32x4*>(s + (c + 1) * 512 + lane * 8);
 #pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = dot8(w[r][c], x, acc[r]);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) x[i] = xn[i];
+    for (int r = 0; r < R; ++r) acc[r] = dot8h(w[r][c], x, acc[r]);
+    x = xn;
     __builtin_amdgcn_sched_barrier(0);
   }
 #pragma unroll
@@ -331,12 +354,12 @@ __device__ __forceinline__ void rows_dot(const u32x4 (&w)[R][KCH], const float* 
 // write of the other).
 struct __align__(16) Smem {
   union {
-    float x[H];               // layer input (QKV phase)
-    float att[H];             // merged attention output (MERGE .. O_PROJ)
+    Act x[H];                 // layer input times input_norm (QKV phase)
+    Act att[H];               // merged attention output (MERGE .. O_PROJ)
   } xa;
-  float r[H];                 // post-attention residual
+  Act r[H];                   // post-attention residual times post_norm
   union {
-    float h[I];               // SiLU(gate) * up (DOWN)
+    Act h[I];                 // SiLU(gate) * up (DOWN)
     float acc[SLOTS][2][D];   // per-slot attention partials (ATTN .. slot merge)
   } ha;
   float raw[4][D];            // raw q0, q1, k, v of this kv head
@@ -391,10 +414,10 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, Ctx& cx, Sm
   const Rsrc r_x = rsrc_of(a.x_t, H), r_qkv = rsrc_of(a.qkv_t, NQKV), r_op = rsrc_of(a.opart_t, HQ * NS * D),
              r_lse = rsrc_of(a.lse_t, HQ * NS), r_att = rsrc_of(a.att_t, HQ * D), r_r = rsrc_of(a.r_t, H),
              r_hid = rsrc_of(a.hid_t, I);
-  float(&s_x)[H] = sm.xa.x;
-  float(&s_att)[H] = sm.xa.att;
-  float(&s_r)[H] = sm.r;
-  float(&s_h)[I] = sm.ha.h;
+  Act(&s_x)[H] = sm.xa.x;
+  Act(&s_att)[H] = sm.xa.att;
+  Act(&s_r)[H] = sm.r;
+  Act(&s_h)[I] = sm.ha.h;
   float(&s_raw)[4][D] = sm.raw;
   float(&s_q)[2][D] = sm.q;
   uint16_t(&s_kv)[2][D] = sm.kv;
@@ -535,8 +558,8 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, Ctx& cx, Sm
         xb = *reinterpret_cast<const uint2*>(a.embed + tok * (long)H + tid * 4);
       }
       const f32x4 xv = {lo_f(xb.x), hi_f(xb.x), lo_f(xb.y), hi_f(xb.y)};
-      *reinterpret_cast<f32x4*>(s_x + tid * 4) =
-          f32x4{xv.x * lo_f(g_first.x), xv.y * hi_f(g_first.x), xv.z * lo_f(g_first.y), xv.w * hi_f(g_first.y)};
+      act_store4(s_x, tid * 4u,
+                 f32x4{xv.x * lo_f(g_first.x), xv.y * hi_f(g_first.x), xv.z * lo_f(g_first.y), xv.w * hi_f(g_first.y)});
       if ((unsigned)(tid * 4 - cx.b * NW) < (unsigned)NW) *reinterpret_cast<f32x4*>(sm.xres + (tid * 4 - cx.b * NW)) = xv;
       const float ss = wave_sum(sumsq4(xv));
       if (lane == 0) sm.ssx[w] = ss;
@@ -656,24 +679,47 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, Ctx& cx, Sm
             vv[u] = *reinterpret_cast<const u32x4*>(&s_kv[1][dl]);
           }
         }
+        // online softmax over the batch's KU rows as one block: their scores,
+        // one running-maximum update and one rescale per head, then one FMA
+        // per dimension and row (rows >= t1 weigh 0; NaN scores stay NaN in
+        // the sums, the maximum skips them)
+        float sc[KU][2];
 #pragma unroll
         for (int u = 0; u < KU; ++u) {
           const bool valid = t + u * SLOTS < t1;
-          float vf[8];
-          unpack8(vv[u], vf);
 #pragma unroll
           for (int g = 0; g < 2; ++g) {
             const float s = row16_sum(dot8(kk[u], q[g], 0.f)) * a.scale;
-            const float dlt = s - m[g];
-            const float e = __expf(-fabsf(dlt));
-            const bool up = valid && dlt > 0.f;
-            const float c = up ? e : 1.f;
-            const float p = valid ? (up ? 1.f : e) : 0.f;
-            m[g] = up ? s : m[g];
-            lsum[g] = __builtin_fmaf(lsum[g], c, p);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) acc[g][i] = __builtin_fmaf(acc[g][i], c, p * vf[i]);
+            sc[u][g] = valid ? s : -INFINITY;
           }
+        }
+        float p[KU][2];
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+          float mb = sc[0][g];
+#pragma unroll
+          for (int u = 1; u < KU; ++u) mb = fmaxf(mb, sc[u][g]);
+          const float mn = fmaxf(m[g], mb);
+          const float c = mn == -INFINITY ? 1.f : __expf(m[g] - mn);
+          float ps = 0.f;
+#pragma unroll
+          for (int u = 0; u < KU; ++u) {
+            p[u][g] = sc[u][g] == -INFINITY ? 0.f : __expf(sc[u][g] - mn);
+            ps += p[u][g];
+          }
+          lsum[g] = __builtin_fmaf(lsum[g], c, ps);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[g][i] *= c;
+          m[g] = mn;
+        }
+#pragma unroll
+        for (int u = 0; u < KU; ++u) {
+          float vf[8];
+          unpack8(vv[u], vf);
+#pragma unroll
+          for (int g = 0; g < 2; ++g)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[g][i] = __builtin_fmaf(p[u][g], vf[i], acc[g][i]);
         }
       }
 #pragma unroll

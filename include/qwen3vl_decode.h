@@ -393,8 +393,10 @@ int qd_decode_layers_persistent(const qd_model_desc* d, void* stream);
  * rotary embedding makes them), the new K/V row written into w->k_cache /
  * w->v_cache ([8, capacity, 128]) at *cache_position, attention over rows
  * 0..min(*cache_position, capacity - 1) scaled by `scale`, o_proj + residual,
- * RMSNorm + gate_up + SiLU*up, down + residual; activations stay fp32 between
- * the phases.  length_out (nullable): set to *cache_position + 1 after every
+ * RMSNorm + gate_up + SiLU*up, down + residual; each linear layer's input is
+ * rounded to fp16 (as the reference's fp16 modules take it), while the
+ * residual stream, the sums of squares and the values handed between the
+ * phases stay fp32.  length_out (nullable): set to *cache_position + 1 after every
  * workgroup has read *cache_position (a static cache's running length; it may
  * be the same word as cache_position).  status: a device word the caller
  * zeroes; bit 0 is set when a hand-off wait ran out of its polling budget
