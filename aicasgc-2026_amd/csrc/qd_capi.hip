@@ -353,10 +353,12 @@ size_t qd_attention_workspace_bytes(int Hq, int Hkv, int n_split) { return attn_
 
 int qd_attention_default_splits(int T) {
   // ~128 positions per workgroup, at least 4 and at most 16 splits per kv head,
-  // so the merge always runs in the partial kernel (one launch).  Measured per
-  // call at T = L: 8 splits are fastest at 1024, 16 at 4096, and at 8192 16
-  // splits (one launch) are within 3% of 32 (partials + merge kernel); more
-  // splits only lengthen the merge.
+  // so the merge runs in the partial kernel (one launch); from 8192 rows on, 32
+  // splits with the merge kernel (all 256 CUs busy).  Measured per call at
+  // T = L, cold copies: 8 splits are fastest at 1024 and 16 at 4096 (32: +5%);
+  // 32 against 16 splits take 12.3 / 17.8 / 28.0 against 12.8 / 19.9 / 33.0 us
+  // at 8192 / 16384 / 32768; 48 and 64 splits are slower than 32 everywhere.
+  if (T >= 8192) return 32;
   int s = (T + 127) / 128;
   if (s < 4) s = 4;
   if (s > 16) s = 16;

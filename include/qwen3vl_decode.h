@@ -258,8 +258,9 @@ int qd_attention_merge(const float* o_part, const float* lse, void* out, int out
                        int Hq, int n_split, void* stream);
 
 /* Default split count for a cache of capacity T (fixed per captured graph):
- * about 128 rows per split, 4..16 splits, so the merge stays in the partial
- * kernel. */
+ * about 128 rows per split, 4..16 splits (the merge then runs in the partial
+ * kernel), and 32 from T = 8192 on (with the merge kernel after the partial
+ * kernel; 256 workgroups at 8 kv heads). */
 int qd_attention_default_splits(int T);
 
 /* ------------------------------------------------------------------ decode step */

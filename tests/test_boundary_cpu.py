@@ -39,7 +39,9 @@ def test_library_host_only_calls():
     assert lib.qd_attention_default_splits(256) == 4
     assert lib.qd_attention_default_splits(1024) == 8
     assert lib.qd_attention_default_splits(4096) == 16
-    assert lib.qd_attention_default_splits(1 << 20) == 16
+    assert lib.qd_attention_default_splits(8191) == 16
+    assert lib.qd_attention_default_splits(8192) == 32
+    assert lib.qd_attention_default_splits(1 << 20) == 32
     assert lib.qd_attention_workspace_bytes(16, 8, 4) >= 16 * 4 * 128 * 4
     assert lib.qd_lm_head_workspace_bytes(151936) > 0
     # argument errors are reported without touching a device
