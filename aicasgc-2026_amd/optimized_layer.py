@@ -278,6 +278,9 @@ def set_decode_layer_lookahead(enabled: bool) -> bool:
     return prev
 
 
+_STACK_MAX_LAYERS = 32   # layers one persistent launch takes (kPersistMaxLayers, csrc/qd_kernels.h)
+
+
 class _LayerStack:
     """The swapped decoder layers of one model, in order (replace_decoder_layers
     makes one per model), and the state of a look-ahead launch in flight: its
@@ -321,7 +324,8 @@ class _LayerStack:
 
     def _launch(self, h, position_embeddings, past_key_values, pos):
         members = self._members()
-        if members is None or len(members) < 2 or not _FUSION_FLAGS["full_layer_softsync"]:
+        if (members is None or not 2 <= len(members) <= _STACK_MAX_LAYERS
+                or not _FUSION_FLAGS["full_layer_softsync"]):
             return None
         cos, sin = position_embeddings
         cos, sin = cos.reshape(-1), sin.reshape(-1)
