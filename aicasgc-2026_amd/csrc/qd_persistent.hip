@@ -657,21 +657,8 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, Ctx& cx, Sm
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc[g][i] = 0.f;
       const int wave_t0 = t0 + w * 4;
-#pragma unroll 1
-      for (int tw = wave_t0; tw < t1; tw += SLOTS * KU) {
-        const int t = tw + row_off;
-        if (tw != wave_t0) {
-#pragma unroll
-          for (int u = 0; u < KU; ++u) {
-            const int tt = t + u * SLOTS;
-            kk[u] = u32x4{0u, 0u, 0u, 0u};
-            vv[u] = u32x4{0u, 0u, 0u, 0u};
-            if (tt < t1 && tt != pos) {
-              kk[u] = ld_stream(kb + (long)tt * D);
-              vv[u] = ld_stream(vb + (long)tt * D);
-            }
-          }
-        }
+      // One batch: the slot's KU rows t, t + SLOTS, ... in kk / vv.
+      auto batch = [&](const int t) {
 #pragma unroll
         for (int u = 0; u < KU; ++u) {
           if (t + u * SLOTS == pos && pos < t1) {
@@ -721,6 +708,26 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, Ctx& cx, Sm
 #pragma unroll
             for (int i = 0; i < 8; ++i) acc[g][i] = __builtin_fmaf(p[u][g], vf[i], acc[g][i]);
         }
+      };
+      // The first batch's rows were loaded before this phase's W_gate/up rows
+      // (issue_kvwo): processed outside the loop, its wait covers only them.
+      // Inside a loop that reloads kk / vv the compiler waits for every load
+      // in flight, the streaming waves' whole W_gate/up burst included.
+      if (wave_t0 < t1) batch(wave_t0 + row_off);
+#pragma unroll 1
+      for (int tw = wave_t0 + SLOTS * KU; tw < t1; tw += SLOTS * KU) {
+        const int t = tw + row_off;
+#pragma unroll
+        for (int u = 0; u < KU; ++u) {
+          const int tt = t + u * SLOTS;
+          kk[u] = u32x4{0u, 0u, 0u, 0u};
+          vv[u] = u32x4{0u, 0u, 0u, 0u};
+          if (tt < t1 && tt != pos) {
+            kk[u] = ld_stream(kb + (long)tt * D);
+            vv[u] = ld_stream(vb + (long)tt * D);
+          }
+        }
+        batch(t);
       }
 #pragma unroll
       for (int g = 0; g < 2; ++g) {
