@@ -377,9 +377,13 @@ int qd_decode_step_mode(const qd_model_desc* d);
  * area per device that the library allocates (uncached device memory, about
  * 330 KB, plus a 256-byte counter block), zeroes at the first persistent step
  * on the device and keeps until the process ends; that first step must run
- * outside stream capture (QD_ERR_ARG otherwise).  Every persistent step on the
- * device shares the area, so persistent steps on one device are serialised
- * (each occupies every CU in any case).  Leaves the
+ * outside stream capture (QD_ERR_ARG otherwise).  Every persistent launch on
+ * the device shares the area, so persistent launches on one device must not
+ * overlap in time: issue them on one stream, or order their streams with
+ * events.  A launch's workgroups fill every CU, but a launch on another stream
+ * can still start on the CUs that the previous launch's finished workgroups
+ * free; such overlap is not detected, and the hand-offs of the launches
+ * involved and of later ones on the device are then undefined.  Leaves the
  * final hidden state (before the final norm) in the workspace's residual vector
  * x (first offset of qd_decode_workspace_layout); the lm_head phase of
  * qd_decode_step_phases continues from there.  Replaces the same span of the
