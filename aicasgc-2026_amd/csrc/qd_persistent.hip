@@ -238,12 +238,32 @@ __device__ __forceinline__ void act_store4(Act* dst, unsigned i, f32x4 v) {
 
 // THREADS threads (ids t = 0..THREADS-1) gather N * THREADS * 4 words into
 // dst: thread t takes words 4 (t + k THREADS) .. +4; every load is issued
-// before the first wait.
+// before the first wait.  Each word is read twice, back to back: a lane whose
+// first reads do not all show `par` takes the second ones when those do, and
+// polls again otherwise.  Measured on the 28-layer launch (same box, A/B):
+// 642-647 against 645-655 us at context 1029 and 673-676 against 677-680 us at
+// 4096; the same second reads left unused measured the same, so the time is
+// not saved by the skipped re-polls (re-polls are rare either way).  Reading
+// the x and r gathers (gather4_scaled) twice as well changed nothing.
 template <int N, int THREADS>
 __device__ __forceinline__ void gather4(Rsrc r, Act* dst, unsigned t, unsigned par, Spin& sp) {
-  u32x4 v[N];
+  u32x4 v[N], v2[N];
 #pragma unroll
   for (int k = 0; k < N; ++k) v[k] = peek4(r, (t + k * THREADS) * 16u);
+#pragma unroll
+  for (int k = 0; k < N; ++k) v2[k] = peek4(r, (t + k * THREADS) * 16u);
+  {
+    bool ok = true, ok2 = true;
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+      ok &= parity_ok(v[k], par);
+      ok2 &= parity_ok(v2[k], par);
+    }
+    if (!ok && ok2) {
+#pragma unroll
+      for (int k = 0; k < N; ++k) v[k] = v2[k];
+    }
+  }
   await4<N>(r, t * 16u, THREADS * 16u, v, par, sp);
 #pragma unroll
   for (int k = 0; k < N; ++k) act_store4(dst, (t + k * THREADS) * 4u, values_of(v[k]));
