@@ -77,13 +77,13 @@ def persistent_launch_bytes(context_len: int, shape) -> int:
 
 def bench_batch8(w, steps: int, warmup: int = 4, cpu: bool = True) -> dict:
     """Config 4: batch 8, per-sequence valid lengths L_i ~ U[2048, 4096]
-    (seeded), random K/V prefixes, greedy steps as HIP-graph replays (4 steps
-    per graph; MFMA batch GEMVs, per-sequence split-KV attention with the merge
-    fused in, per-sequence argmax).
+    (seeded), seeded random K/V prefixes, greedy steps as HIP-graph replays (4
+    steps per graph; MFMA batch GEMVs, per-sequence split-KV attention with the
+    merge fused in, per-sequence argmax).
 
     The first step's 8 tokens are checked against the oracle's batch step on a
-    host copy of the same caches (raises on a mismatch); that oracle call is
-    also the CPU baseline's sample."""
+    host copy of the same caches (raises on a mismatch that is not a tie of
+    the oracle's logits); that oracle call is also the CPU baseline's sample."""
     import torch
 
     from qwen3vl_hip import synthetic as syn
@@ -92,9 +92,10 @@ def bench_batch8(w, steps: int, warmup: int = 4, cpu: bool = True) -> dict:
     lens = [int(v) for v in syn.batch8_kv_lengths()]
     n = warmup + steps
     eng = BatchDecodeEngine(w, batch=8, capacity=max(lens) + n + 1)
+    gen = torch.Generator(device=eng.device).manual_seed(44)   # the same caches whatever ran before
     for k, v in zip(eng.k_caches, eng.v_caches):
-        k.normal_()
-        v.normal_()
+        k.normal_(generator=gen)
+        v.normal_(generator=gen)
     host_caches = [(k.cpu(), v.cpu()) for k, v in zip(eng.k_caches, eng.v_caches)]
     tokens = [int(t) for t in syn.randint(4, ("text_ids",), (8,), 0, w.shape.vocab)]
     eng.reserve_tokens(n)
@@ -128,7 +129,9 @@ def bench_batch8(w, steps: int, warmup: int = 4, cpu: bool = True) -> dict:
     mfma_tflops = 2 * 8 * gemv_params / (ms * 1e-3) / 1e12
     return {"workload": "config4: 8 sequences, valid KV lengths U[2048,4096] (seeded), greedy, 4 steps per HIP graph",
             "kv_lengths": lens, "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 4),
-            "first_step_tokens_match_oracle": True, "first_step_min_top2_margin": check["min_margin"],
+            "first_step_tokens_match_oracle": not check["ties_within_tolerance"],
+            "first_step_ties_within_tolerance": check["ties_within_tolerance"],
+            "first_step_min_top2_margin": check["min_margin"],
             "cpu_baseline": check["cpu_baseline"] if cpu else None,
             "tokens_per_s": round(8 * 1000.0 / ms, 1), "step_bytes": int(nbytes), "achieved_GBps": round(gbps, 1),
             "roofline_frac": round(gbps / PEAK_HBM_GBPS, 4),
@@ -140,8 +143,9 @@ def bench_batch8(w, steps: int, warmup: int = 4, cpu: bool = True) -> dict:
 def batch8_first_step_check(weights_gpu, tokens, lens, host_caches, gpu_tokens) -> dict:
     """Config 4 on the host: the oracle's batch step (each sequence its own
     fp32 step on its own cache rows) on a copy of the GPU engine's caches taken
-    before its first step.  Its tokens must equal the GPU's first-step tokens
-    (raises otherwise); its time is the batch-8 CPU baseline sample."""
+    before its first step.  Its tokens must equal the GPU's first-step tokens,
+    except where the oracle's own logits tie within 2e-3 * max|logit| (raises
+    otherwise); its time is the batch-8 CPU baseline sample."""
     import torch
 
     from oracle import qwen3vl_oracle as O
@@ -157,10 +161,20 @@ def batch8_first_step_check(weights_gpu, tokens, lens, host_caches, gpu_tokens) 
     logits, toks = O.decode_step_batch(f32, tokens, host_caches, lens, lens)
     dt = time.perf_counter() - t0
     margins = [O.top2_margin(row) for row in logits]
-    if list(toks) != list(gpu_tokens):
-        raise RuntimeError(f"batch8 first step: GPU tokens {gpu_tokens} != oracle {list(toks)} "
-                           f"(top-2 margins {margins})")
-    return {"min_margin": round(min(margins), 6),
+    # A GPU token that differs from the oracle's must be a tie within the
+    # logits' tolerance (2e-3 * max|logit| of the sequence, the bar of the GPU
+    # tests): the oracle's logit at the GPU's token that close to its maximum.
+    ties = []
+    for b, (t_ref, t_gpu) in enumerate(zip(toks, gpu_tokens)):
+        if int(t_ref) == int(t_gpu):
+            continue
+        row = logits[b].to(torch.float64)
+        gap = float(row.max() - row[int(t_gpu)])
+        if not gap <= 2e-3 * float(row.abs().max()):
+            raise RuntimeError(f"batch8 first step: GPU tokens {gpu_tokens} != oracle {list(toks)} "
+                               f"(top-2 margins {margins})")
+        ties.append({"sequence": b, "oracle": int(t_ref), "gpu": int(t_gpu), "logit_gap": gap})
+    return {"min_margin": round(min(margins), 6), "ties_within_tolerance": ties,
             "cpu_baseline": {"value": round(1000.0 * dt, 1), "unit": "ms/step", "cores": cores, "kind": "port",
                              "sample": "one batch-8 step of the oracle's fp32 restatement at the KV lengths above "
                                        "(the step whose tokens check the GPU's first step)"}}
