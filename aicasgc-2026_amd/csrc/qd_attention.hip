@@ -26,6 +26,9 @@
 
 #include <math.h>
 
+#include <mutex>
+#include <vector>
+
 #include "qd_common.h"
 #include "qd_kernels.h"
 
@@ -129,14 +132,163 @@ __device__ __forceinline__ void load_kv_batch(const uint16_t* kb, const uint16_t
   }
 }
 
-template <int G, typename TQ, bool FUSED_ROPE>
+// ---------------------------------------------------------------- batch qkv hand-off
+//
+// attention_qkv8_launch runs the batch step's qkv GEMV in the attention launch:
+// workgroup p < kQkv8Producers computes rows [16 p, 16 p + 16) of every
+// sequence's qkv vector and stores each value as a 32-bit word whose mantissa
+// LSB carries the parity of the launch (hgen); the workgroups of a (sequence,
+// kv head) poll the 512 words they need until every one shows that parity.
+// Each word is written once per launch, so consecutive writes alternate their
+// parity and a reader can only see the previous write or the awaited one.  The
+// producers are the first workgroups of the grid, dispatched first, and wait
+// only for each other; the other workgroups wait only for them.  A wait is
+// bounded: past its polling budget it records bit 0 in the status word and
+// hands NaN on (every output of the launch is then NaN, none looks valid).
+
+constexpr unsigned kQkvSpinLimit = 1u << 16;   // polls per thread and launch (tens of ms)
+constexpr int kQkvK = 2048;                    // K of the qkv GEMV
+constexpr int kQkvWaves = 4;                   // K slices of a producer (one per wave)
+constexpr int kQkvKS = kQkvK / kQkvWaves;      // 512
+constexpr int kQkvNT = kQkvKS / 32;            // MFMA K tiles per wave
+constexpr unsigned kQkvPoison = 0x7fc00000u;   // quiet NaN, tag bit clear
+
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ u32x4 bperm4(int addr, const u32x4& v) {
+  return u32x4{(unsigned)__builtin_amdgcn_ds_bpermute(addr, (int)v.x), (unsigned)__builtin_amdgcn_ds_bpermute(addr, (int)v.y),
+               (unsigned)__builtin_amdgcn_ds_bpermute(addr, (int)v.z), (unsigned)__builtin_amdgcn_ds_bpermute(addr, (int)v.w)};
+}
+
+__device__ __forceinline__ unsigned tagged_word(float v, unsigned par) {
+  return (__builtin_bit_cast(unsigned, v) & ~1u) | par;
+}
+
+__device__ __forceinline__ unsigned peek_word(const unsigned* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Values of words p[0] and p[o1] once both show parity `par` (bounded wait;
+// `left` is the thread's remaining polling budget for the launch).
+__device__ __forceinline__ void take_words(const unsigned* p, long o1, unsigned par, unsigned& left,
+                                           unsigned* status, float& v0, float& v1) {
+  unsigned w0 = peek_word(p), w1 = peek_word(p + o1);
+#pragma clang loop unroll(disable)
+  while ((((w0 ^ par) | (w1 ^ par)) & 1u) != 0u) {
+    if (left == 0) {
+      __hip_atomic_fetch_or(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      w0 = w1 = kQkvPoison;
+      break;
+    }
+    --left;
+    __builtin_amdgcn_s_sleep(1);
+    w0 = peek_word(p);
+    w1 = peek_word(p + o1);
+  }
+  v0 = __builtin_bit_cast(float, w0 & ~1u);
+  v1 = __builtin_bit_cast(float, w1 & ~1u);
+}
+
+// Inputs of one producer's GEMV, loaded in the order they are used: the image
+// tiles of the wave's K slice, the norm partial sums of the wave's two
+// sequences, then the weights (16 rows x 512 K per wave as coalesced 128-byte
+// row pieces: load 2 j + h covers rows 8 h .. 8 h + 7, K 64 j .. 64 j + 64 of
+// the slice, 8 lanes x 16 bytes per row).
+struct Qkv8In {
+  u32x4 bt[kQkvNT];
+  u32x4 wt[kQkvNT];
+  float ss[2][4];
+};
+
+__device__ __forceinline__ void qkv8_load(const AttnArgs& a, int p, int w, int lane, Qkv8In& in) {
+  const long kb = (long)w * kQkvKS;
+  const u32x4* src = reinterpret_cast<const u32x4*>(a.xb) + (kb / 32) * 64 + lane;
+#pragma unroll
+  for (int i = 0; i < kQkvNT; ++i) in.bt[i] = src[i * 64];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int seq = 2 * w + q;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int part = lane + i * kWave;
+      in.ss[q][i] = part < a.in_parts ? a.in_ss[(long)part * kBatchMax + seq] : 0.f;
+    }
+  }
+  const uint16_t* wp = a.wqkv + ((long)p * 16 + (lane >> 3)) * kQkvK + kb + (lane & 7) * 8;
+#pragma unroll
+  for (int j = 0; j < kQkvNT / 2; ++j) {
+    in.wt[2 * j] = ld_stream(wp + 64 * j);
+    in.wt[2 * j + 1] = ld_stream(wp + 8L * kQkvK + 64 * j);
+  }
+}
+
+// The producer's rows: MFMA over the wave's K slice (C[r][n] + C[r][n + 8] is
+// row r of sequence n), the 4 slices summed through LDS, scaled by
+// rstd / in_scale of the sequence and stored as tagged words.  Every thread of
+// the workgroup calls it (it contains workgroup barriers).
+__device__ __forceinline__ void qkv8_produce(const AttnArgs& a, int p, int w, int lane, const Qkv8In& in,
+                                             unsigned par, float (&s_part)[kQkvWaves][kBatchMax][16],
+                                             float (&s_fac)[kBatchMax]) {
+  const int m = lane & 15;
+  const int src0 = (8 * (m & 7) + (lane >> 4)) * 4;   // ds_bpermute byte addresses
+  const int src1 = src0 + 16;
+  const bool upper = m >= 8;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < kQkvNT / 2; ++j) {
+    const u32x4 a0 = bperm4(src0, in.wt[2 * j]), a1 = bperm4(src1, in.wt[2 * j]);
+    const u32x4 b0 = bperm4(src0, in.wt[2 * j + 1]), b1 = bperm4(src1, in.wt[2 * j + 1]);
+    const u32x4 t0 = upper ? b0 : a0, t1 = upper ? b1 : a1;
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8v, t0), __builtin_bit_cast(h8v, in.bt[2 * j]),
+                                                 acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8v, t1),
+                                                 __builtin_bit_cast(h8v, in.bt[2 * j + 1]), acc, 0, 0, 0);
+  }
+  {
+    const int g = lane >> 4;
+    const float c[4] = {acc.x, acc.y, acc.z, acc.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float v = c[j] + dpp<kDppRowRor8>(c[j]);
+      if (m < kBatchMax) s_part[w][m][4 * g + j] = v;
+    }
+  }
+  // factor of sequences 2 w and 2 w + 1: rstd of x / the image's scale (0 past nseq)
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int seq = 2 * w + q;
+    const float ss = wave_sum((in.ss[q][0] + in.ss[q][1]) + (in.ss[q][2] + in.ss[q][3]));
+    float f = rsqrtf(ss / (float)kQkvK + a.eps);
+    if (a.in_scale != nullptr) f /= a.in_scale[seq];
+    if (seq >= a.batch) f = 0.f;
+    if (lane == 0) s_fac[seq] = f;
+  }
+  __syncthreads();
+  const int t = threadIdx.x;
+  if (t < kBatchMax * 16) {
+    const int seq = t >> 4, rl = t & 15;
+    float v = 0.f;
+#pragma unroll
+    for (int q = 0; q < kQkvWaves; ++q) v += s_part[q][seq][rl];
+    v *= s_fac[seq];
+    if (seq < a.batch)
+      __hip_atomic_store(a.qkv_t + (long)seq * kQkv8Producers * 16 + p * 16 + rl, tagged_word(v, par),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  stores_done();   // polling with a store of the wave still in flight is much slower
+}
+
+template <int G, typename TQ, bool FUSED_ROPE, bool XQKV = false>
 __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
-  const int kvh = blockIdx.x / a.n_split;
-  const int split = blockIdx.x % a.n_split;
+  static_assert(!XQKV || (G == 2 && FUSED_ROPE), "the qkv hand-off serves the fused batch prologue");
+  // XQKV: one-dimensional grid in dispatch order, sequence-major
+  const int bx = XQKV ? (int)(blockIdx.x % (unsigned)(a.Hkv * a.n_split)) : (int)blockIdx.x;
+  const int kvh = bx / a.n_split;
+  const int split = bx % a.n_split;
   const int slot = threadIdx.x >> 4;
   const int dl = (threadIdx.x & 15) * 8;
   // sequence of a batch (grid y); every per-sequence pointer is offset here
-  const int bq = blockIdx.y;
+  const int bq = XQKV ? (int)(blockIdx.x / (unsigned)(a.Hkv * a.n_split)) : (int)blockIdx.y;
   const TQ* q_in = reinterpret_cast<const TQ*>(a.q) + bq * a.bs_q;
   const TQ* qkv = reinterpret_cast<const TQ*>(a.qkv) + bq * a.bs_q;
   const uint16_t* kc = a.k + bq * a.bs_cache;
@@ -148,6 +300,17 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
   float* o_part = a.o_part + part0 * kD;
   float* lse_out = a.lse + part0;
   float* q_rot_out = a.q_rot_out == nullptr ? nullptr : a.q_rot_out + (long)bq * a.Hq * kD;
+
+  // XQKV: the launch's parity, and a producer's GEMV inputs ahead of every
+  // other load (a wave's loads complete in issue order)
+  unsigned gen = 0u, par = 0u;
+  const bool producer = XQKV && blockIdx.x < (unsigned)kQkv8Producers;
+  Qkv8In qin;
+  if constexpr (XQKV) {
+    gen = __hip_atomic_load(a.hgen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    par = (gen + 1u) & 1u;
+    if (producer) qkv8_load(a, (int)blockIdx.x, (int)(threadIdx.x / kWave), lane_id(), qin);
+  }
 
   const long pos = a.cache_position[bq];
   long Ll = pos + 1 < (long)a.T ? pos + 1 : (long)a.T;
@@ -196,11 +359,13 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
     for (int i = 0; i < kPre; ++i) {
       const int item = w + 4 * i;
       if (item < G + 2) {
-        const TQ* src = item < G    ? qkv + (long)(kvh * G + item) * kD
-                        : item == G ? qkv + (long)a.Hq * kD + (long)kvh * kD
-                                    : qkv + (long)(a.Hq + a.Hkv) * kD + (long)kvh * kD;
-        pre[i][0] = load_act(src, j);
-        pre[i][1] = load_act(src, j + kHalf);
+        if constexpr (!XQKV) {
+          const TQ* src = item < G    ? qkv + (long)(kvh * G + item) * kD
+                          : item == G ? qkv + (long)a.Hq * kD + (long)kvh * kD
+                                      : qkv + (long)(a.Hq + a.Hkv) * kD + (long)kvh * kD;
+          pre[i][0] = load_act(src, j);
+          pre[i][1] = load_act(src, j + kHalf);
+        }
         if (item <= G) {
           const uint16_t* nw = item < G ? a.q_weight : a.k_weight;
           pw[i][0] = nw[j];
@@ -216,8 +381,35 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
   u32x4 kk[kUnroll], vv[kUnroll], kn[kUnroll], vn[kUnroll];
   __builtin_amdgcn_sched_barrier(0);   // every prologue input is requested before the K/V rows
   load_kv_batch(kb, vb, a.stride_s, wave_t0 + row_off, t1, kk, vv);
-  load_kv_batch(kb, vb, a.stride_s, wave_t0 + kStep + row_off, t1, kn, vn);
+  if constexpr (!XQKV) load_kv_batch(kb, vb, a.stride_s, wave_t0 + kStep + row_off, t1, kn, vn);
   __builtin_amdgcn_sched_barrier(0);   // both batches issued before the prologue's math waits
+
+  // XQKV: the hand-off comes before the K/V rows are requested.  A wave's
+  // loads complete in issue order and the memory side serves the chip's
+  // requests in order, so polls issued behind every workgroup's K/V batches
+  // would wait for all of them (measured: no gain over two launches); issued
+  // first, they wait only behind the producers' weight rows.
+  if constexpr (XQKV) {
+    __shared__ float s_part[kQkvWaves][kBatchMax][16];
+    __shared__ float s_fac[kBatchMax];
+    if (producer) qkv8_produce(a, (int)blockIdx.x, w, j, qin, par, s_part, s_fac);
+    // this sequence's raw q (G heads), k and v of kv head kvh, as the words show them
+    unsigned left = a.spin_limit != 0u ? a.spin_limit : kQkvSpinLimit;
+    const unsigned* words = a.qkv_t + (long)bq * kQkv8Producers * 16;
+#pragma unroll
+    for (int i = 0; i < kPre; ++i) {
+      const int item = w + 4 * i;
+      if (item < G + 2) {
+        const long row = item < G    ? (long)(kvh * G + item) * kD
+                         : item == G ? (long)a.Hq * kD + (long)kvh * kD
+                                     : (long)(a.Hq + a.Hkv) * kD + (long)kvh * kD;
+        take_words(words + row + j, kHalf, par, left, a.status, pre[i][0], pre[i][1]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    load_kv_batch(kb, vb, a.stride_s, wave_t0 + kStep + row_off, t1, kn, vn);
+    __builtin_amdgcn_sched_barrier(0);
+  }
 
   __shared__ float s_q[G][kD];
   __shared__ __align__(16) uint16_t s_kv[2][kD];   // new token's K_rot and V, fp16 as cached
@@ -341,7 +533,13 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
   __shared__ int s_last;
   stores_done();
   __syncthreads();
-  if (threadIdx.x == 0) s_last = arrive_last(a.done + (long)bq * a.Hkv + kvh, (unsigned)a.n_split);
+  if (threadIdx.x == 0) {
+    s_last = arrive_last(a.done + (long)bq * a.Hkv + kvh, (unsigned)a.n_split);
+    // XQKV: every workgroup read the launch's parity long before; the last to
+    // arrive advances it for the next launch
+    if (XQKV && arrive_last(a.hdone, gridDim.x))
+      __hip_atomic_store(a.hgen, gen + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
   __syncthreads();
   if (!s_last) return;
   const int S = a.n_split;
@@ -471,6 +669,36 @@ template <typename TQ>
 int attention_partial_launch(const AttnArgs& a, hipStream_t s) {
   if (a.done != nullptr && a.n_split > kFusedMergeMaxSplits) return QD_ERR_SHAPE;
   return a.qkv != nullptr ? launch_partial_g<TQ, true>(a, s) : launch_partial_g<TQ, false>(a, s);
+}
+
+bool attention_qkv8_device_ok() {
+  static std::mutex mu;
+  static std::vector<signed char> ok;   // per device: -1 unknown, 0 no, 1 yes
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return false;
+  std::lock_guard<std::mutex> lk(mu);
+  if ((int)ok.size() <= dev) ok.resize(dev + 1, -1);
+  if (ok[dev] < 0) {
+    int cus = 0, per_cu = 0;
+    const bool q = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+                   hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                       &per_cu, reinterpret_cast<const void*>(&attn_partial_kernel<2, float, true, true>), 256, 0) ==
+                       hipSuccess;
+    ok[dev] = (q && (long)cus * per_cu >= kQkv8Producers) ? 1 : 0;
+    (void)hipGetLastError();
+  }
+  return ok[dev] == 1;
+}
+
+int attention_qkv8_launch(const AttnArgs& a, hipStream_t s) {
+  const long grid = (long)a.batch * a.Hkv * a.n_split;
+  if (a.Hq != 2 * a.Hkv || (a.Hq + 2 * a.Hkv) * kD != kQkv8Producers * 16 || grid < kQkv8Producers ||
+      a.batch < 1 || a.batch > kBatchMax || a.done == nullptr || a.out_img == nullptr || a.n_split > kFusedMergeMaxSplits ||
+      a.wqkv == nullptr || a.xb == nullptr || a.in_ss == nullptr || a.in_parts < 1 || a.in_parts > 4 * kWave ||
+      a.qkv_t == nullptr || a.hgen == nullptr || a.hdone == nullptr || a.status == nullptr)
+    return QD_ERR_SHAPE;
+  hipLaunchKernelGGL((attn_partial_kernel<2, float, true, true>), dim3((unsigned)grid), dim3(256), 0, s, a);
+  return qd_host::launch_status("attn_partial_kernel<qkv>");
 }
 
 template <typename TO>

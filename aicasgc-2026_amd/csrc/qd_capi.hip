@@ -505,6 +505,8 @@ struct StepBuffers {
   unsigned* attn_done;
   float* part_val;
   long* part_idx;
+  unsigned* qkv_t;    // batch step, qkv GEMV in the attention launch: tagged words [8][rows]
+  unsigned* qkv_ctl;  // its launch count (parity) and finished-workgroup counter
 };
 
 using qd::kBatchMaxKsplit;
@@ -529,7 +531,7 @@ bool step_layout(const qd_model_desc* d, int splits, StepBuffers* b, size_t* tot
   size_t o_gw = off; off += align256(argmax_ws_bytes());
   size_t o_ct = off; off += 256;
   size_t o_xb = off, o_ab = off, o_rb = off, o_hb = off, o_ssx = off, o_ssr = off, o_sc = off, o_kp = off,
-         o_kc = off, o_ad = off, o_pv = off, o_pi = off;
+         o_kc = off, o_ad = off, o_pv = off, o_pi = off, o_qt = off, o_qc = off;
   if (B > 1) {
     // an operand image holds 16 fp16 columns per K index
     const size_t groups = (size_t)qd::gemv8_row_groups(d->vocab);
@@ -547,6 +549,8 @@ bool step_layout(const qd_model_desc* d, int splits, StepBuffers* b, size_t* tot
     o_ad = off; off += align256(4 * B * (size_t)d->num_kv_heads);
     o_pv = off; off += align256(4 * groups * qd::kBatchMax);
     o_pi = off; off += align256(8 * groups * qd::kBatchMax);
+    o_qt = off; off += align256(4 * qd::kBatchMax * qkv_rows);
+    o_qc = off; off += 256;
   }
   *total = off;
   if (b != nullptr) {
@@ -573,6 +577,8 @@ bool step_layout(const qd_model_desc* d, int splits, StepBuffers* b, size_t* tot
     b->attn_done = reinterpret_cast<unsigned*>(base + o_ad);
     b->part_val = reinterpret_cast<float*>(base + o_pv);
     b->part_idx = reinterpret_cast<long*>(base + o_pi);
+    b->qkv_t = reinterpret_cast<unsigned*>(base + o_qt);
+    b->qkv_ctl = reinterpret_cast<unsigned*>(base + o_qc);
   }
   return true;
 }
@@ -822,7 +828,8 @@ BatchSplit batch_split(long rows, long K, bool silu) {
 
 // Batch step (batch 2..8): the kernel chain with MFMA batch GEMVs and the
 // split-KV attention run per sequence (grid y), every sequence at its own cache
-// position.  Activations move between the GEMVs as operand images: x (times
+// position; with QD_STEP_AUTO each layer's qkv GEMV runs inside its attention
+// launch (attention_qkv8_launch) where the shape and the device allow it.  Activations move between the GEMVs as operand images: x (times
 // the next input_norm, or final_norm after the last layer, scaled by rstd of
 // the previous r), the attention output, r (times post_norm, scaled by rstd
 // of x) and the MLP hidden; each producer also writes per-row-group sums of
@@ -844,6 +851,12 @@ int batch_step(const qd_model_desc* d, hipStream_t s) {
   // (down and o_proj)
   const int x_parts = qd::gemv8_row_groups(H, batch_split(H, I, false).rows_per_group);
   const int r_parts = qd::gemv8_row_groups(H, batch_split(H, (long)Hq * D, false).rows_per_group);
+  // QD_STEP_AUTO: each layer's qkv GEMV runs inside its attention launch
+  // (attention_qkv8_launch) where the shape and the device allow it; the
+  // words it hands over and their counters live in this step's workspace
+  const bool fuse_qkv = d->step_mode == QD_STEP_AUTO && H == 2048 && D == 128 && Hq == 2 * Hkv &&
+                        qkv_rows == (long)qd::kQkv8Producers * 16 && (long)B * Hkv * splits >= qd::kQkv8Producers &&
+                        splits <= 64 && qd::attention_qkv8_device_ok();
   int st = QD_OK;
   if ((st = qd::embed8_launch((const u16*)d->embed, d->token, b.x, H, d->vocab, B,
                               (const u16*)d->layers[0].input_norm, d->eps, b.xb, b.ss_x, b.sc_x, s)))
@@ -860,7 +873,7 @@ int batch_step(const qd_model_desc* d, hipStream_t s) {
     base(g, qkv_rows, H);
     g.xb = b.xb; g.in_ss = b.ss_x; g.in_parts = xparts; g.in_scale = b.sc_x; g.W = (const u16*)w.qkv;
     g.y = b.qkv; g.ldy = qkv_rows;
-    if ((st = qd::gemv8_launch(g, qd::EPI_STORE, s))) return st;
+    if (!fuse_qkv && (st = qd::gemv8_launch(g, qd::EPI_STORE, s))) return st;
     qd::AttnArgs aa;
     aa.k = (const u16*)w.k_cache; aa.v = (const u16*)w.v_cache; aa.k_w = (u16*)w.k_cache; aa.v_w = (u16*)w.v_cache;
     aa.stride_h = (long)d->capacity * D; aa.stride_s = D; aa.T = d->capacity; aa.cache_position = d->cache_position;
@@ -872,7 +885,14 @@ int batch_step(const qd_model_desc* d, hipStream_t s) {
     aa.out_img = b.ab; aa.done = b.attn_done;
     attn_ws(b.attn_ws, aa);
     aa.lse = aa.o_part + (size_t)B * Hq * splits * 128;
-    if ((st = qd::attention_partial_launch<float>(aa, s))) return st;
+    if (fuse_qkv) {
+      aa.wqkv = (const u16*)w.qkv; aa.xb = b.xb; aa.in_ss = b.ss_x; aa.in_parts = xparts; aa.in_scale = b.sc_x;
+      aa.qkv_t = b.qkv_t; aa.hgen = b.qkv_ctl; aa.hdone = b.qkv_ctl + 1; aa.status = b.control;
+      aa.spin_limit = g_spin_limit.load();
+      if ((st = qd::attention_qkv8_launch(aa, s))) return st;
+    } else if ((st = qd::attention_partial_launch<float>(aa, s))) {
+      return st;
+    }
     // r = x + W_o attn; image of r * post_norm * rstd(x)
     qd::Gemv8Args go;
     base(go, H, (long)Hq * D);

@@ -95,6 +95,21 @@ struct AttnArgs {
   uint16_t* out_img = nullptr;        // merge: batch operand image of the output (instead of out)
   unsigned* done = nullptr;           // [batch][Hkv] arrival counters: the last split of a kv head
                                       // merges in the partial kernel (no merge launch), or null
+  // batch step with the qkv GEMV in the same launch (attention_qkv8_launch):
+  // the first kQkv8Producers workgroups compute 16 rows of
+  // qkv[b] = rstd_b / in_scale[b] * (W_qkv . image(x)[b]) each and hand them
+  // to every workgroup through parity-tagged words in the uncached hand-off
+  // area (qkv_t [kBatchMax][rows]); `qkv` is then unused
+  const uint16_t* wqkv = nullptr;     // fp16 [rows][2048]
+  const uint16_t* xb = nullptr;       // operand image of x [2048/32][64][8]
+  const float* in_ss = nullptr;       // [in_parts][8] partial sums of squares of x
+  int in_parts = 0;
+  const float* in_scale = nullptr;    // [8] scale of the image
+  unsigned* qkv_t = nullptr;
+  unsigned* hgen = nullptr;           // launches so far (the words' parity), advanced by the last workgroup
+  unsigned* hdone = nullptr;          // workgroups finished in this launch (self-resetting)
+  unsigned* status = nullptr;         // bit 0: a hand-off wait ran out of its polling budget
+  unsigned spin_limit = 0;            // polls per thread and launch (0: the default)
 };
 
 // Partials of every (kv head, split); fused prologue when a.qkv != nullptr.
@@ -102,6 +117,16 @@ template <typename TQ>
 int attention_partial_launch(const AttnArgs& a, hipStream_t s);
 template <typename TO>
 int attention_merge_launch(const AttnArgs& a, hipStream_t s);
+// Batch step: the qkv GEMV and the fused attention (q/k norm + RoPE + K/V
+// write + split-KV + merge into out_img) in one launch of batch * Hkv * n_split
+// workgroups, the first kQkv8Producers of which produce the qkv rows (the
+// launch needs them resident together: one per CU on 256 CUs).  Hq = 2 Hkv,
+// head dim 128, qkv rows = kQkv8Producers * 16, K = 2048, a.done set.
+constexpr int kQkv8Producers = 256;
+int attention_qkv8_launch(const AttnArgs& a, hipStream_t s);
+// True when the current device keeps kQkv8Producers workgroups of that launch
+// resident at once (queried once per device).
+bool attention_qkv8_device_ok();
 
 // ---------------------------------------------------------------- small ops
 

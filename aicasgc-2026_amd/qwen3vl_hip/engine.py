@@ -431,12 +431,16 @@ class BatchDecodeEngine(_CapturedSteps):
     step is ``qd_decode_step`` with ``batch = B`` (MFMA batch GEMVs, per-sequence
     split-KV attention, per-sequence argmax) followed by the advance of
     ``qd_decode_advance_batch`` (done by the argmax reduction itself unless
-    ``fuse_advance`` is False), captured once into a HIP graph.  The reference
-    has no batch decode path (it rejects batch != 1, evaluation_wrapper.py:110-111).
+    ``fuse_advance`` is False), captured once into a HIP graph.  With
+    ``fuse_qkv`` (default) each layer's qkv GEMV runs inside its attention
+    launch where the library allows it (``QD_STEP_AUTO``); False keeps two
+    launches.  The reference has no batch decode path (it rejects batch != 1,
+    evaluation_wrapper.py:110-111).
     """
 
     def __init__(self, weights: ModelWeights, batch: int, capacity: int, device="cuda", attn_splits: int = 0,
-                 keep_logits: bool = False, steps_per_graph: int = 4, fuse_advance: bool = True):
+                 keep_logits: bool = False, steps_per_graph: int = 4, fuse_advance: bool = True,
+                 fuse_qkv: bool = True):
         if not torch.cuda.is_available():
             raise RuntimeError("BatchDecodeEngine needs a ROCm GPU")
         if steps_per_graph < 1:
@@ -487,7 +491,9 @@ class BatchDecodeEngine(_CapturedSteps):
         d.rope_position = self.rope_position.data_ptr()
         d.logits_out = self.logits.data_ptr() if self.logits is not None else None
         d.attn_splits = int(attn_splits)
-        d.step_mode = _lib.STEP_CHAIN
+        # AUTO: each layer's qkv GEMV runs inside its attention launch where the
+        # device allows it; CHAIN: two launches
+        d.step_mode = _lib.STEP_AUTO if fuse_qkv else _lib.STEP_CHAIN
         d.batch = B
         nbytes = _lib.lib().qd_decode_workspace_bytes(ctypes.byref(d))
         self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
@@ -531,6 +537,13 @@ class BatchDecodeEngine(_CapturedSteps):
             ctypes.c_void_p(self.step_counter.data_ptr()), ctypes.c_void_p(self.cache_position.data_ptr()),
             ctypes.c_void_p(self.rope_position.data_ptr()), int(self.out_tokens.shape[0]), self.batch, st),
             "qd_decode_advance_batch")
+
+    def status(self, reset: bool = True) -> int:
+        """Status word of the batch step's hand-offs (0: every wait completed)."""
+        v = ctypes.c_uint(0)
+        _lib.check(_lib.lib().qd_decode_status(ctypes.byref(self.desc), ctypes.byref(v), int(reset)),
+                   "qd_decode_status")
+        return int(v.value)
 
     def _snapshot(self):
         pos = self.cache_position.tolist()

@@ -323,7 +323,14 @@ typedef struct qd_model_desc {
  *                       shape, needs 256 resident workgroups of 512 threads);
  *   QD_STEP_AUTO        persistent when possible, else the chain.
  * The attention of the persistent kernel always uses 32 splits per kv head;
- * attn_splits applies to the chain. */
+ * attn_splits applies to the chain.  Batch step (batch 2..8): QD_STEP_AUTO
+ * runs each layer's qkv GEMV inside its attention launch, the first 256
+ * workgroups computing 16 qkv rows each and handing them to the attention
+ * workgroups through parity-tagged words in the workspace (bounded waits,
+ * reported by qd_decode_status), when the shape allows it (H = 2048, Hq = 2 Hkv,
+ * head dim 128, 4096 qkv rows, batch x Hkv x splits >= 256) and the device keeps
+ * 256 of its workgroups resident; QD_STEP_CHAIN keeps the two launches;
+ * QD_STEP_PERSISTENT is rejected. */
 #define QD_STEP_AUTO 0
 #define QD_STEP_CHAIN 1
 #define QD_STEP_PERSISTENT 2
@@ -475,9 +482,10 @@ int qd_persistent_set_spin_limit(unsigned polls);
  * cuda_decode_gemv_ops/profile.py, are out of scope). */
 int qd_persistent_trace_read(uint64_t* dst, size_t n, int* dims);
 
-/* Synchronously reads the persistent step's status word (0 = every hand-off
- * completed; bit 0 = a wait exhausted its spin budget, results of that step
- * are invalid) and clears it when reset != 0. */
+/* Synchronously reads the status word of the persistent step, or of the
+ * batch step's qkv hand-off (0 = every hand-off completed; bit 0 = a wait
+ * exhausted its spin budget, results of that step are invalid) and clears it
+ * when reset != 0. */
 int qd_decode_status(const qd_model_desc* d, unsigned* status, int reset);
 
 /* Batch decoding (batch 2..8 in qd_model_desc.batch).  qd_decode_step runs

@@ -305,3 +305,69 @@ def test_batch_full_model_config4_lengths(cuda):
     print(f"gpu {got}\noracle {ref}\nmargins {margins}", flush=True)
     assert_close_rel(gpu_logits, logits, what=f"28-layer batch logits at config-4 lengths (step {n_steps - 1})")
     assert got == ref
+
+
+def test_batch_qkv_in_attention_launch_equals_two_launches(cuda, two_layer_weights):
+    """The batch step's qkv GEMV inside the attention launch (the default,
+    parity-tagged hand-off to the attention workgroups) against the same step
+    with the GEMV as a launch of its own, at config-4 lengths: three
+    graph-replayed steps, tokens equal, logits and written K/V rows within the
+    kernels' tolerance, status word clear."""
+    from qwen3vl_hip import synthetic as syn
+    from qwen3vl_hip.engine import BatchDecodeEngine
+
+    w = two_layer_weights
+    positions = [int(v) for v in syn.batch8_kv_lengths()]
+    tokens = [17, 4000, 8191, 2, 555, 1234, 6000, 42]
+    cap = max(positions) + 8
+    res = {}
+    for fuse in (True, False):
+        print(f"case batch qkv fusion={fuse}", flush=True)
+        eng = BatchDecodeEngine(w, batch=8, capacity=cap, keep_logits=True, fuse_qkv=fuse)
+        _fill_caches_device(eng, positions, 43)
+        got = eng.decode(tokens, positions, positions, 3, use_graph=True)
+        rows = [(eng.k_caches[li][:, :, min(positions):max(positions) + 3].cpu(),
+                 eng.v_caches[li][:, :, min(positions):max(positions) + 3].cpu()) for li in range(2)]
+        res[fuse] = (got, eng.logits.cpu(), rows, eng.status())
+        del eng
+    (g1, l1, r1, s1), (g0, l0, r0, s0) = res[True], res[False]
+    assert s1 == 0 and s0 == 0
+    print(f"fused {g1}\ntwo launches {g0}", flush=True)
+    assert_close_rel(l1, l0, what="batch logits, qkv in the attention launch vs its own launch")
+    for li in range(2):
+        assert_close_rel(r1[li][0].float(), r0[li][0].float(), what=f"K rows layer {li}")
+        assert_close_rel(r1[li][1].float(), r0[li][1].float(), what=f"V rows layer {li}")
+    assert g1 == g0
+
+
+def test_batch_qkv_hand_off_exhausted_wait_is_reported(cuda, two_layer_weights):
+    """With a one-poll budget the qkv hand-off's waits run out: the status word
+    reports it (which also shows that the step ran the hand-off), and the next
+    step with the default budget is unaffected."""
+    from qwen3vl_hip import _lib
+    from qwen3vl_hip.engine import BatchDecodeEngine
+
+    w = two_layer_weights
+    positions = [5, 17, 0, 63, 100, 33, 1, 77]
+    tokens = [123, 4000, 7, 8191, 55, 1024, 2048, 3]
+    eng = BatchDecodeEngine(w, batch=8, capacity=128, keep_logits=True)
+
+    def run():
+        _fill_caches(eng, positions, 19)
+        eng.decode(tokens, positions, positions, 1, use_graph=False)
+        torch.cuda.synchronize()
+        return eng.logits.cpu().clone(), eng.status()
+
+    ref, st = run()
+    assert st == 0
+    lib = _lib.lib()
+    print("case batch step with a one-poll budget", flush=True)
+    _lib.check(lib.qd_persistent_set_spin_limit(1), "qd_persistent_set_spin_limit")
+    try:
+        _, st_bad = run()
+    finally:
+        _lib.check(lib.qd_persistent_set_spin_limit(0), "qd_persistent_set_spin_limit")
+    assert st_bad & 1, "a batch step with a one-poll budget reported no exhausted wait"
+    again, st = run()
+    assert st == 0
+    assert torch.equal(again, ref)
