@@ -454,11 +454,12 @@ int qd_persistent_prepare(void* stream);
 
 /* Diagnostic: every later persistent launch of the process (qd_decode_step in
  * persistent mode, qd_decode_layers_persistent, qd_decoder_layer_persistent_f16)
- * lets each thread poll at most `polls` times over the whole launch before
- * its hand-off waits give up (0 restores the default, tens of milliseconds of
- * polling).  A launch whose budget runs out sets bit 0 of its status word,
- * finishes every wave and writes every hand-off word once per layer, so the
- * next launch is unaffected; its own results are invalid.  Launches already
+ * and every later batch step's qkv hand-off lets each thread poll at most
+ * `polls` times over the whole launch before its hand-off waits give up (0
+ * restores the default, tens of milliseconds of polling).  A launch whose
+ * budget runs out sets bit 0 of its status word, finishes every wave and
+ * writes every hand-off word once per layer, so the next launch is
+ * unaffected; its own results are invalid.  Launches already
  * captured in a graph keep the limit they were captured with.  For tests of
  * the failure path; no counterpart in the reference (its soft-sync waits are
  * unbounded). */
