@@ -117,7 +117,10 @@ def bench_batch8(w, steps: int, warmup: int = 4, cpu: bool = True) -> dict:
     first_gpu = eng.out_tokens[0].tolist()
     final_pos = eng.cache_position.tolist()
     counter = int(eng.step_counter.item())
+    status = eng.status()
     del eng
+    if status != 0:
+        raise RuntimeError(f"batch8: a qkv hand-off wait ran out of its polling budget (status {status})")
     if counter != n or final_pos != [L + n for L in lens]:
         raise RuntimeError(f"batch8: device positions did not advance {n} steps: counter {counter}, {final_pos}")
     check = batch8_first_step_check(w, tokens, lens, host_caches, first_gpu)
