@@ -379,16 +379,17 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
   }
   constexpr int kStep = kSlots * kUnroll;
   u32x4 kk[kUnroll], vv[kUnroll], kn[kUnroll], vn[kUnroll];
+  // XQKV: only the first batch is requested before the hand-off.  A wave's
+  // loads complete in issue order and the memory side serves the chip's
+  // requests in order, so every K/V batch requested before the polls delays
+  // them by its drain time, while one batch in flight keeps HBM busy as the
+  // producers' rows arrive (measured: both batches first, or none, ran slower
+  // than the qkv GEMV as a launch of its own; one batch first ran faster).
   __builtin_amdgcn_sched_barrier(0);   // every prologue input is requested before the K/V rows
   load_kv_batch(kb, vb, a.stride_s, wave_t0 + row_off, t1, kk, vv);
   if constexpr (!XQKV) load_kv_batch(kb, vb, a.stride_s, wave_t0 + kStep + row_off, t1, kn, vn);
-  __builtin_amdgcn_sched_barrier(0);   // both batches issued before the prologue's math waits
+  __builtin_amdgcn_sched_barrier(0);   // the batches issued before the prologue's math waits
 
-  // XQKV: the hand-off comes before the K/V rows are requested.  A wave's
-  // loads complete in issue order and the memory side serves the chip's
-  // requests in order, so polls issued behind every workgroup's K/V batches
-  // would wait for all of them (measured: no gain over two launches); issued
-  // first, they wait only behind the producers' weight rows.
   if constexpr (XQKV) {
     __shared__ float s_part[kQkvWaves][kBatchMax][16];
     __shared__ float s_fac[kBatchMax];
@@ -406,7 +407,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
         take_words(words + row + j, kHalf, par, left, a.status, pre[i][0], pre[i][1]);
       }
     }
-    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_sched_barrier(0);   // the second batch behind the polls
     load_kv_batch(kb, vb, a.stride_s, wave_t0 + kStep + row_off, t1, kn, vn);
     __builtin_amdgcn_sched_barrier(0);
   }
