@@ -307,23 +307,25 @@ def test_batch_full_model_config4_lengths(cuda):
     assert got == ref
 
 
-def test_batch_qkv_in_attention_launch_equals_two_launches(cuda, two_layer_weights):
+@pytest.mark.parametrize("batch", [8, 3])
+def test_batch_qkv_in_attention_launch_equals_two_launches(cuda, two_layer_weights, batch):
     """The batch step's qkv GEMV inside the attention launch (the default,
     parity-tagged hand-off to the attention workgroups) against the same step
     with the GEMV as a launch of its own, at config-4 lengths: three
     graph-replayed steps, tokens equal, logits and written K/V rows within the
-    kernels' tolerance, status word clear."""
+    kernels' tolerance, status word clear.  Batch 3 (19 splits per sequence,
+    456 workgroups) leaves the producers' rows of sequences 3..7 unwritten."""
     from qwen3vl_hip import synthetic as syn
     from qwen3vl_hip.engine import BatchDecodeEngine
 
     w = two_layer_weights
-    positions = [int(v) for v in syn.batch8_kv_lengths()]
-    tokens = [17, 4000, 8191, 2, 555, 1234, 6000, 42]
+    positions = [int(v) for v in syn.batch8_kv_lengths()][:batch]
+    tokens = [17, 4000, 8191, 2, 555, 1234, 6000, 42][:batch]
     cap = max(positions) + 8
     res = {}
     for fuse in (True, False):
-        print(f"case batch qkv fusion={fuse}", flush=True)
-        eng = BatchDecodeEngine(w, batch=8, capacity=cap, keep_logits=True, fuse_qkv=fuse)
+        print(f"case batch {batch} qkv fusion={fuse}", flush=True)
+        eng = BatchDecodeEngine(w, batch=batch, capacity=cap, keep_logits=True, fuse_qkv=fuse)
         _fill_caches_device(eng, positions, 43)
         got = eng.decode(tokens, positions, positions, 3, use_graph=True)
         rows = [(eng.k_caches[li][:, :, min(positions):max(positions) + 3].cpu(),
@@ -340,17 +342,39 @@ def test_batch_qkv_in_attention_launch_equals_two_launches(cuda, two_layer_weigh
     assert g1 == g0
 
 
-def test_batch_qkv_hand_off_exhausted_wait_is_reported(cuda, two_layer_weights):
+def test_batch_partial_batch_qkv_in_attention_launch_matches_oracle(cuda, two_layer_weights):
+    """Batch 3 at the first three config-4 lengths, qkv GEMV inside the
+    attention launch (456 workgroups): one step against the oracle's."""
+    from qwen3vl_hip import synthetic as syn
+    from qwen3vl_hip.engine import BatchDecodeEngine
+
+    w = two_layer_weights
+    positions = [int(v) for v in syn.batch8_kv_lengths()][:3]
+    tokens = [100, 8000, 300]
+    eng = BatchDecodeEngine(w, batch=3, capacity=max(positions) + 8, keep_logits=True)
+    caches = _fill_caches_device(eng, positions, 31)
+    print(f"case batch 3 fused qkv at {positions}", flush=True)
+    out = eng.decode(tokens, positions, positions, 1, use_graph=False)
+    assert eng.status() == 0
+    logits, toks = O.decode_step_batch(w, tokens, caches, positions, positions,
+                                       shape=O.OracleShape(num_layers=2, vocab=VOCAB))
+    assert_close_rel(eng.logits.cpu(), logits, what="batch-3 logits, qkv in the attention launch")
+    assert out[0] == toks
+
+
+@pytest.mark.parametrize("batch,capacity", [(8, 128), (3, 4096)])
+def test_batch_qkv_hand_off_exhausted_wait_is_reported(cuda, two_layer_weights, batch, capacity):
     """With a one-poll budget the qkv hand-off's waits run out: the status word
-    reports it (which also shows that the step ran the hand-off), and the next
-    step with the default budget is unaffected."""
+    reports it (which also shows that the step ran the hand-off: at batch 8 and
+    128 rows the grid has 256 workgroups, at batch 3 and 4096 rows 504), and
+    the next step with the default budget is unaffected."""
     from qwen3vl_hip import _lib
     from qwen3vl_hip.engine import BatchDecodeEngine
 
     w = two_layer_weights
-    positions = [5, 17, 0, 63, 100, 33, 1, 77]
-    tokens = [123, 4000, 7, 8191, 55, 1024, 2048, 3]
-    eng = BatchDecodeEngine(w, batch=8, capacity=128, keep_logits=True)
+    positions = [5, 17, 0, 63, 100, 33, 1, 77][:batch]
+    tokens = [123, 4000, 7, 8191, 55, 1024, 2048, 3][:batch]
+    eng = BatchDecodeEngine(w, batch=batch, capacity=capacity, keep_logits=True)
 
     def run():
         _fill_caches(eng, positions, 19)
