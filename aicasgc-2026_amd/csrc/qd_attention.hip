@@ -271,9 +271,11 @@ __device__ __forceinline__ void qkv8_produce(const AttnArgs& a, int p, int w, in
 #pragma unroll
     for (int q = 0; q < kQkvWaves; ++q) v += s_part[q][seq][rl];
     v *= s_fac[seq];
-    if (seq < a.batch)
-      __hip_atomic_store(a.qkv_t + (long)seq * kQkv8Producers * 16 + p * 16 + rl, tagged_word(v, par),
-                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // every sequence slot's word, also past the batch (factor 0), so each word
+    // is written once per launch whatever batch the launches on this
+    // workspace run
+    __hip_atomic_store(a.qkv_t + (long)seq * kQkv8Producers * 16 + p * 16 + rl, tagged_word(v, par),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   stores_done();   // polling with a store of the wave still in flight is much slower
 }

@@ -293,7 +293,10 @@ typedef struct qd_model_desc {
   const int64_t* cache_position;   /* int64 [1] */
   const int64_t* rope_position;    /* int64 [3]: T/H/W rope positions of this step */
   void* logits_out;            /* fp16 [V] or NULL */
-  void* workspace;             /* qd_decode_workspace_bytes() bytes, zeroed once */
+  void* workspace;             /* qd_decode_workspace_bytes() bytes, zeroed once; its layout
+                                  and self-resetting counters follow this descriptor's batch,
+                                  capacity and attn_splits: a descriptor that changes any of
+                                  them needs a workspace of its own, zeroed */
   int attn_splits;             /* 0 = qd_attention_default_splits(capacity) */
   int step_mode;               /* QD_STEP_AUTO / QD_STEP_CHAIN / QD_STEP_PERSISTENT */
   int batch;                   /* sequences per step: 0 or 1 = batch 1; 2..8 = batch step, then
