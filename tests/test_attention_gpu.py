@@ -163,3 +163,28 @@ def test_attention_unsupported_returns_none(cuda):
     # head_dim 64 is not supported -> None (caller falls back)
     assert A.decode_attn_v4_fused(q[..., :64].contiguous().to(cuda), kc[..., :64].contiguous().to(cuda),
                                   vc[..., :64].contiguous().to(cuda), SCALE, 2, cp) is None
+
+
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (16, 4), (32, 8)])       # GQA groups 1, 4, 4
+@pytest.mark.parametrize("L,split_k", [(700, 4), (5000, 40)])          # merge in the partial kernel / merge kernel
+def test_attention_other_gqa_groups(cuda, hq, hkv, L, split_k):
+    """Group sizes 1 and 4, which the entry points accept besides Qwen3-VL's 2,
+    against the oracle; one length merged by the last split of each kv head,
+    one with enough splits for the separate merge launch, a stale tail."""
+    import cuda_decode_attention as A
+    from qwen3vl_hip import synthetic as syn
+
+    cap = L + 64
+    q = syn.normal(11, ("q", hq, hkv, L), (1, hq, 1, 128))
+    kc = syn.normal(11, ("k_cache", hq, hkv, L), (1, hkv, cap, 128))
+    vc = syn.normal(11, ("v_cache", hq, hkv, L), (1, hkv, cap, 128))
+    kc[:, :, L:] = 60000.0
+    vc[:, :, L:] = 60000.0
+    pos = L - 1
+    print(f"case attention Hq={hq} Hkv={hkv} L={L} split_k={split_k}", flush=True)
+    cp = torch.tensor([pos], dtype=torch.int64, device=cuda)
+    ref = O.decode_attention(q.reshape(hq, 128), kc, vc, pos, SCALE)
+    for fn in (A.decode_attn_v4_cta_qhead_splitkv_fused, A.decode_attn_v4_splitkv):
+        out = fn(q.to(cuda), kc.to(cuda), vc.to(cuda), SCALE, hq // hkv, cp, split_k=split_k)
+        assert out is not None and out.shape == (1, 1, hq, 128)
+        assert_close_rel(out.reshape(hq, 128), ref, what=f"{fn.__name__} Hq={hq} Hkv={hkv} L={L}")
