@@ -188,3 +188,20 @@ def test_attention_other_gqa_groups(cuda, hq, hkv, L, split_k):
         out = fn(q.to(cuda), kc.to(cuda), vc.to(cuda), SCALE, hq // hkv, cp, split_k=split_k)
         assert out is not None and out.shape == (1, 1, hq, 128)
         assert_close_rel(out.reshape(hq, 128), ref, what=f"{fn.__name__} Hq={hq} Hkv={hkv} L={L}")
+
+
+def test_grouped_prefix_entry_points(cuda):
+    """The reference's older split-KV entry points (cuda_decode_attention.py:90-215)
+    give the same attention, and decline a split count of 1 as the reference does."""
+    import cuda_decode_attention as A
+    from qwen3vl_hip import synthetic as syn
+
+    q, kc, vc, pos = syn.attention_inputs(1500, capacity=1600)
+    ref = O.decode_attention(q.reshape(16, 128), kc, vc, pos, SCALE)
+    for fn in (A.grouped_prefix_cachepos_splitkv, A.grouped_prefix_cachepos_splitkv_qhead):
+        print(f"case {fn.__name__}", flush=True)
+        cp = torch.tensor([pos], dtype=torch.int64, device=cuda)
+        assert fn(q.to(cuda), kc.to(cuda), vc.to(cuda), SCALE, 2, cp, 1) is None
+        out = fn(q.to(cuda), kc.to(cuda), vc.to(cuda), SCALE, 2, cp, 8)
+        assert out is not None
+        assert_close_rel(out.reshape(16, 128), ref, what=fn.__name__)
