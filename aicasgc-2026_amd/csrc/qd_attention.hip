@@ -597,63 +597,50 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
 }
 
 // out[h, d] = sum_s w_s o_s[d] / sum_s w_s with w_s = exp(lse_s - max lse).
-// One 256-thread block per q head: the split LSEs are staged in LDS in one
-// parallel load, then each half of the block sums every other split for all
-// 128 dims with the partial loads issued kMergeUnroll at a time.
+// One wave per (q head, half of the 128 dims): lane s reads the LSE of split s
+// and every lane the partials of its dim for 64 splits, every load issued
+// before the first is used (unconditional, index clamped to the last split; a
+// clamped duplicate gets weight 0), so up to 64 splits cost one round trip.
+// Lane s's weight reaches the other lanes by readlane.  More splits run in
+// chunks of 64 with a running maximum.  Empty splits (lse = -inf) weigh 0; a
+// NaN LSE makes the sum of weights NaN and the output 0, as in the in-kernel
+// merge.
 constexpr int kMergeMaxSplits = 1024;
-constexpr int kMergeUnroll = 8;
+constexpr int kMergeChunk = kWave;
 
 template <typename TO>
-__global__ __launch_bounds__(256) void attn_merge_kernel(const AttnArgs a) {
-  __shared__ float s_w[kMergeMaxSplits];
-  __shared__ float s_num[kD];
-  __shared__ float s_red[4];
-  const int h = blockIdx.x;
+__global__ __launch_bounds__(kWave) void attn_merge_kernel(const AttnArgs a) {
+  const int h = (int)(blockIdx.x >> 1);
+  const int lane = lane_id();
+  const int d = (int)(blockIdx.x & 1u) * kWave + lane;
   const int S = a.n_split;
   const long bq = blockIdx.y;   // sequence of a batch
   const float* lse = a.lse + (bq * a.Hq + h) * S;
-  float mx = -INFINITY;
-  for (int s = threadIdx.x; s < S; s += blockDim.x) {
-    const float v = lse[s];
-    s_w[s] = v;
-    mx = fmaxf(mx, v);
-  }
-  mx = wave_max(mx);
-  if (lane_id() == 0) s_red[threadIdx.x / kWave] = mx;
-  __syncthreads();
-  const float M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
-  __syncthreads();
-  for (int s = threadIdx.x; s < S; s += blockDim.x) s_w[s] = (M == -INFINITY) ? 0.f : __expf(s_w[s] - M);
-  __syncthreads();
-  const int d = threadIdx.x & (kD - 1);
-  const int half = threadIdx.x >> 7;
   const float* op = a.o_part + (bq * a.Hq + h) * S * kD + d;
-  float num = 0.f;
-  for (int s0 = half; s0 < S; s0 += 2 * kMergeUnroll) {
-    float v[kMergeUnroll];
+  float M = -INFINITY, num = 0.f, den = 0.f;
+  for (int c = 0; c < S; c += kMergeChunk) {
+    const int n = min(kMergeChunk, S - c);
+    const float l = lane < n ? lse[c + lane] : -INFINITY;
+    float v[kMergeChunk];
 #pragma unroll
-    for (int u = 0; u < kMergeUnroll; ++u) {
-      const int s = s0 + 2 * u;
-      v[u] = s < S ? op[(long)s * kD] : 0.f;
-    }
+    for (int u = 0; u < kMergeChunk; ++u) v[u] = op[(long)min(c + u, S - 1) * kD];
+    const float mn = fmaxf(M, wave_max(l));
+    if (mn != -INFINITY) {
+      const float r = M == -INFINITY ? 0.f : __expf(M - mn);   // num = den = 0 while M = -inf
+      num *= r;
+      den *= r;
+      const float w = __expf(l - mn);                            // 0 for lanes >= n
+      den += wave_sum(w);
 #pragma unroll
-    for (int u = 0; u < kMergeUnroll; ++u) {
-      const int s = s0 + 2 * u;
-      if (s < S) num = __builtin_fmaf(s_w[s], v[u], num);
+      for (int u = 0; u < kMergeChunk; ++u) num = __builtin_fmaf(readlane(w, u), v[u], num);
+      M = mn;
     }
   }
-  if (half == 1) s_num[d] = num;
-  __syncthreads();
-  if (half == 0) {
-    float den = 0.f;
-    for (int s = 0; s < S; ++s) den += s_w[s];
-    num += s_num[d];
-    const float o = den > 0.f ? num / den : 0.f;
-    if (a.out_img != nullptr)
-      bimg_store(a.out_img, (int)bq, (long)h * kD + d, o);
-    else
-      store_act(reinterpret_cast<TO*>(a.out), (bq * a.Hq + h) * kD + d, o);
-  }
+  const float o = den > 0.f ? num / den : 0.f;
+  if (a.out_img != nullptr)
+    bimg_store(a.out_img, (int)bq, (long)h * kD + d, o);
+  else
+    store_act(reinterpret_cast<TO*>(a.out), (bq * a.Hq + h) * kD + d, o);
 }
 
 template <typename TQ, bool FUSED>
@@ -707,7 +694,7 @@ int attention_qkv8_launch(const AttnArgs& a, hipStream_t s) {
 template <typename TO>
 int attention_merge_launch(const AttnArgs& a, hipStream_t s) {
   if (a.n_split > kMergeMaxSplits) return QD_ERR_SHAPE;
-  hipLaunchKernelGGL((attn_merge_kernel<TO>), dim3((unsigned)a.Hq, (unsigned)a.batch), dim3(256), 0, s, a);
+  hipLaunchKernelGGL((attn_merge_kernel<TO>), dim3(2u * (unsigned)a.Hq, (unsigned)a.batch), dim3(kWave), 0, s, a);
   return qd_host::launch_status("attn_merge_kernel");
 }
 

@@ -352,16 +352,16 @@ int qd_add_f16(const void* a, const void* b, void* out, long n, void* stream) {
 size_t qd_attention_workspace_bytes(int Hq, int Hkv, int n_split) { return attn_ws_bytes(Hq, Hkv, n_split); }
 
 int qd_attention_default_splits(int T) {
-  // ~128 positions per workgroup, at least 4 and at most 16 splits per kv head,
-  // so the merge runs in the partial kernel (one launch); from 8192 rows on, 32
-  // splits with the merge kernel (all 256 CUs busy).  Measured per call at
-  // T = L, cold copies: 8 splits are fastest at 1024 and 16 at 4096 (32: +5%);
-  // 32 against 16 splits take 12.3 / 17.8 / 28.0 against 12.8 / 19.9 / 33.0 us
-  // at 8192 / 16384 / 32768; 48 and 64 splits are slower than 32 everywhere.
-  if (T >= 8192) return 32;
+  // ~128 positions per workgroup, at least 4 and at most 32 splits per kv
+  // head.  Up to 16 splits (T <= 2048) the merge runs in the partial kernel (one
+  // launch); beyond, the merge kernel (one round trip for up to 64 splits).
+  // Measured per call at T = L, cold copies (16 / 24 / 32 splits, us): 8.14 /
+  // 8.49 / 8.20 at 2048, 9.05 / 8.72 / 9.00 at 3072, 9.75 / 9.61 / 9.34 at
+  // 4096, 11.3 / 10.7 / 10.5 at 6144, 12.8 / 12.4 / 11.6 at 8192, 20.2 / 18.3
+  // / 17.4 at 16384; 48 and 64 splits are no faster than 32.
   int s = (T + 127) / 128;
   if (s < 4) s = 4;
-  if (s > 16) s = 16;
+  if (s > 32) s = 32;
   return s;
 }
 

@@ -258,9 +258,9 @@ int qd_attention_merge(const float* o_part, const float* lse, void* out, int out
                        int Hq, int n_split, void* stream);
 
 /* Default split count for a cache of capacity T (fixed per captured graph):
- * about 128 rows per split, 4..16 splits (the merge then runs in the partial
- * kernel), and 32 from T = 8192 on (with the merge kernel after the partial
- * kernel; 256 workgroups at 8 kv heads). */
+ * about 128 rows per split, 4..32 splits; up to 16 (T <= 2048) the merge runs
+ * in the partial kernel, beyond it the merge kernel follows the partial kernel
+ * (32 splits from T = 3969 on: 256 workgroups at 8 kv heads). */
 int qd_attention_default_splits(int T);
 
 /* ------------------------------------------------------------------ decode step */

@@ -38,8 +38,9 @@ def test_library_host_only_calls():
     assert lib.qd_version() >= 1
     assert lib.qd_attention_default_splits(256) == 4
     assert lib.qd_attention_default_splits(1024) == 8
-    assert lib.qd_attention_default_splits(4096) == 16
-    assert lib.qd_attention_default_splits(8191) == 16
+    assert lib.qd_attention_default_splits(2048) == 16
+    assert lib.qd_attention_default_splits(3072) == 24
+    assert lib.qd_attention_default_splits(4096) == 32
     assert lib.qd_attention_default_splits(8192) == 32
     assert lib.qd_attention_default_splits(1 << 20) == 32
     assert lib.qd_attention_workspace_bytes(16, 8, 4) >= 16 * 4 * 128 * 4
