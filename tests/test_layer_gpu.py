@@ -187,6 +187,8 @@ def test_engine_one_layer_step_config0(cuda):
     ("chain", 2, 600, "inf"),     # 301 rows per split: three trips of the K/V loop, the new row in the third
     ("chain", 2, 600, None),
     ("chain", 1, 700, "nan"),     # one split of 701 rows (six loop trips)
+    ("chain", 24, 600, "nan"),    # more than 16 splits: the merge kernel after the partials
+    ("chain", 80, 1000, "inf"),   # more than 64 splits: the merge kernel's second chunk
     ("persistent", 0, 600, "nan"),
 ])
 def test_engine_step_long_splits_and_poisoned_new_row(cuda, step_mode, splits, pos, poison):
