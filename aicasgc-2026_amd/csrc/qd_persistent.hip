@@ -29,9 +29,12 @@
 // written once per layer and every reader reads the same words at every layer,
 // so the parity alternates between consecutive writes and a reader, having
 // seen the previous write, can only see that write (wrong parity) or the one
-// it waits for: one bit is a complete tag.  A wave waits for its own stores to
-// complete before it polls; polling with a store in flight is several times
-// slower on this part.  The words live in one uncached area per device, shared
+// it waits for: one bit is a complete tag.  The hidden vector (GATE_UP ->
+// DOWN), whose reader takes it as fp16 anyway, moves as 64-bit words of three
+// fp16 values and a 16-bit tag (one word per wave, one 64-bit store): 16
+// instead of 24 KB per workgroup to gather, no value bit given to the tag.
+// A wave waits for its own stores to complete before it polls; polling with a
+// store in flight is several times slower on this part.  The words live in one uncached area per device, shared
 // by every persistent launch on it; the parity follows a per-device layer
 // generation, so launches of different layer counts keep the sequence.
 //
@@ -267,6 +270,72 @@ __device__ __forceinline__ void gather4(Rsrc r, Act* dst, unsigned t, unsigned p
   await4<N>(r, t * 16u, THREADS * 16u, v, par, sp);
 #pragma unroll
   for (int k = 0; k < N; ++k) act_store4(dst, (t + k * THREADS) * 4u, values_of(v[k]));
+}
+
+// The hidden vector's hand-off packs the three values a wave produces into one
+// 64-bit word: three fp16 values (the rounding the DOWN rows' LDS input takes)
+// and a 16-bit tag whose bit 0 is the write parity, stored with one 64-bit
+// atomic store, so the tag and the values of a word change together.
+__device__ __forceinline__ void put3h(unsigned* p, unsigned par, float v0, float v1, float v2) {
+  const uint64_t w = (uint64_t)pack2(v0, v1) | ((uint64_t)((unsigned)f2h(v2) | (par << 16)) << 32);
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool tags3h_ok(u32x4 v, unsigned par) {
+  return ((((v.y >> 16) ^ par) | ((v.w >> 16) ^ par)) & 1u) == 0u;
+}
+constexpr unsigned kPoison3h = 0x7e007e00u;   // fp16 quiet NaN in both halves
+
+template <int N>
+__device__ __forceinline__ void await3h(Rsrc r, unsigned off0, unsigned step, u32x4 (&v)[N], unsigned par,
+                                        Spin& sp) {
+#pragma clang loop unroll(disable)
+  while (true) {
+    bool ok = true;
+#pragma unroll
+    for (int k = 0; k < N; ++k) ok &= tags3h_ok(v[k], par);
+    if (ok) break;
+    if (sp.left == 0) {
+      wait_failed(sp);
+#pragma unroll
+      for (int k = 0; k < N; ++k) v[k] = u32x4{kPoison3h, kPoison3h, kPoison3h, kPoison3h};
+      break;
+    }
+    --sp.left;
+    __builtin_amdgcn_s_sleep(1);
+    repoll4<0, N>(r, off0, step, v);
+  }
+}
+
+// gather4 for the packed words: thread t takes the 16 bytes (two words, six
+// values) t + k THREADS and writes values 6 (t + k THREADS) .. +6 to dst.
+// Every 16-byte read is issued twice, as in gather4.
+template <int N, int THREADS>
+__device__ __forceinline__ void gather3h(Rsrc r, Act* dst, unsigned t, unsigned par, Spin& sp) {
+  u32x4 v[N], v2[N];
+#pragma unroll
+  for (int k = 0; k < N; ++k) v[k] = peek4(r, (t + k * THREADS) * 16u);
+#pragma unroll
+  for (int k = 0; k < N; ++k) v2[k] = peek4(r, (t + k * THREADS) * 16u);
+  {
+    bool ok = true, ok2 = true;
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+      ok &= tags3h_ok(v[k], par);
+      ok2 &= tags3h_ok(v2[k], par);
+    }
+    if (!ok && ok2) {
+#pragma unroll
+      for (int k = 0; k < N; ++k) v[k] = v2[k];
+    }
+  }
+  await3h<N>(r, t * 16u, THREADS * 16u, v, par, sp);
+#pragma unroll
+  for (int k = 0; k < N; ++k) {
+    unsigned* d = reinterpret_cast<unsigned*>(dst + 6u * (t + k * THREADS));
+    d[0] = v[k].x;
+    d[1] = (v[k].y & 0xffffu) | (v[k].z << 16);
+    d[2] = (v[k].z >> 16) | (v[k].w << 16);
+  }
 }
 
 // Sum of squares of four values, in the one order every path uses (the
@@ -875,11 +944,13 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, Ctx& cx, Sm
       rows_dot<4, 6>(wgu, s_r, lane, gu);
       const float rstd = rstd_of(sm.ssr, (float)H, a.eps);
       if (lane == 0) {
+        float hv[3];
 #pragma unroll
         for (int p = 0; p < 3; ++p) {
           const float g = gu[p] * rstd;
-          put(a.hid_t + (long)gw * 3 + p, par, (g / (1.0f + __expf(-g))) * (gu[3 + p] * rstd));
+          hv[p] = (g / (1.0f + __expf(-g))) * (gu[3 + p] * rstd);
         }
+        put3h(a.hid_t + 2L * gw, par, hv[0], hv[1], hv[2]);
       }
       if (!streamer) {
         puts_done();
@@ -901,7 +972,7 @@ __device__ __forceinline__ void persist_layers(const PersistArgs& a, Ctx& cx, Sm
 
     // ================================================================ DOWN
     QD_FRESH_LANE();
-    if (!streamer) gather4<I / (4 * NA * kWave), NA * kWave>(r_hid, s_h, (unsigned)tid, par, sp);
+    if (!streamer) gather3h<I / (6 * NA * kWave), NA * kWave>(r_hid, s_h, (unsigned)tid, par, sp);
     __syncthreads();
     QD_TRACE_AT(l, 11);
     QD_TRACE_ST(l, 14);
