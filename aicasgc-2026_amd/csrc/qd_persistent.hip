@@ -34,9 +34,10 @@
 // fp16 values and a 16-bit tag (one word per wave, one 64-bit store): 16
 // instead of 24 KB per workgroup to gather, no value bit given to the tag.
 // A wave waits for its own stores to complete before it polls; polling with a
-// store in flight is several times slower on this part.  The words live in one uncached area per device, shared
-// by every persistent launch on it; the parity follows a per-device layer
-// generation, so launches of different layer counts keep the sequence.
+// store in flight is several times slower on this part.  The words live in one
+// uncached area per device, shared by every persistent launch on it; the
+// parity follows a per-device layer generation, so launches of different
+// layer counts keep the sequence.
 //
 // Every wait is bounded: a thread polls at most kSpinLimit times per launch,
 // then records an error in the status word and continues, so the grid always
