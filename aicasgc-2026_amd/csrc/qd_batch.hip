@@ -133,7 +133,15 @@ __device__ __forceinline__ void argmax8_finish(const Gemv8Args& a, int nblk) {
 // RG: rows per workgroup, 16 (the MFMA M dimension) or 8 (rows 8..15 of the
 // A operand are zero: twice the workgroups for the same rows, so a shape with
 // few row groups fills the CUs without splitting K).
-template <int KW, int EPI, int RG>
+// TILED: W is stored in MFMA tile order, so each 16-byte load of a lane is
+// already its A operand and a wave's load is one contiguous 1 KB:
+//   RG 16: [rows/16][K/8][16][8], element (g, q, r, e) = W[16 g + r][8 q + e];
+//          lane d of K tile kt reads 16 bytes at ((g K/8 + 4 kt) 16 + d) 8;
+//   RG 8:  [rows/8][K/64][4][2][8][8], element (g, p, c, h, r, e) =
+//          W[8 g + r][64 p + 32 h + 8 c + e]; one load covers the K tile pair
+//          (2 p, 2 p + 1): lanes d % 16 < 8 hold rows 0..7 of tile 2 p, the
+//          others those of tile 2 p + 1, moved down by a row_ror:8 DPP.
+template <int KW, int EPI, int RG, bool TILED = false>
 __global__ __launch_bounds__(512) void gemv8_kernel(const Gemv8Args a) {
   constexpr int KS = KW / kWaves;
   constexpr int NT = KS / kKT;
@@ -146,6 +154,7 @@ __global__ __launch_bounds__(512) void gemv8_kernel(const Gemv8Args a) {
   constexpr int OUT = RG * kB;               // outputs of one row group
   static_assert(RG == 8 || RG == 16, "8 or 16 rows per workgroup");
   static_assert(!ARGMAX || RG == 16, "argmax epilogue: 16 rows per group");
+  static_assert(!(TILED && ARGMAX), "tile order: not the looping lm_head (row-major streams faster there)");
   __shared__ float s_fac[kB], s_osc[kB];
   __shared__ float s_part[NA][kWaves][kB][RG];
   __shared__ int s_last;
@@ -167,6 +176,17 @@ __global__ __launch_bounds__(512) void gemv8_kernel(const Gemv8Args a) {
   static_assert(NT % 2 == 0, "tile pairs");
   // (issued in the order the MFMA loop consumes them: gate pair, up pair, ...)
   auto load_w = [&](int rg, u32x4 (&wt)[NWT], u32x4 (&wt2)[NW2]) {
+    if constexpr (TILED) {
+      // RG 16: tiles 2 j, 2 j + 1 in wt[2 j], wt[2 j + 1]; RG 8: tile pair j in wt[j]
+      const uint16_t* p = a.W + ((long)rg * (a.K / 8) + kb / 8) * RG * 8 + lane * 8;
+      const uint16_t* p2 = p + (a.up_offset / RG) * (a.K / 8) * RG * 8;
+#pragma unroll
+      for (int i = 0; i < NWT; ++i) {
+        wt[i] = ld_stream(p + (long)i * 512);
+        if constexpr (DUAL) wt2[i] = ld_stream(p2 + (long)i * 512);
+      }
+      return;
+    }
     const uint16_t* p = a.W + ((long)rg * RG + (lane >> 3)) * a.ldw + kb + (lane & 7) * 8;
     const uint16_t* p2 = p + a.up_offset * a.ldw;
     const long h8row = 8 * a.ldw;
@@ -184,6 +204,20 @@ __global__ __launch_bounds__(512) void gemv8_kernel(const Gemv8Args a) {
   const int src1 = src0 + 16;
   const bool upper = m >= 8;
   auto pair_to_mfma = [&](const auto& w, int j, u32x4& t0, u32x4& t1) {
+    if constexpr (TILED) {
+      if constexpr (NL == 2) {
+        t0 = w[2 * j];
+        t1 = w[2 * j + 1];
+      } else {
+        const u32x4 z = {0u, 0u, 0u, 0u};
+        const u32x4 x = w[j];
+        const u32x4 r = {dpp_u<kDppRowRor8>(x.x), dpp_u<kDppRowRor8>(x.y), dpp_u<kDppRowRor8>(x.z),
+                         dpp_u<kDppRowRor8>(x.w)};
+        t0 = upper ? z : x;
+        t1 = upper ? z : r;
+      }
+      return;
+    }
     const u32x4 a0 = bpermute4(src0, w[j * NL]);
     const u32x4 a1 = bpermute4(src1, w[j * NL]);
     if constexpr (NL == 2) {
@@ -495,7 +529,20 @@ __global__ void advance8_kernel(const int64_t* token, int64_t* out_tokens, int64
 
 template <int KW, int EPI, int RG>
 int launch8(const Gemv8Args& a, unsigned gx, hipStream_t s) {
-  hipLaunchKernelGGL((gemv8_kernel<KW, EPI, RG>), dim3(gx, (unsigned)a.ksplit), dim3(kWaves * kWave), 0, s, a);
+  if (a.w_tiled)
+    hipLaunchKernelGGL((gemv8_kernel<KW, EPI, RG, true>), dim3(gx, (unsigned)a.ksplit), dim3(kWaves * kWave), 0, s,
+                       a);
+  else
+    hipLaunchKernelGGL((gemv8_kernel<KW, EPI, RG>), dim3(gx, (unsigned)a.ksplit), dim3(kWaves * kWave), 0, s, a);
+  return qd_host::launch_status("gemv8_kernel");
+}
+
+// Only the row-major form for the looping lm_head.
+template <>
+int launch8<2048, EPI_ARGMAX, 16>(const Gemv8Args& a, unsigned gx, hipStream_t s) {
+  if (a.w_tiled) return QD_ERR_SHAPE;
+  hipLaunchKernelGGL((gemv8_kernel<2048, EPI_ARGMAX, 16>), dim3(gx, (unsigned)a.ksplit), dim3(kWaves * kWave), 0, s,
+                     a);
   return qd_host::launch_status("gemv8_kernel");
 }
 

@@ -866,6 +866,18 @@ int batch_step(const qd_model_desc* d, hipStream_t s) {
     g.nseq = B; g.eps = d->eps; g.N = N; g.K = K; g.ldw = K; g.ksplit = sp.ksplit; g.rows_per_group = sp.rows_per_group;
     g.kpart = b.kpart; g.kcount = b.kcount;
   };
+  // o_proj, gate_up and down in tile order (qd_model_desc.batch_tiled_weights):
+  // every row group of the layout the GEMV's row group size implies
+  const int gu_tiled = d->batch_tiled_weights ? 1 : 0;
+  if (gu_tiled) {
+    const struct { long rows, K; bool silu; } m[3] = {{H, (long)Hq * D, false}, {I, H, true}, {H, I, false}};
+    for (const auto& x : m) {
+      const int rg = batch_split(x.rows, x.K, x.silu).rows_per_group;
+      QD_REQUIRE(x.rows % rg == 0 && x.K % (rg == 8 ? 64 : 32) == 0, QD_ERR_SHAPE,
+                 "tile-ordered weights need rows %% %d == 0 and K %% %d == 0 (%ld x %ld)", rg, rg == 8 ? 64 : 32, x.rows,
+                 x.K);
+    }
+  }
   for (int li = 0; li < d->num_layers; ++li) {
     const qd_layer_weights& w = d->layers[li];
     const int xparts = li == 0 ? 1 : x_parts;   // the embedding kernel writes one partial
@@ -897,13 +909,14 @@ int batch_step(const qd_model_desc* d, hipStream_t s) {
     qd::Gemv8Args go;
     base(go, H, (long)Hq * D);
     go.xb = b.ab; go.W = (const u16*)w.o_proj; go.residual = b.x; go.ldr = H; go.y = b.r; go.ldy = H;
+    go.w_tiled = gu_tiled;
     go.yb = b.rb; go.yb_gamma = (const u16*)w.post_norm; go.pre_ss = b.ss_x; go.pre_parts = xparts;
     go.out_scale = b.sc_r; go.yss = b.ss_r;
     if ((st = qd::gemv8_launch(go, qd::EPI_STORE, s))) return st;
     qd::Gemv8Args gu;
     base(gu, I, H, true);
     gu.xb = b.rb; gu.in_ss = b.ss_r; gu.in_parts = r_parts; gu.in_scale = b.sc_r; gu.W = (const u16*)w.gate_up;
-    gu.up_offset = I; gu.yb = b.hb;
+    gu.up_offset = I; gu.yb = b.hb; gu.w_tiled = gu_tiled;
     if ((st = qd::gemv8_launch(gu, qd::EPI_SILU, s))) return st;
     // x = r + W_down hidden; image of x * (next input_norm | final_norm) * rstd(r)
     const u16* next_gamma =
@@ -912,7 +925,7 @@ int batch_step(const qd_model_desc* d, hipStream_t s) {
     base(gd, H, I);
     gd.xb = b.hb; gd.W = (const u16*)w.down; gd.residual = b.r; gd.ldr = H; gd.y = b.x; gd.ldy = H;
     gd.yb = b.xb; gd.yb_gamma = next_gamma; gd.pre_ss = b.ss_r; gd.pre_parts = r_parts; gd.out_scale = b.sc_x;
-    gd.yss = b.ss_x;
+    gd.yss = b.ss_x; gd.w_tiled = gu_tiled;
     if ((st = qd::gemv8_launch(gd, qd::EPI_STORE, s))) return st;
   }
   // final RMSNorm (applied through the image of x), tied lm_head, per-sequence argmax
@@ -1183,6 +1196,11 @@ int qd_decode_advance_batch(const int64_t* token, int64_t* out_tokens, int64_t* 
   QD_REQUIRE(batch >= 1 && batch <= qd::kBatchMax, QD_ERR_SHAPE, "batch %d outside 1..%d", batch, qd::kBatchMax);
   return qd::advance8_launch(token, out_tokens, counter, cache_position, rope_position, max_tokens, batch,
                              S(stream));
+}
+
+int qd_batch_tile_rows(long rows, long K, int silu) {
+  if (rows <= 0 || K <= 0) return 0;
+  return batch_split(rows, K, silu != 0).rows_per_group;
 }
 
 size_t qd_batch_gemv_workspace_bytes(long N, long K) {

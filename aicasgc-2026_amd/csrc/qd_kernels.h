@@ -263,8 +263,9 @@ struct Gemv8Args {
   int in_parts = 0;
   const float* in_scale = nullptr; // [8] scale of the input image, or null (1)
   float eps = 1e-6f;
-  const uint16_t* W = nullptr;     // fp16 [rows][ldw]
+  const uint16_t* W = nullptr;     // fp16 [rows][ldw], or in tile order (w_tiled)
   long ldw = 0;
+  int w_tiled = 0;                 // W in MFMA tile order (gemv8_tile_order; not EPI_ARGMAX)
   long N = 0;                      // output rows (EPI_SILU: gate rows == up rows == up_offset)
   long K = 0;
   long up_offset = 0;

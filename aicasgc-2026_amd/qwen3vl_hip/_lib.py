@@ -79,6 +79,7 @@ _SIGS = {
     "qd_decode_status": (c_int, [P, POINTER(ctypes.c_uint), c_int]),
     "qd_persistent_trace_read": (c_int, [P, c_size_t, POINTER(c_int)]),
     "qd_batch_gemv_workspace_bytes": (ctypes.c_size_t, [c_long, c_long]),
+    "qd_batch_tile_rows": (c_int, [c_long, c_long, c_int]),
     "qd_batch_gemv": (c_int, [P, c_long, P, c_float, P, c_long, c_long, c_long, c_long, P, c_long, P, c_long, c_int,
                               c_int, P, ctypes.c_size_t, P]),
     "qd_decode_advance_batch": (c_int, [P, P, P, P, P, c_int, c_int, P]),
@@ -150,6 +151,7 @@ ModelDesc._fields_ = [
     ("attn_splits", c_int), ("step_mode", c_int), ("batch", c_int),
     ("advance_out_tokens", c_void_p), ("advance_counter", c_void_p), ("advance_max_tokens", c_int),
     ("argmax_f16_logits", c_int),
+    ("batch_tiled_weights", c_int),
 ]
 
 __all__ = ["lib", "check", "ptr", "stream", "call", "QD_F16", "QD_F32", "ModelDesc", "LayerDesc", "EXPORTED",

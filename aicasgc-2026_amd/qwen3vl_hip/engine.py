@@ -434,13 +434,17 @@ class BatchDecodeEngine(_CapturedSteps):
     ``fuse_advance`` is False), captured once into a HIP graph.  With
     ``fuse_qkv`` (default) each layer's qkv GEMV runs inside its attention
     launch where the library allows it (``QD_STEP_AUTO``); False keeps two
-    launches.  The reference has no batch decode path (it rejects batch != 1,
-    evaluation_wrapper.py:110-111).
+    launches.  With ``tiled_weights`` (default) the engine keeps copies of every
+    layer's o_proj, gate_up and down in the batch GEMVs' MFMA tile order
+    (``qd_model_desc.batch_tiled_weights``; 84 MB per layer of the 2B model):
+    each wave load is then one contiguous 1 KB that is already the MFMA
+    operand, with the same results bit for bit.  The reference has no batch
+    decode path (it rejects batch != 1, evaluation_wrapper.py:110-111).
     """
 
     def __init__(self, weights: ModelWeights, batch: int, capacity: int, device="cuda", attn_splits: int = 0,
                  keep_logits: bool = False, steps_per_graph: int = 4, fuse_advance: bool = True,
-                 fuse_qkv: bool = True):
+                 fuse_qkv: bool = True, tiled_weights: bool = True):
         if not torch.cuda.is_available():
             raise RuntimeError("BatchDecodeEngine needs a ROCm GPU")
         if steps_per_graph < 1:
@@ -467,10 +471,21 @@ class BatchDecodeEngine(_CapturedSteps):
         self.inv_freq = rope_inv_freq(s).to(dev)
         self.logits = torch.empty(B, s.vocab, dtype=torch.float32, device=dev) if keep_logits else None
         layers = (_lib.LayerDesc * len(self.w.layers))()
+        self.tiled = []   # per layer (o_proj, gate_up, down) in tile order, or empty
+        if tiled_weights:
+            lib = _lib.lib()
+            qs = s.num_heads * s.head_dim
+            r_o = int(lib.qd_batch_tile_rows(s.hidden, qs, 0))
+            r_gu = int(lib.qd_batch_tile_rows(s.intermediate, s.hidden, 1))
+            r_d = int(lib.qd_batch_tile_rows(s.hidden, s.intermediate, 0))
+            self.tiled = [(batch_tile_order(lw.o_proj_weight, r_o), batch_tile_order(lw.gate_up_weight, r_gu),
+                           batch_tile_order(lw.down_proj_weight, r_d)) for lw in self.w.layers]
         for i, lw in enumerate(self.w.layers):
             L = layers[i]
             L.qkv, L.o_proj = lw.qkv_weight.data_ptr(), lw.o_proj_weight.data_ptr()
             L.gate_up, L.down = lw.gate_up_weight.data_ptr(), lw.down_proj_weight.data_ptr()
+            if self.tiled:
+                L.o_proj, L.gate_up, L.down = (x.data_ptr() for x in self.tiled[i])
             L.input_norm, L.post_norm = lw.input_layernorm_weight.data_ptr(), lw.post_attn_layernorm_weight.data_ptr()
             L.q_norm, L.k_norm = lw.q_norm_weight.data_ptr(), lw.k_norm_weight.data_ptr()
             L.k_cache, L.v_cache = self.k_caches[i].data_ptr(), self.v_caches[i].data_ptr()
@@ -495,6 +510,7 @@ class BatchDecodeEngine(_CapturedSteps):
         # device allows it; CHAIN: two launches
         d.step_mode = _lib.STEP_AUTO if fuse_qkv else _lib.STEP_CHAIN
         d.batch = B
+        d.batch_tiled_weights = 1 if self.tiled else 0
         nbytes = _lib.lib().qd_decode_workspace_bytes(ctypes.byref(d))
         self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
         d.workspace = self.workspace.data_ptr()
@@ -577,6 +593,19 @@ class BatchDecodeEngine(_CapturedSteps):
                 self.step_eager()
         torch.cuda.synchronize(self.device)
         return self.out_tokens[:n_steps].tolist()
+
+
+def batch_tile_order(w: torch.Tensor, rows_per_group: int) -> torch.Tensor:
+    """A copy of the row-major fp16 matrix ``w`` [rows, K] in the batch GEMVs'
+    MFMA tile order for row groups of ``rows_per_group`` (qd_batch_tile_rows):
+    16: [rows/16][K/8][16][8]; 8: [rows/8][K/64][4][2][8][8] with element
+    (g, p, c, h, r, e) = w[8 g + r][64 p + 32 h + 8 c + e]."""
+    n, k = w.shape
+    if rows_per_group == 16:
+        return w.reshape(n // 16, 16, k // 8, 8).permute(0, 2, 1, 3).contiguous()
+    if rows_per_group == 8:
+        return w.reshape(n // 8, 8, k // 64, 2, 4, 8).permute(0, 2, 4, 3, 1, 5).contiguous()
+    raise ValueError(f"rows per group {rows_per_group}")
 
 
 def roofline_bytes_batch_step(context_lens, shape: Qwen3VLTextShape = QWEN3VL_2B) -> int:

@@ -318,6 +318,18 @@ typedef struct qd_model_desc {
    * is stated in; the two differ only where the top logits round to one fp16
    * value. */
   int argmax_f16_logits;
+  /* Batch step only: when nonzero, every layer's o_proj, gate_up and down
+   * point to copies of those matrices in MFMA tile order (the reference keeps
+   * row-major weights; this layout is the batch GEMVs' own, no counterpart
+   * there).  With R = qd_batch_tile_rows(rows, K, silu) for the matrix
+   * (o_proj: H x Hq*D, silu 0; gate_up: I x H, silu 1, both halves tiled as
+   * one [2I, H] matrix; down: H x I, silu 0), element W[row][k] sits at
+   *   R = 16: ((row / 16) * (K / 8) + k / 8) * 128 + (row % 16) * 8 + k % 8;
+   *   R = 8:  ((row / 8) * (K / 64) + k / 64) * 512 + ((k % 64) / 8 % 4) * 128
+   *           + ((k % 64) / 32) * 64 + (row % 8) * 8 + k % 8,
+   * so one wave load is one contiguous 1 KB that is already the MFMA operand
+   * (no lane permutation).  Results equal the row-major step's bit for bit. */
+  int batch_tiled_weights;
 } qd_model_desc;
 
 /* How qd_decode_step runs the 28 layers.
@@ -515,6 +527,11 @@ size_t qd_batch_gemv_workspace_bytes(long N, long K);
 int qd_batch_gemv(const float* x, long ldx, const void* gamma, float eps, const void* W, long ldw, long N,
                   long K, long up_offset, const float* residual, long ldr, float* y, long ldy, int nseq,
                   int epilogue, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Rows per row group (8 or 16) of the batch step's GEMV over a rows x K
+ * matrix (silu: the gate_up GEMV, rows = I), which fixes its tile-order
+ * layout (qd_model_desc.batch_tiled_weights); 0 for sizes <= 0. */
+int qd_batch_tile_rows(long rows, long K, int silu);
 
 /* qd_decode_advance for a batch: out_tokens [max_tokens][batch]. */
 int qd_decode_advance_batch(const int64_t* token, int64_t* out_tokens, int64_t* counter,

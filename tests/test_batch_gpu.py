@@ -395,3 +395,34 @@ def test_batch_qkv_hand_off_exhausted_wait_is_reported(cuda, two_layer_weights, 
     again, st = run()
     assert st == 0
     assert torch.equal(again, ref)
+
+
+@pytest.mark.parametrize("fuse", [True, False])
+def test_batch_tile_ordered_weights_equal_row_major(cuda, two_layer_weights, fuse):
+    """o_proj, gate_up and down read from tile-ordered copies (the default)
+    against the row-major weights: the MFMA operands are the same values in
+    the same order, so logits, tokens and written K/V rows are bit-equal
+    (three graph-replayed steps at config-4 lengths; both qkv forms)."""
+    from qwen3vl_hip import synthetic as syn
+    from qwen3vl_hip.engine import BatchDecodeEngine
+
+    w = two_layer_weights
+    positions = [int(v) for v in syn.batch8_kv_lengths()]
+    tokens = [17, 4000, 8191, 2, 555, 1234, 6000, 42]
+    cap = max(positions) + 8
+    res = {}
+    for tiled in (True, False):
+        print(f"case batch tile-ordered weights={tiled} fuse_qkv={fuse}", flush=True)
+        eng = BatchDecodeEngine(w, batch=8, capacity=cap, keep_logits=True, fuse_qkv=fuse, tiled_weights=tiled)
+        assert bool(eng.tiled) == tiled
+        _fill_caches_device(eng, positions, 47)
+        got = eng.decode(tokens, positions, positions, 3, use_graph=True)
+        rows = [eng.k_caches[li][:, :, min(positions):max(positions) + 3].cpu() for li in range(2)]
+        res[tiled] = (got, eng.logits.cpu(), rows, eng.status())
+        del eng
+    (g1, l1, r1, s1), (g0, l0, r0, s0) = res[True], res[False]
+    assert s1 == 0 and s0 == 0
+    assert g1 == g0
+    assert torch.equal(l1, l0)
+    for a, b in zip(r1, r0):
+        assert torch.equal(a, b)

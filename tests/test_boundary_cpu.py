@@ -248,3 +248,29 @@ def test_fusion_flags_follow_the_reference_environment():
     assert out[None] == ["True", "False"]
     assert out["0"] == ["False", "False"]
     assert out["1"] == ["True", "True"]
+
+
+def test_batch_tile_order_layout():
+    """The batch GEMVs' tile order (qd_model_desc.batch_tiled_weights): the
+    library's row-group sizes for the 2B shapes, and the positions the header
+    states for both layouts, checked element by element on small matrices."""
+    import torch
+
+    from qwen3vl_hip import _lib
+    from qwen3vl_hip.engine import batch_tile_order
+
+    lib = _lib.lib()
+    assert lib.qd_batch_tile_rows(2048, 2048, 0) == 8      # o_proj
+    assert lib.qd_batch_tile_rows(6144, 2048, 1) == 8      # gate_up
+    assert lib.qd_batch_tile_rows(2048, 6144, 0) == 16     # down
+    assert lib.qd_batch_tile_rows(0, 2048, 0) == 0
+    rows, K = 32, 256
+    w = torch.arange(rows * K, dtype=torch.float32).reshape(rows, K)
+    t16 = batch_tile_order(w, 16).reshape(-1)
+    t8 = batch_tile_order(w, 8).reshape(-1)
+    for r in range(rows):
+        for k in range(K):
+            o16 = ((r // 16) * (K // 8) + k // 8) * 128 + (r % 16) * 8 + k % 8
+            o8 = ((r // 8) * (K // 64) + k // 64) * 512 + ((k % 64) // 8 % 4) * 128 + ((k % 64) // 32) * 64 \
+                + (r % 8) * 8 + k % 8
+            assert t16[o16] == w[r, k] and t8[o8] == w[r, k]
