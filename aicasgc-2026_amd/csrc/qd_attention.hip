@@ -200,6 +200,7 @@ struct Qkv8In {
   float ss[2][4];
 };
 
+template <bool TILED>
 __device__ __forceinline__ void qkv8_load(const AttnArgs& a, int p, int w, int lane, Qkv8In& in) {
   const long kb = (long)w * kQkvKS;
   const u32x4* src = reinterpret_cast<const u32x4*>(a.xb) + (kb / 32) * 64 + lane;
@@ -214,6 +215,13 @@ __device__ __forceinline__ void qkv8_load(const AttnArgs& a, int p, int w, int l
       in.ss[q][i] = part < a.in_parts ? a.in_ss[(long)part * kBatchMax + seq] : 0.f;
     }
   }
+  if constexpr (TILED) {
+    // tile order: tile t of the slice is one contiguous 1 KB, already the MFMA operand
+    const uint16_t* tp = a.wqkv + ((long)p * (kQkvK / 8) + kb / 8) * 128 + lane * 8;
+#pragma unroll
+    for (int i = 0; i < kQkvNT; ++i) in.wt[i] = ld_stream(tp + 512L * i);
+    return;
+  }
   const uint16_t* wp = a.wqkv + ((long)p * 16 + (lane >> 3)) * kQkvK + kb + (lane & 7) * 8;
 #pragma unroll
   for (int j = 0; j < kQkvNT / 2; ++j) {
@@ -226,6 +234,7 @@ __device__ __forceinline__ void qkv8_load(const AttnArgs& a, int p, int w, int l
 // row r of sequence n), the 4 slices summed through LDS, scaled by
 // rstd / in_scale of the sequence and stored as tagged words.  Every thread of
 // the workgroup calls it (it contains workgroup barriers).
+template <bool TILED>
 __device__ __forceinline__ void qkv8_produce(const AttnArgs& a, int p, int w, int lane, const Qkv8In& in,
                                              unsigned par, float (&s_part)[kQkvWaves][kBatchMax][16],
                                              float (&s_fac)[kBatchMax]) {
@@ -236,9 +245,13 @@ __device__ __forceinline__ void qkv8_produce(const AttnArgs& a, int p, int w, in
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int j = 0; j < kQkvNT / 2; ++j) {
-    const u32x4 a0 = bperm4(src0, in.wt[2 * j]), a1 = bperm4(src1, in.wt[2 * j]);
-    const u32x4 b0 = bperm4(src0, in.wt[2 * j + 1]), b1 = bperm4(src1, in.wt[2 * j + 1]);
-    const u32x4 t0 = upper ? b0 : a0, t1 = upper ? b1 : a1;
+    u32x4 t0 = in.wt[2 * j], t1 = in.wt[2 * j + 1];
+    if constexpr (!TILED) {
+      const u32x4 a0 = bperm4(src0, in.wt[2 * j]), a1 = bperm4(src1, in.wt[2 * j]);
+      const u32x4 b0 = bperm4(src0, in.wt[2 * j + 1]), b1 = bperm4(src1, in.wt[2 * j + 1]);
+      t0 = upper ? b0 : a0;
+      t1 = upper ? b1 : a1;
+    }
     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8v, t0), __builtin_bit_cast(h8v, in.bt[2 * j]),
                                                  acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8v, t1),
@@ -280,7 +293,7 @@ __device__ __forceinline__ void qkv8_produce(const AttnArgs& a, int p, int w, in
   stores_done();   // polling with a store of the wave still in flight is much slower
 }
 
-template <int G, typename TQ, bool FUSED_ROPE, bool XQKV = false>
+template <int G, typename TQ, bool FUSED_ROPE, bool XQKV = false, bool WT = false>
 __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
   static_assert(!XQKV || (G == 2 && FUSED_ROPE), "the qkv hand-off serves the fused batch prologue");
   // XQKV: one-dimensional grid in dispatch order, sequence-major
@@ -311,7 +324,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
   if constexpr (XQKV) {
     gen = __hip_atomic_load(a.hgen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     par = (gen + 1u) & 1u;
-    if (producer) qkv8_load(a, (int)blockIdx.x, (int)(threadIdx.x / kWave), lane_id(), qin);
+    if (producer) qkv8_load<WT>(a, (int)blockIdx.x, (int)(threadIdx.x / kWave), lane_id(), qin);
   }
 
   const long pos = a.cache_position[bq];
@@ -395,7 +408,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
   if constexpr (XQKV) {
     __shared__ float s_part[kQkvWaves][kBatchMax][16];
     __shared__ float s_fac[kBatchMax];
-    if (producer) qkv8_produce(a, (int)blockIdx.x, w, j, qin, par, s_part, s_fac);
+    if (producer) qkv8_produce<WT>(a, (int)blockIdx.x, w, j, qin, par, s_part, s_fac);
     // this sequence's raw q (G heads), k and v of kv head kvh, as the words show them
     unsigned left = a.spin_limit != 0u ? a.spin_limit : kQkvSpinLimit;
     const unsigned* words = a.qkv_t + (long)bq * kQkv8Producers * 16;
@@ -670,10 +683,15 @@ bool attention_qkv8_device_ok() {
   if ((int)ok.size() <= dev) ok.resize(dev + 1, -1);
   if (ok[dev] < 0) {
     int cus = 0, per_cu = 0;
+    int per_cu_t = 0;
     const bool q = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
                    hipOccupancyMaxActiveBlocksPerMultiprocessor(
                        &per_cu, reinterpret_cast<const void*>(&attn_partial_kernel<2, float, true, true>), 256, 0) ==
-                       hipSuccess;
+                       hipSuccess &&
+                   hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                       &per_cu_t, reinterpret_cast<const void*>(&attn_partial_kernel<2, float, true, true, true>), 256,
+                       0) == hipSuccess;
+    if (per_cu_t < per_cu) per_cu = per_cu_t;
     ok[dev] = (q && (long)cus * per_cu >= kQkv8Producers) ? 1 : 0;
     (void)hipGetLastError();
   }
@@ -687,7 +705,10 @@ int attention_qkv8_launch(const AttnArgs& a, hipStream_t s) {
       a.wqkv == nullptr || a.xb == nullptr || a.in_ss == nullptr || a.in_parts < 1 || a.in_parts > 4 * kWave ||
       a.qkv_t == nullptr || a.hgen == nullptr || a.hdone == nullptr || a.status == nullptr)
     return QD_ERR_SHAPE;
-  hipLaunchKernelGGL((attn_partial_kernel<2, float, true, true>), dim3((unsigned)grid), dim3(256), 0, s, a);
+  if (a.wqkv_tiled)
+    hipLaunchKernelGGL((attn_partial_kernel<2, float, true, true, true>), dim3((unsigned)grid), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((attn_partial_kernel<2, float, true, true>), dim3((unsigned)grid), dim3(256), 0, s, a);
   return qd_host::launch_status("attn_partial_kernel<qkv>");
 }
 

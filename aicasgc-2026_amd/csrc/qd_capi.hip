@@ -870,7 +870,8 @@ int batch_step(const qd_model_desc* d, hipStream_t s) {
   // every row group of the layout the GEMV's row group size implies
   const int gu_tiled = d->batch_tiled_weights ? 1 : 0;
   if (gu_tiled) {
-    const struct { long rows, K; bool silu; } m[3] = {{H, (long)Hq * D, false}, {I, H, true}, {H, I, false}};
+    const struct { long rows, K; bool silu; } m[4] = {
+        {qkv_rows, H, false}, {H, (long)Hq * D, false}, {I, H, true}, {H, I, false}};
     for (const auto& x : m) {
       const int rg = batch_split(x.rows, x.K, x.silu).rows_per_group;
       QD_REQUIRE(x.rows % rg == 0 && x.K % (rg == 8 ? 64 : 32) == 0, QD_ERR_SHAPE,
@@ -884,7 +885,7 @@ int batch_step(const qd_model_desc* d, hipStream_t s) {
     qd::Gemv8Args g;
     base(g, qkv_rows, H);
     g.xb = b.xb; g.in_ss = b.ss_x; g.in_parts = xparts; g.in_scale = b.sc_x; g.W = (const u16*)w.qkv;
-    g.y = b.qkv; g.ldy = qkv_rows;
+    g.y = b.qkv; g.ldy = qkv_rows; g.w_tiled = gu_tiled;
     if (!fuse_qkv && (st = qd::gemv8_launch(g, qd::EPI_STORE, s))) return st;
     qd::AttnArgs aa;
     aa.k = (const u16*)w.k_cache; aa.v = (const u16*)w.v_cache; aa.k_w = (u16*)w.k_cache; aa.v_w = (u16*)w.v_cache;
@@ -898,7 +899,8 @@ int batch_step(const qd_model_desc* d, hipStream_t s) {
     attn_ws(b.attn_ws, aa);
     aa.lse = aa.o_part + (size_t)B * Hq * splits * 128;
     if (fuse_qkv) {
-      aa.wqkv = (const u16*)w.qkv; aa.xb = b.xb; aa.in_ss = b.ss_x; aa.in_parts = xparts; aa.in_scale = b.sc_x;
+      aa.wqkv = (const u16*)w.qkv; aa.wqkv_tiled = gu_tiled; aa.xb = b.xb; aa.in_ss = b.ss_x; aa.in_parts = xparts;
+      aa.in_scale = b.sc_x;
       aa.qkv_t = b.qkv_t; aa.hgen = b.qkv_ctl; aa.hdone = b.qkv_ctl + 1; aa.status = b.control;
       aa.spin_limit = g_spin_limit.load();
       if ((st = qd::attention_qkv8_launch(aa, s))) return st;

@@ -100,7 +100,8 @@ struct AttnArgs {
   // qkv[b] = rstd_b / in_scale[b] * (W_qkv . image(x)[b]) each and hand them
   // to every workgroup through parity-tagged words in the uncached hand-off
   // area (qkv_t [kBatchMax][rows]); `qkv` is then unused
-  const uint16_t* wqkv = nullptr;     // fp16 [rows][2048]
+  const uint16_t* wqkv = nullptr;     // fp16 [rows][2048], or in tile order (wqkv_tiled)
+  int wqkv_tiled = 0;                 // wqkv in the batch GEMVs' tile order for 16-row groups
   const uint16_t* xb = nullptr;       // operand image of x [2048/32][64][8]
   const float* in_ss = nullptr;       // [in_parts][8] partial sums of squares of x
   int in_parts = 0;

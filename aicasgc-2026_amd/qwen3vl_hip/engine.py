@@ -435,8 +435,8 @@ class BatchDecodeEngine(_CapturedSteps):
     ``fuse_qkv`` (default) each layer's qkv GEMV runs inside its attention
     launch where the library allows it (``QD_STEP_AUTO``); False keeps two
     launches.  With ``tiled_weights`` (default) the engine keeps copies of every
-    layer's o_proj, gate_up and down in the batch GEMVs' MFMA tile order
-    (``qd_model_desc.batch_tiled_weights``; 84 MB per layer of the 2B model):
+    layer's qkv, o_proj, gate_up and down in the batch GEMVs' MFMA tile order
+    (``qd_model_desc.batch_tiled_weights``; 101 MB per layer of the 2B model):
     each wave load is then one contiguous 1 KB that is already the MFMA
     operand, with the same results bit for bit.  The reference has no batch
     decode path (it rejects batch != 1, evaluation_wrapper.py:110-111).
@@ -471,21 +471,23 @@ class BatchDecodeEngine(_CapturedSteps):
         self.inv_freq = rope_inv_freq(s).to(dev)
         self.logits = torch.empty(B, s.vocab, dtype=torch.float32, device=dev) if keep_logits else None
         layers = (_lib.LayerDesc * len(self.w.layers))()
-        self.tiled = []   # per layer (o_proj, gate_up, down) in tile order, or empty
+        self.tiled = []   # per layer (qkv, o_proj, gate_up, down) in tile order, or empty
         if tiled_weights:
             lib = _lib.lib()
             qs = s.num_heads * s.head_dim
+            r_q = int(lib.qd_batch_tile_rows(qs + 2 * s.num_kv_heads * s.head_dim, s.hidden, 0))
             r_o = int(lib.qd_batch_tile_rows(s.hidden, qs, 0))
             r_gu = int(lib.qd_batch_tile_rows(s.intermediate, s.hidden, 1))
             r_d = int(lib.qd_batch_tile_rows(s.hidden, s.intermediate, 0))
-            self.tiled = [(batch_tile_order(lw.o_proj_weight, r_o), batch_tile_order(lw.gate_up_weight, r_gu),
-                           batch_tile_order(lw.down_proj_weight, r_d)) for lw in self.w.layers]
+            self.tiled = [(batch_tile_order(lw.qkv_weight, r_q), batch_tile_order(lw.o_proj_weight, r_o),
+                           batch_tile_order(lw.gate_up_weight, r_gu), batch_tile_order(lw.down_proj_weight, r_d))
+                          for lw in self.w.layers]
         for i, lw in enumerate(self.w.layers):
             L = layers[i]
             L.qkv, L.o_proj = lw.qkv_weight.data_ptr(), lw.o_proj_weight.data_ptr()
             L.gate_up, L.down = lw.gate_up_weight.data_ptr(), lw.down_proj_weight.data_ptr()
             if self.tiled:
-                L.o_proj, L.gate_up, L.down = (x.data_ptr() for x in self.tiled[i])
+                L.qkv, L.o_proj, L.gate_up, L.down = (x.data_ptr() for x in self.tiled[i])
             L.input_norm, L.post_norm = lw.input_layernorm_weight.data_ptr(), lw.post_attn_layernorm_weight.data_ptr()
             L.q_norm, L.k_norm = lw.q_norm_weight.data_ptr(), lw.k_norm_weight.data_ptr()
             L.k_cache, L.v_cache = self.k_caches[i].data_ptr(), self.v_caches[i].data_ptr()

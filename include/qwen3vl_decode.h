@@ -318,12 +318,13 @@ typedef struct qd_model_desc {
    * is stated in; the two differ only where the top logits round to one fp16
    * value. */
   int argmax_f16_logits;
-  /* Batch step only: when nonzero, every layer's o_proj, gate_up and down
-   * point to copies of those matrices in MFMA tile order (the reference keeps
-   * row-major weights; this layout is the batch GEMVs' own, no counterpart
-   * there).  With R = qd_batch_tile_rows(rows, K, silu) for the matrix
-   * (o_proj: H x Hq*D, silu 0; gate_up: I x H, silu 1, both halves tiled as
-   * one [2I, H] matrix; down: H x I, silu 0), element W[row][k] sits at
+  /* Batch step only: when nonzero, every layer's qkv, o_proj, gate_up and
+   * down point to copies of those matrices in MFMA tile order (the reference
+   * keeps row-major weights; this layout is the batch GEMVs' own, no
+   * counterpart there).  With R = qd_batch_tile_rows(rows, K, silu) for the
+   * matrix (qkv: (Hq + 2 Hkv) D x H, silu 0; o_proj: H x Hq*D, silu 0;
+   * gate_up: I x H, silu 1, both halves tiled as one [2I, H] matrix; down:
+   * H x I, silu 0), element W[row][k] sits at
    *   R = 16: ((row / 16) * (K / 8) + k / 8) * 128 + (row % 16) * 8 + k % 8;
    *   R = 8:  ((row / 8) * (K / 64) + k / 64) * 512 + ((k % 64) / 8 % 4) * 128
    *           + ((k % 64) / 32) * 64 + (row % 8) * 8 + k % 8,

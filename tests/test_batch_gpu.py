@@ -399,7 +399,7 @@ def test_batch_qkv_hand_off_exhausted_wait_is_reported(cuda, two_layer_weights, 
 
 @pytest.mark.parametrize("fuse", [True, False])
 def test_batch_tile_ordered_weights_equal_row_major(cuda, two_layer_weights, fuse):
-    """o_proj, gate_up and down read from tile-ordered copies (the default)
+    """qkv, o_proj, gate_up and down read from tile-ordered copies (the default)
     against the row-major weights: the MFMA operands are the same values in
     the same order, so logits, tokens and written K/V rows are bit-equal
     (three graph-replayed steps at config-4 lengths; both qkv forms)."""

@@ -260,6 +260,7 @@ def test_batch_tile_order_layout():
     from qwen3vl_hip.engine import batch_tile_order
 
     lib = _lib.lib()
+    assert lib.qd_batch_tile_rows(4096, 2048, 0) == 16     # qkv
     assert lib.qd_batch_tile_rows(2048, 2048, 0) == 8      # o_proj
     assert lib.qd_batch_tile_rows(6144, 2048, 1) == 8      # gate_up
     assert lib.qd_batch_tile_rows(2048, 6144, 0) == 16     # down
